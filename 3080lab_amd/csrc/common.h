@@ -1,0 +1,93 @@
+// Shared device helpers for the gfx950 (CDNA4) Qwen2.5 Q4_0 hot path.
+//
+// Device formats (one layout for every kernel of the library):
+//   Q4_0 matrix W [N, K] (N % 16 == 0, K % 32 == 0), "16-row tiled planes":
+//     qs  uint8 [N/16][K/32][16 rows][16 B]   the GGUF qs bytes of each block, unchanged: byte i holds
+//                                             weight i (low nibble) and weight i+16 (high nibble), stored 0..15
+//     d   fp16  [N/16][K/32][16 rows]         the GGUF block scale; value = d * (q - 8)
+//   For a fixed (tile, block) the 16 rows' nibbles are 256 contiguous bytes, so one wave64 load of
+//   16 B per lane (16 rows x 4 consecutive blocks) reads 1 KB contiguous, and the same bytes form the
+//   A operand of v_mfma_i32_16x16x32_i8 (lane = row, 8 bytes per k-group).
+//   Q8_1 activations X [T, K]:
+//     xq  int8  [T][K]
+//     xds half2 [T][K/32] = (d, s): d = fp16(amax/127), s = fp16(d * sum q) (llama.cpp block_q8_1 fields)
+//   Kernels use the exact integer block correction dot - 8 * sum(q) (sum recomputed from xq), not s.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <stdint.h>
+
+#define Q355_QK 32
+#define Q355_WAVE 64
+
+namespace q355 {
+
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+
+// 16-byte streaming load (nontemporal hint: weights are read once per step).
+__device__ __forceinline__ uint4 ld_stream16(const void* p) {
+  u32x4 v = __builtin_nontemporal_load((const u32x4*)p);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+__device__ __forceinline__ int dot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
+
+// Exact int32 dot of one Q4_0 block (16 B of GGUF qs, unsigned nibbles 0..15) with 32 int8 values.
+__device__ __forceinline__ int q4_block_dot(const uint4 w, const int* x) {
+  int acc = 0;
+  acc = dot4((int)(w.x & 0x0F0F0F0Fu), x[0], acc);
+  acc = dot4((int)(w.y & 0x0F0F0F0Fu), x[1], acc);
+  acc = dot4((int)(w.z & 0x0F0F0F0Fu), x[2], acc);
+  acc = dot4((int)(w.w & 0x0F0F0F0Fu), x[3], acc);
+  acc = dot4((int)((w.x >> 4) & 0x0F0F0F0Fu), x[4], acc);
+  acc = dot4((int)((w.y >> 4) & 0x0F0F0F0Fu), x[5], acc);
+  acc = dot4((int)((w.z >> 4) & 0x0F0F0F0Fu), x[6], acc);
+  acc = dot4((int)((w.w >> 4) & 0x0F0F0F0Fu), x[7], acc);
+  return acc;
+}
+
+__device__ __forceinline__ int sum_i8x32(const int* x) {
+  int s = 0;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) s = dot4(x[i], 0x01010101, s);
+  return s;
+}
+
+// Wave64 reductions (xor butterfly over all 64 lanes, or over `width` lanes).
+template <int WIDTH = 64>
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = WIDTH / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+template <int WIDTH = 64>
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = WIDTH / 2; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+template <int WIDTH = 64>
+__device__ __forceinline__ int wave_isum(int v) {
+#pragma unroll
+  for (int o = WIDTH / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+// Q8_1 of one value inside a group of 32 lanes that hold one block (lane group aligned to 32).
+// Returns q; writes (d, s) through `ds` from the group's first lane. Bit-exact with the oracle:
+// d = fp16(amax / 127) (IEEE fp32 divide), q = roundf(x / d16) clamped to +-127, q = 0 when d16 == 0.
+__device__ __forceinline__ int q8_1_lane32(float x, half2* ds, bool leader) {
+  float amax = wave_max<32>(fabsf(x));
+  __half d16 = __float2half_rn(amax / 127.0f);
+  float df = __half2float(d16);
+  int q = 0;
+  if (df != 0.0f) {
+    q = (int)roundf(x / df);
+    q = q > 127 ? 127 : (q < -127 ? -127 : q);
+  }
+  int sq = wave_isum<32>(q);
+  if (leader) *ds = __halves2half2(d16, __float2half_rn(df * (float)sq));
+  return q;
+}
+
+}  // namespace q355

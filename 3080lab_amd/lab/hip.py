@@ -1,0 +1,112 @@
+"""ctypes binding of libqwen355.so (the gfx950 C ABI declared in include/qwen355.h).
+
+Replaces the reference's NVRTC/cuda-python launch layer (lab/toolchain.py:107-110 build,
+scripts/qwen_fused.py:30-42 Kern: cuModuleLoadData + cuLaunchKernel with ctypes argument arrays).
+Kernels are compiled ahead of time by hipcc (3080lab_amd/build.py); every entry point enqueues on an
+explicit stream (torch's current stream by default, so torch.cuda.CUDAGraph capture records them).
+
+There is no CPU fallback: if the library is missing or fails to load, `lib()` raises.
+"""
+from __future__ import annotations
+
+import ctypes
+from ctypes import POINTER, c_char_p, c_float, c_int, c_uint32, c_void_p
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parents[1] / "lib" / "libqwen355.so"
+
+_P = c_void_p
+# name -> argtypes (all return int status)
+_SIGS = {
+    "q355_quant_q8_1": [_P, _P, _P, c_int, c_int, _P],
+    "q355_rmsnorm_q8_1": [_P, _P, _P, _P, c_int, c_int, c_float, _P],
+    "q355_gemv_q4_0_q8_1": [_P, _P, c_int, c_int, _P, _P, c_int, _P, _P, c_int, c_int, _P],
+    "q355_gemv_blockdots": [_P, c_int, c_int, _P, c_int, _P, _P],
+    "q355_qkv_rope_kv": [_P, _P, c_int, _P, _P, c_float, _P, _P, _P, _P, _P, c_int, c_int, _P, _P, _P,
+                         c_int, c_int, c_int, _P],
+    "q355_ffn_gate_up": [_P, _P, c_int, c_int, _P, _P, c_float, _P, _P, c_int, _P],
+    "q355_head_logits": [_P, _P, c_int, c_int, _P, _P, c_float, _P, _P, _P, c_int, _P],
+    "q355_head_nparts": [c_int],
+    "q355_finish": [_P, _P, c_int, _P, _P, c_int, _P],
+    "q355_embed_q4_0": [_P, _P, c_int, c_int, _P, _P, c_int, _P],
+    "q355_attn_decode": [_P, _P, _P, _P, _P, c_int, c_int, c_int, c_int, c_float, _P, _P, _P, _P, _P, c_int, _P],
+}
+# entry points returning something other than an int status
+_VALUE_FUNCS = {"q355_head_nparts"}
+
+_lib = None
+
+
+class HipError(RuntimeError):
+    pass
+
+
+def lib():
+    """Load libqwen355.so once; raise HipError if it is not built (no fallback path exists)."""
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise HipError(f"{LIB_PATH} is not built: run `python 3080lab_amd/build.py` (hipcc, gfx950)")
+        L = ctypes.CDLL(str(LIB_PATH))
+        L.q355_last_error.restype = c_char_p
+        L.q355_last_error.argtypes = []
+        L.q355_version.restype = c_char_p
+        L.q355_version.argtypes = []
+        for name, args in _SIGS.items():
+            f = getattr(L, name)
+            f.argtypes = args
+            f.restype = c_int
+        _lib = L
+    return _lib
+
+
+def exported_symbols():
+    return ["q355_last_error", "q355_version", *_SIGS]
+
+
+def current_stream() -> int:
+    import torch
+    return torch.cuda.current_stream().cuda_stream
+
+
+def ptr(t) -> int | None:
+    """Device pointer of a torch tensor (None passes NULL)."""
+    if t is None:
+        return None
+    return t.data_ptr()
+
+
+def call(name: str, *args):
+    """Call entry point `name`; the trailing stream argument is added (torch's current stream).
+    Raises HipError with the library's message on a non-zero status."""
+    L = lib()
+    f = getattr(L, name)
+    if name in _VALUE_FUNCS:
+        return f(*args)
+    rc = f(*args, current_stream())
+    if rc != 0:
+        raise HipError(f"{name}: status {rc}: {L.q355_last_error().decode()}")
+    return rc
+
+
+class Kern:
+    """Reference-compatible launcher (scripts/qwen_fused.py:30-42): Kern(spec).launch(grid, block, args).
+    `spec` is a KernelSpec from lab.qwen_kernels / lab.qwen_batched naming a C-ABI entry point; the
+    launch geometry is chosen by the library for gfx950, so grid/block are accepted for signature
+    compatibility and ignored. `args` are the entry point's arguments in declaration order (device
+    pointers as ints or tensors, scalars as Python numbers or ctypes values)."""
+
+    def __init__(self, spec):
+        self.spec = spec
+        lib()
+
+    def launch(self, grid=None, block=None, args=()):
+        conv = []
+        for a in args:
+            if hasattr(a, "data_ptr"):
+                conv.append(a.data_ptr())
+            elif isinstance(a, (ctypes.c_uint64, ctypes.c_int32, ctypes.c_float)):
+                conv.append(a.value)
+            else:
+                conv.append(a)
+        return call(self.spec.symbol, *conv)

@@ -1,0 +1,103 @@
+/* qwen355.h -- C ABI of libqwen355.so, the gfx950 (MI355X) Qwen2.5 Q4_0 inference hot path.
+ *
+ * Every entry point takes plain device pointers, sizes and a hipStream_t (passed as void*; NULL =
+ * the default stream), enqueues its kernels on that stream, allocates nothing and returns 0 on
+ * success, Q355_EINVAL for a shape/argument error (checked on the host before any launch), or the
+ * hipError_t of a failed launch. q355_last_error() describes the last failure of the calling thread.
+ * Entry points can be captured into a hipGraph (no host synchronisation, no allocation, scratch
+ * counters reset themselves).
+ *
+ * Formats (see 3080lab_amd/csrc/common.h):
+ *   Q4_0 matrix [N, K]: qs uint8 [N/16][K/32][16][16] (GGUF qs bytes per block), d fp16 [N/16][K/32][16].
+ *   Q8_1 activations [T, K]: xq int8 [T][K], xds half2 [T][K/32] = (d, s = d * sum q).
+ *   KV cache (per layer): fp16 [n_pages][nkv][64][128]; block_table int32 [n_seq][bt_stride] page ids.
+ *   RoPE tables: fp32 [maxlen][64] (cos, sin). Token positions and ids are int32.
+ *
+ * Each declaration names the reference interface it replaces (paths relative to the reference
+ * repository lblommesteyn/3080lab).
+ */
+#ifndef QWEN355_H
+#define QWEN355_H
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define Q355_OK 0
+#define Q355_EINVAL 1
+
+/* Replaces check()/RuntimeError reporting (scripts/qwen_e2e.py:38-41, lab/gpu.py:11-21). */
+const char* q355_last_error(void);
+
+/* Library version string, for the loader's sanity check (no reference counterpart needed by callers
+ * beyond lab/toolchain.py:107-110's "build returned a module"). */
+const char* q355_version(void);
+
+/* Q8_1 activation quantizer: x fp32 [T][K] -> xq, xds.
+ * Replaces QUANT_Q8 (lab/qwen_batched.py:1016-1041). K % 32 == 0. */
+int q355_quant_q8_1(const float* x, int8_t* xq, void* xds, int T, int K, void* stream);
+
+/* Fused RMSNorm + Q8_1: x = Q8_1(h * rsqrt(mean(h^2) + eps) * w) per token.
+ * Replaces rmsnorm_q8_source (lab/qwen_batched.py:1044-1091) and RMSNORM_F32W_1P
+ * (lab/qwen_kernels.py:683-705). H % 32 == 0, H <= 2048. */
+int q355_rmsnorm_q8_1(const float* h, const float* w, int8_t* xq, void* xds, int T, int H, float eps,
+                      void* stream);
+
+/* Q4_0 x Q8_1 GEMV for T = 1..4 tokens: y[T][N] (epi 0: =, 1: +=, 2: = acc + bias[N]).
+ * split > 1 (epi 1 only) splits K over `split` workgroups that add with fp32 atomics (order not fixed).
+ * Replaces gemv_source epilogues store / bias / biasf / resid / logits (lab/qwen_kernels.py:14-113).
+ * N % 16 == 0, K % 32 == 0, K <= 8960. */
+int q355_gemv_q4_0_q8_1(const uint8_t* qs, const void* d, int N, int K, const int8_t* xq, const void* xds,
+                        int T, float* y, const float* bias, int epi, int split, void* stream);
+
+/* Debug: every per-block int32 dot out[T][N][K/32] = sum_i q_w,i (0..15) * q_x,i (bit-exact check).
+ * Replaces the per-block timing/debug arguments of gemv_source (lab/qwen_kernels.py:46-53). */
+int q355_gemv_blockdots(const uint8_t* qs, int N, int K, const int8_t* xq, int T, int32_t* out, void* stream);
+
+/* Fused ln1 RMSNorm + Q8_1 + QKV GEMV + bias + RoPE(q, k) + fp16 K/V cache write + fp16 q out.
+ * Rows of q and k heads are stored interleaved (d, d + 64) and the bias in the same order.
+ * Replaces RMSNORM_F32W_1P + gemv_source('biasf') + the RoPE/KV-write head of ATTN4
+ * (lab/qwen_kernels.py:33, 517-546) and gemm 'biasf_kv' (lab/qwen_batched.py:1316-1362).
+ * Token j (j < T <= 4) is at position pos[j] of sequence j * seq_stride. */
+int q355_qkv_rope_kv(const uint8_t* qs, const void* d, int K, const float* h, const float* nw, float eps,
+                     const float* bias, const float* rope_cos, const float* rope_sin, const int32_t* pos,
+                     const int32_t* block_table, int bt_stride, int seq_stride, void* kcache, void* vcache,
+                     void* qout, int nh, int nkv, int T, void* stream);
+
+/* Fused ln2 RMSNorm + Q8_1 + gate_up GEMV (rows interleaved gate, up) + SwiGLU + Q8_1 of the result.
+ * N2 = 2 * FFN rows; output mq int8 [T][N2/2], mds half2 [T][N2/64].
+ * Replaces gemv_source('swiglu') (lab/qwen_kernels.py:21-28) and 'swiglu_q8' (lab/qwen_batched.py:1363-1396). */
+int q355_ffn_gate_up(const uint8_t* qs, const void* d, int N2, int K, const float* h, const float* nw, float eps,
+                     int8_t* mq, void* mds, int T, void* stream);
+
+/* Final RMSNorm + Q8_1 + tied Q4_0 head: logits fp32 [T][V] and per-workgroup (max, lowest index)
+ * partials pmax/pidx [T][q355_head_nparts(V)]. Replaces gemv_q6_source / 'logits'
+ * (lab/qwen_kernels.py:608-678, 36) and the first stage of FINISH_MB (250-270). */
+int q355_head_logits(const uint8_t* qs, const void* d, int V, int K, const float* h, const float* nw, float eps,
+                     float* logits, float* pmax, int32_t* pidx, int T, void* stream);
+int q355_head_nparts(int V);
+
+/* Greedy finish: tok[j] = argmax (lowest index on ties) over the head partials, pos[j] += 1.
+ * Replaces FINISH / FINISH_MB (lab/qwen_kernels.py:222-282). */
+int q355_finish(const float* pmax, const int32_t* pidx, int nparts, int32_t* tok, int32_t* pos, int T,
+                void* stream);
+
+/* Embedding lookup from the tied Q4_0 table: h[j] = dequant(E[tok[j]]).
+ * Replaces EMBED_F32 (lab/qwen_kernels.py:284-290). */
+int q355_embed_q4_0(const uint8_t* qs, const void* d, int V, int H, const int32_t* tok, float* h, int T,
+                    void* stream);
+
+/* Decode GQA attention, split-K over 64-position pages: token j attends to positions 0..pos[j] of its
+ * sequence (block_table row j). Output: Q8_1 oq/ods [T][nh*128] for the O projection and optionally
+ * fp32 o32 (may be NULL). Scratch: part fp32 [T][nh][max_chunks][130], counter uint32 [T][nkv]
+ * (zero before the first call; the kernel leaves it zero). max_chunks >= (max pos)/64 + 1.
+ * Replaces ATTN2 / ATTN4 (lab/qwen_kernels.py:358-442, 517-605). */
+int q355_attn_decode(const void* q, const void* kcache, const void* vcache, const int32_t* pos,
+                     const int32_t* block_table, int bt_stride, int nh, int nkv, int max_chunks, float scale,
+                     float* part, uint32_t* counter, int8_t* oq, void* ods, float* o32, int T, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* QWEN355_H */

@@ -1,0 +1,120 @@
+"""Oracle: Q4_0 / Q8_1 formats and the Q4_0 x Q8_1 GEMV (numpy). TEST INFRASTRUCTURE ONLY.
+
+Restates:
+  * the GGUF Q4_0 block (lab/gguf.py:3-5, 88-94): 18 B = fp16 d + 16 B qs; weight i is
+    (qs[i] & 15) - 8 and weight i+16 is (qs[i] >> 4) - 8, value = d * weight;
+  * the Q4_0 quantizer of BASELINE config 0 (llama.cpp quantize_row_q4_0_ref semantics, not in
+    the reference tree): m = the signed value of max |x| (first on ties), d = m / -8 in fp32,
+    stored fp16, q = clamp(round(x / d) + 8, 0, 15) with round = half away from zero, q = 8 when d = 0;
+  * the Q8_1 activation quantizer (the reference's int8 quantizer QUANT_Q8,
+    lab/qwen_batched.py:1016-1041, with fp16 d as llama.cpp block_q8_1): d = amax / 127 in fp32,
+    stored fp16; q = round(x / d16) half away from zero, clamped to [-127, 127], 0 when d16 = 0;
+    s = fp16(d16 * sum(q)) (llama.cpp's block sum field);
+  * the per-block int32 dot and the Q4_0 offset correction of the reference's int8 MMQ
+    (lab/qwen_batched.py:1099-1101, 1237-1243): per 32-block b,
+    dot_b = sum_i q_w,i (0..15) * q_x,i (exact int32), y += d_w * d_x * (dot_b - 8 * sum_i q_x,i).
+"""
+from __future__ import annotations
+
+import numpy as np
+
+QK = 32                 # weights per Q4_0 / Q8_1 block
+Q4_0_BYTES = 18         # fp16 d + 16 B nibbles
+
+
+def round_half_away(v: np.ndarray) -> np.ndarray:
+    """C roundf(): nearest integer, halves away from zero. Evaluated in float64 so that
+    v + 0.5 is exact for every float32 v of magnitude < 2^24 (no double rounding).
+    pinned by: tests/test_oracle_quant.py::test_round_half_away (hand cases incl. 0.49999997, 2.5, -2.5)."""
+    v64 = np.asarray(v, dtype=np.float64)
+    return np.trunc(v64 + np.copysign(0.5, v64))
+
+
+def quantize_q4_0(x: np.ndarray) -> np.ndarray:
+    """fp32 [..., K] (K % 32 == 0) -> GGUF Q4_0 bytes uint8 [n_blocks, 18] in row-major block order.
+    pinned by: hand-computed known-answer block, invariants (extreme element -> q = 0 exactly, |x - deq| <= |d|/2
+    away from the clamp), round trip through the independent decoder q4_0_blocks()."""
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1, QK)
+    idx = np.argmax(np.abs(x), axis=1)                      # first maximum, as llama.cpp's strict '<' scan
+    m = x[np.arange(x.shape[0]), idx]
+    d = (m / np.float32(-8.0)).astype(np.float32)
+    with np.errstate(divide="ignore", invalid="ignore"):
+        r = np.where(d[:, None] != 0, x / d[:, None], np.float32(0.0)).astype(np.float32)
+    q = np.clip(round_half_away(r) + 8, 0, 15).astype(np.uint8)
+    out = np.empty((x.shape[0], Q4_0_BYTES), np.uint8)
+    out[:, :2] = d.astype(np.float16).reshape(-1, 1).view(np.uint8)
+    out[:, 2:] = q[:, :16] | (q[:, 16:] << 4)
+    return out
+
+
+def q4_0_blocks(b: np.ndarray):
+    """GGUF Q4_0 bytes -> (d float32 [nblk], q uint8 [nblk, 32] stored 0..15) exactly as lab/gguf.py:88-94.
+    pinned by: hand-written bytes with known nibbles (tests/test_oracle_quant.py)."""
+    blk = np.asarray(b, np.uint8).reshape(-1, Q4_0_BYTES)
+    d = blk[:, :2].copy().view(np.float16).astype(np.float32).reshape(-1)
+    qs = blk[:, 2:]
+    q = np.concatenate([qs & 15, qs >> 4], axis=1)
+    return d, q
+
+
+def dequant_q4_0(b: np.ndarray, shape) -> np.ndarray:
+    """GGUF Q4_0 bytes -> float32 values, reshaped (lab/gguf.py:77-79)."""
+    d, q = q4_0_blocks(b)
+    return (d[:, None] * (q.astype(np.float32) - 8)).reshape(shape)
+
+
+def quantize_q8_1(x: np.ndarray):
+    """fp32 [T, K] -> (qs int8 [T, K], d fp16 [T, K/32], s fp16 [T, K/32]).
+    pinned by: known-answer blocks (amax element -> +-127, all-zero block -> q = 0, d = 0), the bound
+    |x - d q| <= d/2 for every element, and brute-force per-element loops on tiny inputs."""
+    x = np.asarray(x, dtype=np.float32)
+    T, K = x.shape
+    xb = x.reshape(T, K // QK, QK)
+    amax = np.abs(xb).max(axis=2)
+    d16 = (amax / np.float32(127.0)).astype(np.float32).astype(np.float16)
+    df = d16.astype(np.float32)
+    with np.errstate(divide="ignore", invalid="ignore"):
+        r = np.where(df[..., None] != 0, xb / df[..., None], np.float32(0.0)).astype(np.float32)
+    q = np.clip(round_half_away(r), -127, 127).astype(np.int8)
+    sq = q.astype(np.int32).sum(axis=2)
+    s = (df * sq.astype(np.float32)).astype(np.float16)
+    return q.reshape(T, K), d16, s
+
+
+def dequant_q8_1(q: np.ndarray, d: np.ndarray) -> np.ndarray:
+    T, K = q.shape
+    return (q.reshape(T, K // QK, QK).astype(np.float32) * d.astype(np.float32)[..., None]).reshape(T, K)
+
+
+def block_dots(qw: np.ndarray, qx: np.ndarray) -> np.ndarray:
+    """Unsigned-nibble x int8 per-block dots: qw uint8 [N, K] (0..15), qx int8 [T, K] -> int32 [T, N, K/32].
+    Exact integer arithmetic (the values the GPU's v_dot4 / MFMA i8 chains must reproduce bit for bit).
+    pinned by: brute-force triple loop on tiny shapes (tests)."""
+    N, K = qw.shape
+    T = qx.shape[0]
+    a = qw.reshape(N, K // QK, QK).astype(np.int32)
+    b = qx.reshape(T, K // QK, QK).astype(np.int32)
+    return np.einsum("nbi,tbi->tnb", a, b, optimize=True).astype(np.int32)
+
+
+def gemv_q4_0_q8_1(wbytes: np.ndarray, N: int, K: int, qx: np.ndarray, dx: np.ndarray) -> np.ndarray:
+    """Y[T, N] = sum_b d_w[n,b] d_x[t,b] (dot_b - 8 sum(q_x,b)), accumulated in float64, returned fp32.
+    wbytes: GGUF Q4_0 bytes of W [N, K] (row-major); qx int8 [T, K], dx fp16 [T, K/32].
+    pinned by: equality (to fp64 rounding) with the dequantize-then-matmul form
+    (d_w (q_w - 8)) @ (d_x q_x)^T, which has no int32 dot and no -8 sum(q) correction term."""
+    dw, qw = q4_0_blocks(wbytes)
+    dw = dw.reshape(N, K // QK).astype(np.float64)
+    qw = qw.reshape(N, K)
+    T = qx.shape[0]
+    dots = block_dots(qw, qx).astype(np.int64)                       # [T, N, nb]
+    sq = qx.reshape(T, K // QK, QK).astype(np.int64).sum(axis=2)    # [T, nb]
+    sumi = dots - 8 * sq[:, None, :]
+    y = np.einsum("tnb,nb,tb->tn", sumi.astype(np.float64), dw, dx.astype(np.float64), optimize=True)
+    return y.astype(np.float32)
+
+
+def gemv_dequant_f64(wbytes: np.ndarray, N: int, K: int, qx: np.ndarray, dx: np.ndarray) -> np.ndarray:
+    """Independent form of gemv_q4_0_q8_1 (dequantize both operands, float64 matmul); pins it."""
+    w = dequant_q4_0(wbytes, (N, K)).astype(np.float64)
+    x = dequant_q8_1(qx, dx).astype(np.float64)
+    return (x @ w.T).astype(np.float32)
