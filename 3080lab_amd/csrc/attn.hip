@@ -1,117 +1,165 @@
 // Decode GQA attention over the paged fp16 KV cache, split-K over pages (flash-decoding), gfx950.
 //
-// Workgroup (chunk c, KV head g, token j) stages one 64-position K page and V page in LDS (32 KB,
-// every lane issues 8 x 16 B loads up front), scores all NH/NKV query heads of the group against
-// it (each K/V byte is read once per group, not once per query head), and writes the partial
-// (o[128], running max m, sum l) per query head. The last workgroup of (j, g) to arrive (arrival
-// counter, self-resetting, so graph replays need no re-initialisation) merges the partials in
-// fixed chunk order and writes the O-projection input already quantized to Q8_1.
-// Semantics follow ATTN2 / ATTN4 (split-K flash decoding and softmax with max subtraction).
+// k_attn_decode: workgroup (chunk c, KV head g, token j) = one wave per query head of the GQA group
+// (G waves). It stages one 64-position K page (row-padded against LDS bank conflicts) and V page in
+// LDS, lane p scores position p for its wave's head, the softmax numerator is a wave reduction, and
+// lane l accumulates dims 2l, 2l+1 of P.V. Output: the unnormalised partial (o[128], m, l) per
+// (token, query head, chunk). No atomics and no cross-workgroup waits.
+// attn_merge_*: merges the partials of one token in fixed chunk order (o = sum_c e^(m_c - M) o_c / L)
+// and quantizes the result to Q8_1 -- fused into the O-projection GEMV prologue, or standalone.
+// Semantics follow ATTN2 / ATTN4 (lab/qwen_kernels.py:358-442, 517-605).
 #include "common.h"
 #include "q355_kernels.h"
 
 namespace q355 {
 
-constexpr int MAXG = 8;  // query heads per KV head supported (Qwen2.5-1.5B: 6)
+constexpr int KROW = HD + 8;  // padded K row in LDS (halves)
 
-__global__ void __launch_bounds__(256) k_attn_decode(const AttnArgs a) {
-  __shared__ __align__(16) __half ks[PAGE][HD];
+template <int G>
+__global__ void __launch_bounds__(G * 64) k_attn_decode(const AttnArgs a) {
+  __shared__ __align__(16) __half ks[PAGE][KROW];
   __shared__ __align__(16) __half vs[PAGE][HD];
-  __shared__ float qf[MAXG][HD];
-  __shared__ float S[MAXG][PAGE];
-  __shared__ float ml[MAXG][2];
-  __shared__ int am_last;
+  __shared__ __align__(16) float qf[G][HD];
+  __shared__ float E[G][PAGE];
 
   const int j = blockIdx.y;
   const int kvh = blockIdx.x / a.max_chunks, c = blockIdx.x % a.max_chunks;
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int pos = a.pos[j];
-  const int nctx = pos + 1, nch = (nctx + PAGE - 1) / PAGE;
-  if (c >= nch) return;                       // whole workgroup leaves; it is not counted
-  const int grp = a.nh / a.nkv;
-  const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
-  const int nvalid = min(PAGE, nctx - c * PAGE);
-
   const int pg = a.block_table[(size_t)j * a.bt_stride + c];
+  const int hq = kvh * G + wv;
+  const half2 qv = ((const half2*)(a.q + ((size_t)j * a.nh + hq) * HD))[lane];
+  if (c * PAGE > pos) return;                       // chunk beyond the context: nothing to do
+  const int nvalid = min(PAGE, pos + 1 - c * PAGE);
+
   const uint4* kp = (const uint4*)(a.kcache + ((size_t)pg * a.nkv + kvh) * PAGE * HD);
   const uint4* vp = (const uint4*)(a.vcache + ((size_t)pg * a.nkv + kvh) * PAGE * HD);
-  uint4 kr[4], vr[4];
+  constexpr int NT = G * 64, PER = (PAGE * HD / 8 + NT - 1) / NT;
+  uint4 kr[PER], vr[PER];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) { kr[i] = kp[t + 256 * i]; vr[i] = vp[t + 256 * i]; }
-  // queries of the group: grp * 128 halves
-  const __half* qh = a.q + (size_t)j * a.nh * HD + (size_t)kvh * grp * HD;
-  for (int e = t; e < grp * HD; e += 256) qf[e / HD][e % HD] = __half2float(qh[e]);
+  for (int i = 0; i < PER; ++i) {
+    const int e = min(threadIdx.x + NT * i, PAGE * HD / 8 - 1);   // clamped: loads stay unconditional
+    kr[i] = kp[e];
+    vr[i] = vp[e];
+  }
+  const float2 qq = __half22float2(qv);
+  qf[wv][2 * lane] = qq.x;
+  qf[wv][2 * lane + 1] = qq.y;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) { ((uint4*)ks)[t + 256 * i] = kr[i]; ((uint4*)vs)[t + 256 * i] = vr[i]; }
+  for (int i = 0; i < PER; ++i) {
+    const int e = threadIdx.x + NT * i;
+    if (e < PAGE * HD / 8) {
+      *(uint4*)&ks[e >> 4][(e & 15) * 8] = kr[i];
+      ((uint4*)vs)[e] = vr[i];
+    }
+  }
   __syncthreads();
 
-  // scores: thread (p = t / 4, quarter qq = t % 4) covers dims [32qq, 32qq + 32) of position p
+  // scores: lane p, this wave's head
+  float s = 0.f;
   {
-    const int p = t >> 2, qq = t & 3;
-    float kf[32];
-    const __half2* krow = (const __half2*)&ks[p][32 * qq];
+    const float* qh = qf[wv];
 #pragma unroll
-    for (int i = 0; i < 16; ++i) { float2 f = __half22float2(krow[i]); kf[2 * i] = f.x; kf[2 * i + 1] = f.y; }
-    for (int h = 0; h < grp; ++h) {
-      float s = 0.f;
+    for (int i = 0; i < HD / 8; ++i) {
+      const uint4 kk = *(const uint4*)&ks[lane][8 * i];
+      const __half2* k2 = (const __half2*)&kk;
 #pragma unroll
-      for (int i = 0; i < 32; ++i) s = fmaf(qf[h][32 * qq + i], kf[i], s);
-      s += __shfl_xor(s, 1, 64);
-      s += __shfl_xor(s, 2, 64);
-      if (qq == 0) S[h][p] = p < nvalid ? s * a.scale : -INFINITY;
+      for (int u = 0; u < 4; ++u) {
+        const float2 kf = __half22float2(k2[u]);
+        s = fmaf(qh[8 * i + 2 * u], kf.x, s);
+        s = fmaf(qh[8 * i + 2 * u + 1], kf.y, s);
+      }
     }
   }
+  s = lane < nvalid ? s * a.scale : -INFINITY;
+  const float m = wave_max(s);
+  const float e = lane < nvalid ? expf(s - m) : 0.f;
+  const float l = wave_sum(e);
+  E[wv][lane] = e;
   __syncthreads();
-  // softmax numerators per head: wave w handles heads w, w + 4
-  for (int h = wv; h < grp; h += 4) {
-    float s = S[h][lane];
-    float m = wave_max(s);
-    float e = lane < nvalid ? expf(s - m) : 0.f;
-    float l = wave_sum(e);
-    S[h][lane] = e;
-    if (lane == 0) { ml[h][0] = m; ml[h][1] = l; }
+
+  // P.V: lane owns dims 2*lane, 2*lane+1
+  float o0 = 0.f, o1 = 0.f, o2 = 0.f, o3 = 0.f;
+  int p = 0;
+  for (; p + 1 < nvalid; p += 2) {
+    const float2 v0 = __half22float2(((const __half2*)vs[p])[lane]);
+    const float2 v1 = __half22float2(((const __half2*)vs[p + 1])[lane]);
+    const float e0 = E[wv][p], e1 = E[wv][p + 1];
+    o0 = fmaf(e0, v0.x, o0);
+    o1 = fmaf(e0, v0.y, o1);
+    o2 = fmaf(e1, v1.x, o2);
+    o3 = fmaf(e1, v1.y, o3);
+  }
+  if (p < nvalid) {
+    const float2 v0 = __half22float2(((const __half2*)vs[p])[lane]);
+    o0 = fmaf(E[wv][p], v0.x, o0);
+    o1 = fmaf(E[wv][p], v0.y, o1);
+  }
+  float* P = a.part + (((size_t)j * a.nh + hq) * a.max_chunks + c) * (HD + 2);
+  ((float2*)P)[lane] = make_float2(o0 + o2, o1 + o3);
+  if (lane == 0) { P[HD] = m; P[HD + 1] = l; }
+}
+
+// ---------------------------------------------------------------------------------------------
+// Merge of one token's partials (nh query heads, nch chunks). Called by every thread of a workgroup of
+// NTH threads; `wgt` is LDS scratch of 2 * nh * max_chunks floats; writes o[h * HD + d] to `out` (LDS).
+template <int NTH>
+__device__ __forceinline__ void attn_merge_token(const float* __restrict__ part, int nh, int max_chunks, int nch,
+                                                 float* wgt, float* out) {
+  // 1. per (h, c): raw m, l -> per-head M, L -> weights e^(m_c - M) / L
+  for (int hc = threadIdx.x; hc < nh * nch; hc += NTH) {
+    const int h = hc / nch, c = hc % nch;
+    const float* P = part + ((size_t)h * max_chunks + c) * (HD + 2);
+    wgt[h * max_chunks + c] = P[HD];
+    wgt[nh * max_chunks + h * max_chunks + c] = P[HD + 1];
   }
   __syncthreads();
-  // P V: thread (dim pair d2 = lane, heads wv, wv + 4)
-  float* part = a.part + (size_t)j * a.nh * a.max_chunks * (HD + 2);
-  for (int h = wv; h < grp; h += 4) {
-    float o0 = 0.f, o1 = 0.f;
-    for (int p = 0; p < nvalid; ++p) {
-      const float pr = S[h][p];
-      const float2 v = __half22float2(((const __half2*)vs[p])[lane]);
-      o0 = fmaf(pr, v.x, o0);
-      o1 = fmaf(pr, v.y, o1);
-    }
-    float* P = part + ((size_t)(kvh * grp + h) * a.max_chunks + c) * (HD + 2);
-    P[2 * lane] = o0;
-    P[2 * lane + 1] = o1;
-    if (lane == 0) { P[HD] = ml[h][0]; P[HD + 1] = ml[h][1]; }
-  }
-  __threadfence();
-  __syncthreads();
-  if (t == 0) am_last = atomicAdd(a.counter + (size_t)j * a.nkv + kvh, 1u) == (unsigned)(nch - 1);
-  __syncthreads();
-  if (!am_last) return;
-  __threadfence();
-  // merge: thread (d = t % 128) for heads h = t / 128, +2, +4 ... ; 32-lane groups = one Q8_1 block
-  const int d = t & (HD - 1);
-  for (int h = t >> 7; h < grp; h += 2) {
-    const float* P0 = part + (size_t)(kvh * grp + h) * a.max_chunks * (HD + 2);
+  if (threadIdx.x < nh) {
+    const int h = threadIdx.x;
     float M = -INFINITY;
-    for (int cc = 0; cc < nch; ++cc) M = fmaxf(M, __builtin_nontemporal_load(P0 + (size_t)cc * (HD + 2) + HD));
-    float L = 0.f, O = 0.f;
-    for (int cc = 0; cc < nch; ++cc) {
-      const float* Pc = P0 + (size_t)cc * (HD + 2);
-      const float w = expf(__builtin_nontemporal_load(Pc + HD) - M);
-      L = fmaf(w, __builtin_nontemporal_load(Pc + HD + 1), L);
-      O = fmaf(w, __builtin_nontemporal_load(Pc + d), O);
-    }
-    const float o = O / L;
-    const int hq = kvh * grp + h;
-    if (a.o32) a.o32[(size_t)j * a.nh * HD + hq * HD + d] = o;
-    const int q = q8_1_lane32(o, a.ods + ((size_t)j * a.nh * HD + hq * HD + d) / 32, (d & 31) == 0);
-    a.oq[(size_t)j * a.nh * HD + hq * HD + d] = (int8_t)q;
+    for (int c = 0; c < nch; ++c) M = fmaxf(M, wgt[h * max_chunks + c]);
+    float L = 0.f;
+    for (int c = 0; c < nch; ++c) L = fmaf(expf(wgt[h * max_chunks + c] - M), wgt[nh * max_chunks + h * max_chunks + c], L);
+    const float inv = 1.0f / L;
+    for (int c = 0; c < nch; ++c) wgt[h * max_chunks + c] = expf(wgt[h * max_chunks + c] - M) * inv;
   }
-  if (t == 0) a.counter[(size_t)j * a.nkv + kvh] = 0u;
+  __syncthreads();
+  // 2. o[h][d] = sum_c w[h][c] o_c[d], chunks in fixed order, 4 loads in flight per thread
+  for (int e = threadIdx.x; e < nh * HD; e += NTH) {
+    const int h = e / HD, d = e % HD;
+    const float* P = part + (size_t)h * max_chunks * (HD + 2) + d;
+    const float* w = wgt + h * max_chunks;
+    float o = 0.f;
+    int c = 0;
+    for (; c + 3 < nch; c += 4) {
+      const float p0 = P[(size_t)c * (HD + 2)], p1 = P[(size_t)(c + 1) * (HD + 2)];
+      const float p2 = P[(size_t)(c + 2) * (HD + 2)], p3 = P[(size_t)(c + 3) * (HD + 2)];
+      o = fmaf(w[c], p0, o);
+      o = fmaf(w[c + 1], p1, o);
+      o = fmaf(w[c + 2], p2, o);
+      o = fmaf(w[c + 3], p3, o);
+    }
+    for (; c < nch; ++c) o = fmaf(w[c], P[(size_t)c * (HD + 2)], o);
+    out[e] = o;
+  }
+  __syncthreads();
+}
+
+// Standalone merge: one workgroup per token -> fp32 o32 (optional) and Q8_1 oq/ods.
+__global__ void __launch_bounds__(256) k_attn_merge(const AttnArgs a) {
+  extern __shared__ float sm[];
+  const int j = blockIdx.x;
+  const int nch = a.pos[j] / PAGE + 1;
+  float* wgt = sm;                                   // 2 * nh * max_chunks
+  float* o = sm + 2 * a.nh * a.max_chunks;           // nh * HD
+  attn_merge_token<256>(a.part + (size_t)j * a.nh * a.max_chunks * (HD + 2), a.nh, a.max_chunks, nch, wgt, o);
+  const int n = a.nh * HD;
+  for (int e = threadIdx.x; e < n; e += 256) {      // n % 256 == 0 keeps 32-lane groups whole
+    const float v = o[e];
+    if (a.o32) a.o32[(size_t)j * n + e] = v;
+    const int q = q8_1_lane32(v, a.ods + ((size_t)j * n + e) / 32, (e & 31) == 0);
+    a.oq[(size_t)j * n + e] = (int8_t)q;
+  }
 }
 
 }  // namespace q355

@@ -53,6 +53,67 @@ __device__ __forceinline__ int sum_i8x32(const int* x) {
   return s;
 }
 
+// DPP lane exchanges (no LDS traffic): quad_perm xor 1 / xor 2, half-row mirror, row mirror.
+constexpr int DPP_XOR1 = 0xB1, DPP_XOR2 = 0x4E, DPP_HALF_MIRROR = 0x141, DPP_MIRROR = 0x140;
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, true));
+}
+template <int CTRL>
+__device__ __forceinline__ int dpp(int v) {
+  return __builtin_amdgcn_mov_dpp(v, CTRL, 0xF, 0xF, true);
+}
+// Reductions over aligned groups of 4 lanes (every lane of the group gets the result).
+__device__ __forceinline__ float quad_max(float v) {
+  v = fmaxf(v, dpp<DPP_XOR1>(v));
+  return fmaxf(v, dpp<DPP_XOR2>(v));
+}
+__device__ __forceinline__ int quad_isum(int v) {
+  v += dpp<DPP_XOR1>(v);
+  return v + dpp<DPP_XOR2>(v);
+}
+__device__ __forceinline__ float quad_sum(float v) {
+  v += dpp<DPP_XOR1>(v);
+  return v + dpp<DPP_XOR2>(v);
+}
+// Full wave64 sum: 4 DPP steps inside each row of 16, then two cross-row exchanges.
+__device__ __forceinline__ float wave_sum_fast(float v) {
+  v += dpp<DPP_XOR1>(v);
+  v += dpp<DPP_XOR2>(v);
+  v += dpp<DPP_HALF_MIRROR>(v);
+  v += dpp<DPP_MIRROR>(v);
+  v += __shfl_xor(v, 16, 64);
+  return v + __shfl_xor(v, 32, 64);
+}
+
+// Q8_1 of 8 consecutive values held by one lane; 4 lanes form a 32-block (lane groups aligned to 4).
+// Bit-exact with the oracle (d = fp16(amax/127), q = roundf(x / d16) clamped, 0 when d16 == 0).
+// Returns the 8 int8 packed in a uint2; d (as float) and the block's sum of q through the references.
+__device__ __forceinline__ uint2 q8_1_x8(const float (&x)[8], float& df, int& sq) {
+  float amax = 0.f;
+#pragma unroll
+  for (int u = 0; u < 8; ++u) amax = fmaxf(amax, fabsf(x[u]));
+  amax = quad_max(amax);
+  df = __half2float(__float2half_rn(amax / 127.0f));
+  const bool live = df != 0.0f;
+  const float dv = live ? df : 1.0f;   // branch-free: a dead block divides by 1 and selects 0
+  int q[8];
+  int s = 0;
+#pragma unroll
+  for (int u = 0; u < 8; ++u) {
+    int v = (int)roundf(x[u] / dv);
+    v = v > 127 ? 127 : (v < -127 ? -127 : v);
+    v = live ? v : 0;
+    q[u] = v;
+    s += v;
+  }
+  sq = quad_isum(s);
+  uint2 pk;
+  pk.x = (q[0] & 255) | ((q[1] & 255) << 8) | ((q[2] & 255) << 16) | ((unsigned)(q[3] & 255) << 24);
+  pk.y = (q[4] & 255) | ((q[5] & 255) << 8) | ((q[6] & 255) << 16) | ((unsigned)(q[7] & 255) << 24);
+  return pk;
+}
+
 // Wave64 reductions (xor butterfly over all 64 lanes, or over `width` lanes).
 template <int WIDTH = 64>
 __device__ __forceinline__ float wave_sum(float v) {

@@ -1,12 +1,18 @@
 // Q8_1 quantizers and the Q4_0 x Q8_1 GEMV (1..4 tokens) with fused prologues/epilogues, gfx950.
 //
-// GEMV work split: a workgroup of 4 waves owns NT 16-row tiles; the 4 waves x 4 lane slots split
-// the K blocks 16 ways (block b goes to k-lane b % 16), lane (slot, row) streams 16 B of nibbles per
-// block (1 KB contiguous per wave instruction) and dots it with the activation block held in LDS
-// (v_dot4_i32_i8, exact int32). Partials reduce over slots (lane xor 16, 32) and over waves through
-// LDS in a fixed order, so results are bitwise reproducible run to run.
+// GEMV work split: workgroup (x, y) owns NT 16-row tiles and the y-th of gridDim.y slices of the K
+// blocks; its NW waves x 4 lane slots split the slice 4*NW ways (block b of the slice goes to k-lane
+// b % (4*NW)). Lane (slot, row) streams 16 B of nibbles per block (1 KB contiguous per wave
+// instruction) and dots it with the activation block held in LDS (v_dot4_i32_i8, exact int32).
+// Partials reduce over slots (lane xor 16, 32) and over waves through LDS in a fixed order. K slices
+// of the residual projections meet in the int64 fixed-point residual stream (integer atomics), so
+// every output is bitwise reproducible run to run.
+//
+// Per-CU streaming bandwidth on MI355X is ~20-28 GB/s (HBM needs all 256 CUs busy), so every launch
+// is cut into >= ~300 workgroups: N = 1536 projections use K slices, gate_up uses one tile each.
 #include "common.h"
 #include "q355_kernels.h"
+#include "attn.hip"
 
 namespace q355 {
 
@@ -63,7 +69,12 @@ __global__ void __launch_bounds__(256) k_rmsnorm_q8_1(const float* __restrict__ 
 }
 
 // ---------------------------------------------------------------------------------------------
-// LDS staging of the activation operand: xq bytes [T][K], dx float [T][nb], sq int [T][nb].
+// GEMV building blocks. Latency plan of every GEMV launch:
+//   1. issue the activation loads (residual + norm weight, fp32 input, or xq + xds),
+//   2. issue every weight load of this lane (NT tiles x KPL blocks of 16 B, all in flight at once),
+//   3. build the Q8_1 activation operand in LDS while the weights are in flight,
+//   4. int8 dots from registers, fixed-order reductions, fused epilogue.
+// LDS activation operand (indexed by absolute K block): xq bytes [T][K], dx float [T][nb], sq int [T][nb].
 struct XStage {
   int8_t* q;
   float* d;
@@ -78,107 +89,209 @@ __device__ __forceinline__ XStage xstage_carve(char* lds, int T, int K) {
   return s;
 }
 
-// Pre-quantized input: copy xq/xds into LDS and precompute per-block sums.
-__device__ __forceinline__ void prologue_q8(const XStage& st, const int8_t* __restrict__ xq,
-                                            const half2* __restrict__ xds, int T, int K) {
-  const int nb = K / 32;
-  for (int task = threadIdx.x; task < T * nb; task += blockDim.x) {
-    const int4* src = (const int4*)(xq + (size_t)task * 32);
-    int4 a = src[0], b = src[1];
-    int4* dst = (int4*)(st.q + (size_t)task * 32);
-    dst[0] = a;
-    dst[1] = b;
-    int xv[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-    st.s[task] = sum_i8x32(xv);
-    st.d[task] = __low2float(xds[task]);
+// Store one lane's 8 quantized values (and, from the first lane of the 4-lane block, d and sum q).
+__device__ __forceinline__ void stage_x8(const XStage& st, int K, int j, int g, const float (&x)[8]) {
+  float df;
+  int sq;
+  const uint2 pk = q8_1_x8(x, df, sq);
+  *(uint2*)(st.q + (size_t)j * K + 8 * g) = pk;
+  if ((g & 3) == 0) {
+    st.d[j * (K / 32) + (g >> 2)] = df;
+    st.s[j * (K / 32) + (g >> 2)] = sq;
   }
 }
 
-// Fused RMSNorm + Q8_1 prologue: h fp32 [T][K] normalized with nw, quantized into LDS.
-__device__ __forceinline__ void prologue_rms(const XStage& st, const float* __restrict__ h,
-                                             const float* __restrict__ nw, float eps, int T, int K, float* red) {
-  for (int tok = 0; tok < T; ++tok) {
-    const float* hr = h + (size_t)tok * K;
-    float v[8];
-    float ss = 0.f;
+// K-block slice of this workgroup.
+struct KSlice {
+  int b0, b1;
+  __device__ __forceinline__ KSlice(int nb) {
+    const int per = (nb + gridDim.y - 1) / gridDim.y;
+    b0 = min(nb, (int)blockIdx.y * per);
+    b1 = min(nb, b0 + per);
+  }
+};
+
+// Activation operand, stage 1 (loads into registers) and stage 2 (quantize / copy into LDS).
+// RMS / F32 / ATTN: a task is 8 consecutive values of one token (4 lanes = one Q8_1 block).
+template <int T, int NW, int PRO>
+struct XLoad {
+  static constexpr int NTH = NW * 64;
+  static constexpr bool R = PRO == PRO_RMS, F = PRO == PRO_F32, Q = PRO == PRO_Q8;
+  static constexpr int P8 = (T * 1536 / 8 + NTH - 1) / NTH;   // RMS: 8-value tasks per thread (K <= 1536)
+  static constexpr int PF = (T * 2304 / 8 + NTH - 1) / NTH;   // F32: tasks per thread (slice <= 2304 values)
+  static constexpr int PT = (T * 288 + NTH - 1) / NTH;        // Q8: 32-blocks per thread (K <= 9216)
+  static constexpr int NX = R ? P8 : (F ? PF : 1);
+  long long hl[R ? P8 : 1][8];
+  float4 xa[NX], xb[NX];                                       // F32 input, or RMS norm weights
+  int4 qa[Q ? PT : 1], qb[Q ? PT : 1];
+  float dx[Q ? PT : 1];
+
+  __device__ __forceinline__ void load(const GemvArgs& a, const KSlice& ks) {
+    const int K = a.K;
+    // tasks past the end re-load the last valid task (clamped): unconditional, straight-line loads
+    if (R) {
+      const int ng = K / 8, ntask = a.T * ng;
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      int i = threadIdx.x + 256 * u;
-      v[u] = i < K ? hr[i] : 0.f;
-      ss += v[u] * v[u];
+      for (int p = 0; p < P8; ++p) {
+        const int task = min(threadIdx.x + NTH * p, ntask - 1);
+        const int j = task / ng, g = task % ng;
+        const longlong2* hp = (const longlong2*)(a.hfix + (size_t)j * K + 8 * g);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) { const longlong2 v = hp[u]; hl[p][2 * u] = v.x; hl[p][2 * u + 1] = v.y; }
+        const float4* wp = (const float4*)(a.nw + 8 * g);
+        xa[p] = wp[0];
+        xb[p] = wp[1];
+      }
+    } else if (F) {
+      const int g0 = ks.b0 * 4, ng = (ks.b1 - ks.b0) * 4, ntask = a.T * ng;
+#pragma unroll
+      for (int p = 0; p < PF; ++p) {
+        const int task = min(threadIdx.x + NTH * p, ntask - 1);
+        const int j = task / ng, g = g0 + task % ng;
+        const float4* xp = (const float4*)(a.xf + (size_t)j * K + 8 * g);
+        xa[p] = xp[0];
+        xb[p] = xp[1];
+      }
+    } else if (Q) {
+      const int nbs = ks.b1 - ks.b0, ntask = a.T * nbs;
+#pragma unroll
+      for (int p = 0; p < PT; ++p) {
+        const int task = min(threadIdx.x + NTH * p, ntask - 1);
+        const int j = task / nbs, b = ks.b0 + task % nbs;
+        const int4* src = (const int4*)(a.xq + (size_t)j * K + (size_t)b * 32);
+        qa[p] = src[0];
+        qb[p] = src[1];
+        dx[p] = __low2float(a.xds[(size_t)j * (K / 32) + b]);
+      }
     }
-    float r = 1.0f / sqrtf(block_sum_256(ss, red) / (float)K + eps);
-#pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      int i = threadIdx.x + 256 * u;
-      if (256 * u < K) {
-        bool act = i < K;
-        float x = act ? v[u] * r * nw[i] : 0.f;
-        float amax = wave_max<32>(fabsf(x));
-        __half d16 = __float2half_rn(amax / 127.0f);
-        float df = __half2float(d16);
-        int q = 0;
-        if (df != 0.0f) {
-          q = (int)roundf(x / df);
-          q = q > 127 ? 127 : (q < -127 ? -127 : q);
+  }
+
+  __device__ __forceinline__ void stage(const GemvArgs& a, const KSlice& ks, const XStage& st, float* red,
+                                        char* extra) {
+    const int K = a.K, nb = K / 32;
+    if (PRO == PRO_ATTN) {
+      // merge the split-K attention partials of the heads in this K slice, then Q8_1 into LDS
+      float* wgt = (float*)extra;
+      float* ob = wgt + 2 * a.nh * a.attn_max_chunks;
+      const int h0 = ks.b0 * 32 / HD, nhs = (ks.b1 - ks.b0) * 32 / HD;
+      for (int j = 0; j < a.T; ++j) {
+        const int nch = a.pos[j] / PAGE + 1;
+        attn_merge_token<NTH>(a.attn_part + ((size_t)j * a.nh + h0) * a.attn_max_chunks * (HD + 2), nhs,
+                              a.attn_max_chunks, nch, wgt, ob);
+        for (int g = threadIdx.x; g < nhs * HD / 8; g += NTH) {   // quads stay whole (HD / 8 % 4 == 0)
+          const float4 u0 = ((const float4*)ob)[2 * g], u1 = ((const float4*)ob)[2 * g + 1];
+          const float x[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
+          stage_x8(st, K, j, h0 * HD / 8 + g, x);
         }
-        int sq = wave_isum<32>(q);
-        if (act) {
-          st.q[(size_t)tok * K + i] = (int8_t)q;
-          if ((threadIdx.x & 31) == 0) {
-            st.d[tok * (K / 32) + (i >> 5)] = df;
-            st.s[tok * (K / 32) + (i >> 5)] = sq;
-          }
+        __syncthreads();
+      }
+    } else if (R) {
+      const int ng = K / 8, ntask = a.T * ng;
+      float hv[P8][8];
+      float ss[T];
+#pragma unroll
+      for (int j = 0; j < T; ++j) ss[j] = 0.f;
+#pragma unroll
+      for (int p = 0; p < P8; ++p) {
+        const int task = threadIdx.x + NTH * p;
+        float v = 0.f;
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          hv[p][u] = from_fix(hl[p][u]);
+          v = fmaf(hv[p][u], hv[p][u], v);
+        }
+#pragma unroll
+        for (int j = 0; j < T; ++j) ss[j] += (task < ntask && task / ng == j) ? v : 0.f;
+      }
+#pragma unroll
+      for (int j = 0; j < T; ++j) {
+        const float w = wave_sum_fast(ss[j]);
+        if ((threadIdx.x & 63) == 0) red[(threadIdx.x >> 6) * T + j] = w;
+      }
+      __syncthreads();
+      float rs[T];
+#pragma unroll
+      for (int j = 0; j < T; ++j) {
+        float t = 0.f;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) t += red[w * T + j];
+        rs[j] = 1.0f / sqrtf(t / (float)K + a.eps);
+      }
+#pragma unroll
+      for (int p = 0; p < P8; ++p) {
+        const int task = threadIdx.x + NTH * p;
+        if (task < ntask) {
+          const int j = task / ng, g = task % ng;
+          float r = rs[0];
+#pragma unroll
+          for (int jj = 1; jj < T; ++jj) r = (j == jj) ? rs[jj] : r;
+          const float x[8] = {hv[p][0] * r * xa[p].x, hv[p][1] * r * xa[p].y, hv[p][2] * r * xa[p].z,
+                              hv[p][3] * r * xa[p].w, hv[p][4] * r * xb[p].x, hv[p][5] * r * xb[p].y,
+                              hv[p][6] * r * xb[p].z, hv[p][7] * r * xb[p].w};
+          stage_x8(st, K, j, g, x);
+        }
+      }
+    } else if (F) {
+      const int g0 = ks.b0 * 4, ng = (ks.b1 - ks.b0) * 4, ntask = a.T * ng;
+#pragma unroll
+      for (int p = 0; p < PF; ++p) {
+        const int task = threadIdx.x + NTH * p;
+        if (task < ntask) {
+          const int j = task / ng, g = g0 + task % ng;
+          const float x[8] = {xa[p].x, xa[p].y, xa[p].z, xa[p].w, xb[p].x, xb[p].y, xb[p].z, xb[p].w};
+          stage_x8(st, K, j, g, x);
+        }
+      }
+    } else {
+      const int nbs = ks.b1 - ks.b0, ntask = a.T * nbs;
+#pragma unroll
+      for (int p = 0; p < PT; ++p) {
+        const int task = threadIdx.x + NTH * p;
+        if (task < ntask) {
+          const int j = task / nbs, b = ks.b0 + task % nbs;
+          int4* dst = (int4*)(st.q + (size_t)j * K + (size_t)b * 32);
+          dst[0] = qa[p];
+          dst[1] = qb[p];
+          const int xv[8] = {qa[p].x, qa[p].y, qa[p].z, qa[p].w, qb[p].x, qb[p].y, qb[p].z, qb[p].w};
+          st.s[j * nb + b] = sum_i8x32(xv);
+          st.d[j * nb + b] = dx[p];
         }
       }
     }
   }
-}
+};
 
 // ---------------------------------------------------------------------------------------------
 // Epilogues. part[w][t][j][r] holds wave w's partial of row (tile0 + t) * 16 + r for token j.
-template <int T, int NT>
-__device__ __forceinline__ float row_value(float (&part)[4][NT][T][16], int t, int j, int r) {
-  return ((part[0][t][j][r] + part[1][t][j][r]) + part[2][t][j][r]) + part[3][t][j][r];
+template <int NW, int T, int NT>
+__device__ __forceinline__ float row_value(float (&part)[NW][NT][T][16], int t, int j, int r) {
+  float v = part[0][t][j][r];
+#pragma unroll
+  for (int w = 1; w < NW; ++w) v += part[w][t][j][r];
+  return v;
 }
 
 __device__ __forceinline__ float silu_mul(float g, float u) { return g / (1.0f + expf(-g)) * u; }
 
-template <int T, int NT, int EPI>
-__device__ __forceinline__ void epilogue(const GemvArgs& a, float (&part)[4][NT][T][16], int tile0) {
+template <int NW, int T, int NT, int EPI>
+__device__ __forceinline__ void epilogue(const GemvArgs& a, float (&part)[NW][NT][T][16], int tile0) {
   const int N = a.N;
-  if (EPI == EPI_SWIGLU_Q8) {
-    // NT == 4: 64 interleaved rows (g0, u0, g1, u1, ...) -> 32 outputs = one Q8_1 block per token
-    const int j = threadIdx.x >> 5, k = threadIdx.x & 31;
-    if (j < T && j < a.T) {
-      const int rg = 2 * k, ru = 2 * k + 1;
-      float g = row_value<T, NT>(part, rg >> 4, j, rg & 15);
-      float u = row_value<T, NT>(part, ru >> 4, j, ru & 15);
-      float m = silu_mul(g, u);
-      const int Nout = N / 2;
-      int q = q8_1_lane32(m, a.ods + (size_t)j * (Nout / 32) + blockIdx.x, k == 0);
-      a.oq[(size_t)j * Nout + blockIdx.x * 32 + k] = (int8_t)q;
-    }
-    return;
-  }
   if (EPI == EPI_LOGITS) {
-    __shared__ float vals[T][NT * 16];
-    for (int e = threadIdx.x; e < NT * T * 16; e += blockDim.x) {
-      const int t = e / (T * 16), j = (e >> 4) % T, r = e & 15;
-      float v = row_value<T, NT>(part, t, j, r);
-      vals[j][t * 16 + r] = v;
-      if (j < a.T) a.y[(size_t)j * N + (tile0 + t) * 16 + r] = v;
-    }
-    __syncthreads();
+    // one wave computes the (value, row) argmax of the NT * 16 rows, lowest row on ties
     if (threadIdx.x < 64) {
       const int l = threadIdx.x;
       for (int j = 0; j < T && j < a.T; ++j) {
-        float v = l < NT * 16 ? vals[j][l] : -INFINITY;
-        int idx = l < NT * 16 ? tile0 * 16 + l : 0x7fffffff;
+        float v = -INFINITY;
+        int idx = 0x7fffffff;
+        for (int rr = l; rr < NT * 16; rr += 64) {   // rows in increasing order: strict '>' keeps the lowest
+          const float x = row_value<NW, T, NT>(part, rr >> 4, j, rr & 15);
+          a.y[(size_t)j * N + tile0 * 16 + rr] = x;
+          if (x > v) { v = x; idx = tile0 * 16 + rr; }
+        }
 #pragma unroll
         for (int o = 32; o > 0; o >>= 1) {
-          float ov = __shfl_xor(v, o, 64);
-          int oi = __shfl_xor(idx, o, 64);
+          const float ov = __shfl_xor(v, o, 64);
+          const int oi = __shfl_xor(idx, o, 64);
           if (ov > v || (ov == v && oi < idx)) { v = ov; idx = oi; }
         }
         if (l == 0) {
@@ -189,16 +302,27 @@ __device__ __forceinline__ void epilogue(const GemvArgs& a, float (&part)[4][NT]
     }
     return;
   }
+  if (EPI == EPI_SWIGLU) {
+    // rows interleaved (g0, u0, g1, u1, ...): one thread per output pair
+    for (int e = threadIdx.x; e < NT * T * 8; e += blockDim.x) {
+      const int t = e / (T * 8), j = (e >> 3) % T, k = e & 7;
+      if (j >= a.T) continue;
+      const float g = row_value<NW, T, NT>(part, t, j, 2 * k), u = row_value<NW, T, NT>(part, t, j, 2 * k + 1);
+      a.y[(size_t)j * (N / 2) + (tile0 + t) * 8 + k] = silu_mul(g, u);
+    }
+    return;
+  }
   for (int e = threadIdx.x; e < NT * T * 16; e += blockDim.x) {
     const int t = e / (T * 16), j = (e >> 4) % T, r = e & 15;
     if (j >= a.T) continue;
     const int row = (tile0 + t) * 16 + r;
-    float v = row_value<T, NT>(part, t, j, r);
+    float v = row_value<NW, T, NT>(part, t, j, r);
     if (EPI == EPI_STORE) {
       a.y[(size_t)j * N + row] = v;
     } else if (EPI == EPI_RESID) {
-      if (gridDim.y == 1) a.y[(size_t)j * N + row] += v;
-      else atomicAdd(a.y + (size_t)j * N + row, v);
+      a.y[(size_t)j * N + row] += v;
+    } else if (EPI == EPI_RESID_FIX) {
+      atomicAdd((unsigned long long*)(a.yfix + (size_t)j * N + row), (unsigned long long)to_fix(v));
     } else if (EPI == EPI_BIAS) {
       a.y[(size_t)j * N + row] = v + a.aux[row];
     } else if (EPI == EPI_QKV) {
@@ -206,8 +330,9 @@ __device__ __forceinline__ void epilogue(const GemvArgs& a, float (&part)[4][NT]
       const int nq = a.nh * HD, nk = a.nkv * HD;
       const int pos = a.pos[j];
       const int seq = j * a.seq_stride;
+      const int pg = a.block_table[(size_t)seq * a.bt_stride + pos / PAGE];
       if (row < nq + nk) {
-        float v2 = row_value<T, NT>(part, t, j, r ^ 1) + a.aux[row ^ 1];
+        const float v2 = row_value<NW, T, NT>(part, t, j, r ^ 1) + a.aux[row ^ 1];
         const int e2 = row % HD, i = e2 >> 1, hi = e2 & 1;
         const float c = a.rope_cos[(size_t)pos * (HD / 2) + i], s = a.rope_sin[(size_t)pos * (HD / 2) + i];
         const float lo_v = hi ? v2 : v, hi_v = hi ? v : v2;
@@ -217,12 +342,10 @@ __device__ __forceinline__ void epilogue(const GemvArgs& a, float (&part)[4][NT]
           a.qout[(size_t)j * nq + (row / HD) * HD + dim] = __float2half_rn(out);
         } else {
           const int kvh = (row - nq) / HD;
-          const int pg = a.block_table[(size_t)seq * a.bt_stride + pos / PAGE];
           a.kcache[(((size_t)pg * a.nkv + kvh) * PAGE + pos % PAGE) * HD + dim] = __float2half_rn(out);
         }
       } else {
         const int rv = row - nq - nk, kvh = rv / HD, dim = rv % HD;
-        const int pg = a.block_table[(size_t)seq * a.bt_stride + pos / PAGE];
         a.vcache[(((size_t)pg * a.nkv + kvh) * PAGE + pos % PAGE) * HD + dim] = __float2half_rn(v);
       }
     }
@@ -230,59 +353,76 @@ __device__ __forceinline__ void epilogue(const GemvArgs& a, float (&part)[4][NT]
 }
 
 // ---------------------------------------------------------------------------------------------
-// The GEMV. Template: T tokens (1..4), NT tiles per workgroup, prologue, epilogue.
-template <int T, int NT, int PRO, int EPI>
-__global__ void __launch_bounds__(256) k_gemv(const GemvArgs a) {
+// The GEMV: T tokens (1..4), NT 16-row tiles per workgroup, NW waves splitting the K slice 4*NW ways,
+// KPL K-blocks per lane (compile time, so all weight loads are issued before the first use).
+template <int T, int NT, int NW, int KPL, int PRO, int EPI>
+__global__ void __launch_bounds__(NW * 64) k_gemv(const GemvArgs a) {
   extern __shared__ __align__(16) char lds[];
-  __shared__ float red[8];
-  __shared__ float part[4][NT][T][16];
+  __shared__ float red[NW * T];
+  __shared__ float part[NW][NT][T][16];
+  constexpr int NKL = 4 * NW;  // k-lanes
   const int K = a.K, nb = K / 32;
+  const KSlice ks(nb);
   const XStage st = xstage_carve(lds, T, K);
-  if (PRO == PRO_RMS) prologue_rms(st, a.h, a.nw, a.eps, T, K, red);
-  else prologue_q8(st, a.xq, a.xds, T, K);
-  __syncthreads();
-
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-  const int r = lane & 15, kl = wv * 4 + (lane >> 4);  // k-lane 0..15
+  const int r = lane & 15, kl = wv * 4 + (lane >> 4);
   const int tile0 = blockIdx.x * NT;
-  // k-split across grid.y (EPI_RESID only): block range [kb0, kb1)
-  const int nks = gridDim.y;
-  const int per = (nb + nks - 1) / nks;
-  const int kb0 = blockIdx.y * per, kb1 = min(nb, kb0 + per);
+
+  XLoad<T, NW, PRO> xl;
+  xl.load(a, ks);
+
+  const uint4* __restrict__ qs = (const uint4*)a.qs;
+  const unsigned short* __restrict__ dd = (const unsigned short*)a.d;
+  uint4 w[NT][KPL];
+  unsigned dh[NT][KPL];   // fp16 scale bits, zero-extended: 16-bit register halves would serialise the loads
+  // Unconditional loads (clamped block index, scale zeroed past the slice): straight-line code lets
+  // the compiler wait for exactly the loads each use needs instead of draining all of them.
+#pragma unroll
+  for (int i = 0; i < KPL; ++i) {
+    const int b = ks.b0 + kl + NKL * i;
+    const int bc = min(b, ks.b1 - 1);
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      const size_t idx = ((size_t)(tile0 + t) * nb + bc) * 16 + r;
+      w[t][i] = ld_stream16(qs + idx);
+      dh[t][i] = dd[idx];
+    }
+  }
+  // compiler barrier: keep every load above issued here (no sinking into the conditional code below)
+  __asm__ __volatile__("" ::: "memory");
+#pragma unroll
+  for (int i = 0; i < KPL; ++i)
+#pragma unroll
+    for (int t = 0; t < NT; ++t) dh[t][i] = (ks.b0 + kl + NKL * i < ks.b1) ? dh[t][i] : 0u;
+
+  xl.stage(a, ks, st, red, lds + (size_t)T * K + (size_t)T * nb * 8);
+  __syncthreads();
 
   float acc[NT][T];
 #pragma unroll
   for (int t = 0; t < NT; ++t)
 #pragma unroll
     for (int j = 0; j < T; ++j) acc[t][j] = 0.f;
-
-  const uint4* __restrict__ qs = (const uint4*)a.qs;
-  const __half* __restrict__ dd = a.d;
-#pragma unroll 2
-  for (int b = kb0 + kl; b < kb1; b += 16) {
-    uint4 w[NT];
-    float dw[NT];
 #pragma unroll
-    for (int t = 0; t < NT; ++t) {
-      size_t idx = ((size_t)(tile0 + t) * nb + b) * 16 + r;
-      w[t] = ld_stream16(qs + idx);
-      dw[t] = __half2float(dd[idx]);
-    }
+  for (int i = 0; i < KPL; ++i) {
+    const int b = min(ks.b0 + kl + NKL * i, ks.b1 - 1);   // lanes past the slice re-read a valid block, scale 0
+    {
 #pragma unroll
-    for (int j = 0; j < T; ++j) {
-      const int4* xp = (const int4*)(st.q + (size_t)j * K + (size_t)b * 32);
-      int4 xa = xp[0], xb = xp[1];
-      int xv[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
-      float dx = st.d[j * nb + b];
-      int s8 = 8 * st.s[j * nb + b];
+      for (int j = 0; j < T; ++j) {
+        const int4* xp = (const int4*)(st.q + (size_t)j * K + (size_t)b * 32);
+        const int4 xa = xp[0], xb = xp[1];
+        const int xv[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+        const float dx = st.d[j * nb + b];
+        const int s8 = 8 * st.s[j * nb + b];
 #pragma unroll
-      for (int t = 0; t < NT; ++t) {
-        int dot = q4_block_dot(w[t], xv);
-        acc[t][j] = fmaf(dw[t] * dx, (float)(dot - s8), acc[t][j]);
+        for (int t = 0; t < NT; ++t) {
+          const int dot = q4_block_dot(w[t][i], xv);
+          acc[t][j] = fmaf(__half2float(__ushort_as_half((unsigned short)dh[t][i])) * dx, (float)(dot - s8), acc[t][j]);
+        }
       }
     }
   }
-  // reduce the 4 slots of each row (lanes r, r+16, r+32, r+48), then the 4 waves in fixed order
+  // reduce the 4 slots of each row (lanes r, r+16, r+32, r+48), then the NW waves in fixed order
 #pragma unroll
   for (int t = 0; t < NT; ++t)
 #pragma unroll
@@ -293,7 +433,7 @@ __global__ void __launch_bounds__(256) k_gemv(const GemvArgs a) {
       if (lane < 16) part[wv][t][j][r] = v;
     }
   __syncthreads();
-  epilogue<T, NT, EPI>(a, part, tile0);
+  epilogue<NW, T, NT, EPI>(a, part, tile0);
 }
 
 }  // namespace q355
@@ -301,9 +441,11 @@ __global__ void __launch_bounds__(256) k_gemv(const GemvArgs a) {
 namespace q355 {
 
 // ---------------------------------------------------------------------------------------------
-// Embedding: h[j] = dequant(E[tok[j]]) from the tiled Q4_0 planes (tied embedding/head).
+// Embedding: h[j] = dequant(E[tok[j]]) from the tiled Q4_0 planes (tied embedding/head), written as
+// the fixed-point residual stream (exact: d * (q - 8) has at most 15 significant bits).
 __global__ void __launch_bounds__(64) k_embed_q4_0(const uint8_t* __restrict__ qs, const __half* __restrict__ d,
-                                                   int V, int H, const int* __restrict__ tok, float* __restrict__ h) {
+                                                   int V, int H, const int* __restrict__ tok,
+                                                   long long* __restrict__ h) {
   const int j = blockIdx.x, nb = H / 32;
   const int t = tok[j];
   if (t < 0 || t >= V) return;
@@ -313,12 +455,12 @@ __global__ void __launch_bounds__(64) k_embed_q4_0(const uint8_t* __restrict__ q
     const uint4 w = ((const uint4*)qs)[idx];
     const float dw = __half2float(d[idx]);
     const unsigned ws[4] = {w.x, w.y, w.z, w.w};
-    float* out = h + (size_t)j * H + b * 32;
+    long long* out = h + (size_t)j * H + b * 32;
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
       const unsigned byte = (ws[i >> 2] >> (8 * (i & 3))) & 0xFFu;
-      out[i] = dw * (float)((int)(byte & 15u) - 8);
-      out[i + 16] = dw * (float)((int)(byte >> 4) - 8);
+      out[i] = to_fix(dw * (float)((int)(byte & 15u) - 8));
+      out[i + 16] = to_fix(dw * (float)((int)(byte >> 4) - 8));
     }
   }
 }

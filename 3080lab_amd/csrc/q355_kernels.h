@@ -6,11 +6,27 @@
 
 namespace q355 {
 
-enum Prologue { PRO_Q8 = 0, PRO_RMS = 1 };
-enum Epilogue { EPI_STORE = 0, EPI_RESID = 1, EPI_BIAS = 2, EPI_QKV = 3, EPI_SWIGLU_Q8 = 4, EPI_LOGITS = 5 };
+enum Prologue { PRO_Q8 = 0, PRO_RMS = 1, PRO_ATTN = 2, PRO_F32 = 3 };
+enum Epilogue {
+  EPI_STORE = 0,       // y = acc (fp32)
+  EPI_RESID = 1,       // y += acc (fp32, one writer per element: no K split)
+  EPI_BIAS = 2,        // y = acc + bias
+  EPI_QKV = 3,         // + bias, RoPE, fp16 q out, fp16 K/V cache write
+  EPI_SWIGLU = 4,      // rows interleaved (gate, up): y[row / 2] = silu(g) * u (fp32)
+  EPI_LOGITS = 5,      // y = acc and per-workgroup (max, lowest index) partials
+  EPI_RESID_FIX = 6,   // fixed-point residual: yfix += round(acc * 2^32) (int64 atomics; any K split)
+};
 
 constexpr int HD = 128;        // head dim (Qwen2.5-1.5B)
 constexpr int PAGE = 64;       // KV cache page: 64 positions of one KV head, [PAGE][HD] fp16
+constexpr float FIX_SCALE = 4294967296.0f;        // residual stream fixed point: value * 2^32 as int64
+constexpr double FIX_INV = 1.0 / 4294967296.0;
+
+// The residual stream h is kept as int64 fixed point (2^-32 resolution, |h| < 2^31). Split-K
+// producers add their partial sums with integer atomics, which are associative, so the stream is
+// bitwise independent of the order in which workgroups finish.
+__device__ __forceinline__ long long to_fix(float v) { return __float2ll_rn(v * FIX_SCALE); }
+__device__ __forceinline__ float from_fix(long long v) { return (float)((double)v * FIX_INV); }
 
 // Everything a GEMV-family launch may need; unused fields are null/zero.
 struct GemvArgs {
@@ -21,11 +37,18 @@ struct GemvArgs {
   const int8_t* xq;            // [T][K]
   const half2* xds;            // [T][K/32]
   // PRO_RMS input
-  const float* h;              // [T][K] fp32 residual stream
+  const long long* hfix;       // [T][K] residual stream, int64 fixed point
   const float* nw;             // [K] RMSNorm weight
   float eps;
-  // STORE / RESID / BIAS / LOGITS output
-  float* y;                    // [T][N]
+  // PRO_F32 input (quantized to Q8_1 in the prologue)
+  const float* xf;             // [T][K]
+  // PRO_ATTN input: split-K attention partials [T][nh][attn_max_chunks][HD + 2], merged and quantized
+  // in the prologue (K == nh * HD); the token positions come from `pos`
+  const float* attn_part;
+  int attn_max_chunks;
+  // STORE / RESID / BIAS / SWIGLU / LOGITS output
+  float* y;                    // [T][N] ([T][N/2] for SWIGLU)
+  long long* yfix;             // RESID_FIX: [T][N] fixed-point residual stream
   const float* aux;            // bias [N] (BIAS, QKV: bias in the permuted row order)
   // QKV epilogue: RoPE on q/k (rows of each head interleaved (d, d+64)), fp16 q out, K/V cache write
   const float* rope_cos;       // [maxlen][HD/2]
@@ -38,9 +61,6 @@ struct GemvArgs {
   __half* vcache;
   __half* qout;                // [T][nh*HD]
   int nh, nkv;
-  // SWIGLU_Q8 output (rows interleaved gate, up): Q8_1 of silu(g) * u, [T][N/2]
-  int8_t* oq;
-  half2* ods;
   // LOGITS: per-workgroup (max, index) partials [T][gridDim.x]
   float* pmax;
   int* pidx;
@@ -56,13 +76,12 @@ struct AttnArgs {
   int nh, nkv, max_chunks;     // chunk = one page
   float scale;
   float* part;                 // [T][nh][max_chunks][HD + 2] partial (o, m, l)
-  unsigned* counter;           // [T][nkv] arrival counters (self-resetting)
-  int8_t* oq;                  // [T][nh*HD] Q8_1 output for the O projection
+  int8_t* oq;                  // [T][nh*HD] Q8_1 output for the O projection (standalone merge)
   half2* ods;                  // [T][nh*HD/32]
   float* o32;                  // optional fp32 output [T][nh*HD] (tests), may be null
 };
 
-template <int T, int NT, int PRO, int EPI>
+template <int T, int NT, int NW, int KPL, int PRO, int EPI>
 __global__ void k_gemv(const GemvArgs a);
 
 }  // namespace q355

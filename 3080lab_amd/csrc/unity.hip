@@ -1,4 +1,3 @@
 // Single translation unit of libqwen355.so (the kernel templates are instantiated by the C ABI layer).
 #include "gemv.hip"
-#include "attn.hip"
 #include "capi.hip"

@@ -20,16 +20,18 @@ _P = c_void_p
 _SIGS = {
     "q355_quant_q8_1": [_P, _P, _P, c_int, c_int, _P],
     "q355_rmsnorm_q8_1": [_P, _P, _P, _P, c_int, c_int, c_float, _P],
-    "q355_gemv_q4_0_q8_1": [_P, _P, c_int, c_int, _P, _P, c_int, _P, _P, c_int, c_int, _P],
+    "q355_gemv_q4_0_q8_1": [_P, _P, c_int, c_int, _P, _P, c_int, _P, _P, c_int, _P],
     "q355_gemv_blockdots": [_P, c_int, c_int, _P, c_int, _P, _P],
     "q355_qkv_rope_kv": [_P, _P, c_int, _P, _P, c_float, _P, _P, _P, _P, _P, c_int, c_int, _P, _P, _P,
                          c_int, c_int, c_int, _P],
-    "q355_ffn_gate_up": [_P, _P, c_int, c_int, _P, _P, c_float, _P, _P, c_int, _P],
+    "q355_ffn_gate_up": [_P, _P, c_int, c_int, _P, _P, c_float, _P, c_int, _P],
+    "q355_ffn_down": [_P, _P, c_int, c_int, _P, _P, c_int, _P],
     "q355_head_logits": [_P, _P, c_int, c_int, _P, _P, c_float, _P, _P, _P, c_int, _P],
     "q355_head_nparts": [c_int],
     "q355_finish": [_P, _P, c_int, _P, _P, c_int, _P],
     "q355_embed_q4_0": [_P, _P, c_int, c_int, _P, _P, c_int, _P],
-    "q355_attn_decode": [_P, _P, _P, _P, _P, c_int, c_int, c_int, c_int, c_float, _P, _P, _P, _P, _P, c_int, _P],
+    "q355_attn_decode": [_P, _P, _P, _P, _P, c_int, c_int, c_int, c_int, c_float, _P, _P, _P, _P, c_int, _P],
+    "q355_attn_o_resid": [_P, _P, c_int, _P, c_int, _P, c_int, _P, c_int, _P],
 }
 # entry points returning something other than an int status
 _VALUE_FUNCS = {"q355_head_nparts"}

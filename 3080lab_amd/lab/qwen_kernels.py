@@ -24,7 +24,8 @@ def gemv_source(S_: int = 1, epi: str = "store", quant: str = "q8_1", G: int = 1
     """Q4_0 x Q8_1 GEMV (reference: split-K Q4_0 x bf16 GEMV, lab/qwen_kernels.py:14-113).
     epi store/logits/resid/bias/biasf -> q355_gemv_q4_0_q8_1 with the matching epi code;
     epi swiglu -> q355_ffn_gate_up (fused RMSNorm prologue + SwiGLU + Q8_1 epilogue);
-    epi biasf_kv -> q355_qkv_rope_kv. S_ (split-K) maps to the `split` argument of resid GEMVs."""
+    epi biasf_kv -> q355_qkv_rope_kv. S_ (the reference's split-K warp count) has no counterpart: the
+    library picks the K split (16 or 32 k-lanes per workgroup) from K."""
     if quant != "q8_1":
         raise ValueError(f"quant={quant!r}: this build's GEMV consumes Q8_1 activations")
     if epi == "swiglu":
@@ -33,7 +34,7 @@ def gemv_source(S_: int = 1, epi: str = "store", quant: str = "q8_1", G: int = 1
         return KernelSpec("q355_qkv_rope_kv")
     if epi not in _EPI_CODE:
         raise ValueError(f"epilogue {epi!r} not in {EPILOGUES}")
-    return KernelSpec("q355_gemv_q4_0_q8_1", {"epi": _EPI_CODE[epi], "split": S_ if epi == "resid" else 1})
+    return KernelSpec("q355_gemv_q4_0_q8_1", {"epi": _EPI_CODE[epi]})
 
 
 # Single kernels of the reference, by name

@@ -4,10 +4,12 @@ The decode step is the reference's FusedQwen.step (scripts/qwen_fused.py:113-145
 scripts/qwen_gguf.py:63-144) re-cut for gfx950 into 5 fused launches per layer:
 
   qkv_rope_kv   RMSNorm(ln1) + Q8_1 + QKV GEMV + bias + RoPE + fp16 K/V cache write   (fused prologue/epilogue)
-  attn_decode   split-K GQA attention over 64-position pages -> Q8_1 input of O
-  gemv resid    O GEMV, h += (fp32 residual stream)
-  ffn_gate_up   RMSNorm(ln2) + Q8_1 + gate_up GEMV + SwiGLU + Q8_1 of the result
-  gemv resid    down GEMV, h += ...
+  attn_decode   split-K GQA attention over 64-position pages -> per-chunk partials
+  attn_o_resid  merge of the partials + Q8_1 + O GEMV (3 K slices), h += ...
+  ffn_gate_up   RMSNorm(ln2) + Q8_1 + gate_up GEMV + SwiGLU -> m (fp32)
+  ffn_down      Q8_1(m) + down GEMV (4 K slices), h += ...
+The residual stream h is int64 fixed point (value * 2^32): the K-sliced projections add into it with
+integer atomics, so results do not depend on workgroup timing.
 then head_logits (final RMSNorm + tied Q4_0 head + per-workgroup argmax partials) and finish
 (argmax, tok <- idx, pos += 1). The whole step is captured once in a torch.cuda.CUDAGraph (a hipGraph)
 and replayed per token, as run_fused does (scripts/qwen_fused.py:148-180).
@@ -163,21 +165,28 @@ class Decoder:
         # sequence j owns pages [j*max_chunks, (j+1)*max_chunks) (identity block table; paged layout)
         self.block_table = torch.arange(n_pages, dtype=torch.int32, device=dev).reshape(T, self.max_chunks)
         H = cfg.H
-        self.h = torch.zeros(T, H, dtype=torch.float32, device=dev)
+        self.h = torch.zeros(T, H, dtype=torch.int64, device=dev)       # fixed point, value * 2^32
         self.q = torch.zeros(T, cfg.NH * cfg.HD, dtype=torch.float16, device=dev)
-        self.aq = torch.zeros(T, cfg.NH * cfg.HD, dtype=torch.int8, device=dev)
-        self.ads = torch.zeros(T, cfg.NH * cfg.HD // 32, 2, dtype=torch.float16, device=dev)
-        self.mq = torch.zeros(T, cfg.FFN, dtype=torch.int8, device=dev)
-        self.mds = torch.zeros(T, cfg.FFN // 32, 2, dtype=torch.float16, device=dev)
+        self.mlp = torch.zeros(T, cfg.FFN, dtype=torch.float32, device=dev)
         self.logits = torch.zeros(T, cfg.V, dtype=torch.float32, device=dev)
         self.nparts = call("q355_head_nparts", cfg.V)
         self.pmax = torch.zeros(T, self.nparts, dtype=torch.float32, device=dev)
         self.pidx = torch.zeros(T, self.nparts, dtype=torch.int32, device=dev)
         self.part = torch.zeros(T, cfg.NH, self.max_chunks, cfg.HD + 2, dtype=torch.float32, device=dev)
-        self.counter = torch.zeros(T, cfg.NKV, dtype=torch.int32, device=dev)
         self.tok = torch.zeros(T, dtype=torch.int32, device=dev)
         self.pos = torch.zeros(T, dtype=torch.int32, device=dev)
         self.scale = 1.0 / math.sqrt(cfg.HD)
+
+    # -- residual stream as fp32 (host-side views for tests and debugging) --
+    def h_f32(self):
+        import torch
+        return (self.h.to(torch.float64) * 2.0 ** -32).to(torch.float32)
+
+    def set_h(self, h):
+        """Set the residual stream from fp32 values [T, H] (numpy or torch)."""
+        import torch
+        t = torch.as_tensor(np.asarray(h, np.float32)).to(self.h.device)
+        self.h.copy_(torch.round(t.to(torch.float64) * 2.0 ** 32).to(torch.int64))
 
     # -- per-layer ops (each is one library call) --
     def layer(self, i: int):
@@ -188,14 +197,12 @@ class Decoder:
              ptr(m.cos), ptr(m.sin), ptr(self.pos), ptr(self.block_table), self.max_chunks, 1,
              ptr(self.kc[i]), ptr(self.vc[i]), ptr(self.q), c.NH, c.NKV, T)
         call("q355_attn_decode", ptr(self.q), ptr(self.kc[i]), ptr(self.vc[i]), ptr(self.pos), ptr(self.block_table),
-             self.max_chunks, c.NH, c.NKV, self.max_chunks, self.scale, ptr(self.part), ptr(self.counter),
-             ptr(self.aq), ptr(self.ads), None, T)
-        call("q355_gemv_q4_0_q8_1", ptr(o.qs), ptr(o.d), o.N, o.K, ptr(self.aq), ptr(self.ads), T, ptr(self.h),
-             None, 1, 1)
+             self.max_chunks, c.NH, c.NKV, self.max_chunks, self.scale, ptr(self.part), None, None, None, T)
+        call("q355_attn_o_resid", ptr(o.qs), ptr(o.d), o.N, ptr(self.part), self.max_chunks, ptr(self.pos), c.NH,
+             ptr(self.h), T)
         call("q355_ffn_gate_up", ptr(gu.qs), ptr(gu.d), gu.N, gu.K, ptr(self.h), ptr(L["ln2"]), c.eps,
-             ptr(self.mq), ptr(self.mds), T)
-        call("q355_gemv_q4_0_q8_1", ptr(down.qs), ptr(down.d), down.N, down.K, ptr(self.mq), ptr(self.mds), T,
-             ptr(self.h), None, 1, 1)
+             ptr(self.mlp), T)
+        call("q355_ffn_down", ptr(down.qs), ptr(down.d), down.N, down.K, ptr(self.mlp), ptr(self.h), T)
 
     def embed(self):
         e = self.m.embed

@@ -12,6 +12,8 @@
  *   Q8_1 activations [T, K]: xq int8 [T][K], xds half2 [T][K/32] = (d, s = d * sum q).
  *   KV cache (per layer): fp16 [n_pages][nkv][64][128]; block_table int32 [n_seq][bt_stride] page ids.
  *   RoPE tables: fp32 [maxlen][64] (cos, sin). Token positions and ids are int32.
+ *   Residual stream h [T][H]: int64 fixed point, value = h * 2^-32 (|h| < 2^31). K-split projections add
+ *   into it with integer atomics, so every result is bitwise independent of workgroup timing.
  *
  * Each declaration names the reference interface it replaces (paths relative to the reference
  * repository lblommesteyn/3080lab).
@@ -45,36 +47,40 @@ int q355_rmsnorm_q8_1(const float* h, const float* w, int8_t* xq, void* xds, int
                       void* stream);
 
 /* Q4_0 x Q8_1 GEMV for T = 1..4 tokens: y[T][N] (epi 0: =, 1: +=, 2: = acc + bias[N]).
- * split > 1 (epi 1 only) splits K over `split` workgroups that add with fp32 atomics (order not fixed).
+ * Deterministic: fixed reduction order, one writer per output.
  * Replaces gemv_source epilogues store / bias / biasf / resid / logits (lab/qwen_kernels.py:14-113).
- * N % 16 == 0, K % 32 == 0, K <= 8960. */
+ * N % 16 == 0, K % 32 == 0, K <= 9216. */
 int q355_gemv_q4_0_q8_1(const uint8_t* qs, const void* d, int N, int K, const int8_t* xq, const void* xds,
-                        int T, float* y, const float* bias, int epi, int split, void* stream);
+                        int T, float* y, const float* bias, int epi, void* stream);
 
 /* Debug: every per-block int32 dot out[T][N][K/32] = sum_i q_w,i (0..15) * q_x,i (bit-exact check).
  * Replaces the per-block timing/debug arguments of gemv_source (lab/qwen_kernels.py:46-53). */
 int q355_gemv_blockdots(const uint8_t* qs, int N, int K, const int8_t* xq, int T, int32_t* out, void* stream);
 
 /* Fused ln1 RMSNorm + Q8_1 + QKV GEMV + bias + RoPE(q, k) + fp16 K/V cache write + fp16 q out.
- * Rows of q and k heads are stored interleaved (d, d + 64) and the bias in the same order.
- * Replaces RMSNORM_F32W_1P + gemv_source('biasf') + the RoPE/KV-write head of ATTN4
- * (lab/qwen_kernels.py:33, 517-546) and gemm 'biasf_kv' (lab/qwen_batched.py:1316-1362).
- * Token j (j < T <= 4) is at position pos[j] of sequence j * seq_stride. */
-int q355_qkv_rope_kv(const uint8_t* qs, const void* d, int K, const float* h, const float* nw, float eps,
+ * h is the fixed-point residual stream. Rows of q and k heads are stored interleaved (d, d + 64) and the
+ * bias in the same order. Replaces RMSNORM_F32W_1P + gemv_source('biasf') + the RoPE/KV-write head of
+ * ATTN4 (lab/qwen_kernels.py:33, 517-546) and gemm 'biasf_kv' (lab/qwen_batched.py:1316-1362).
+ * Token j (j < T <= 4) is at position pos[j] of sequence j * seq_stride. K <= 1536. */
+int q355_qkv_rope_kv(const uint8_t* qs, const void* d, int K, const int64_t* h, const float* nw, float eps,
                      const float* bias, const float* rope_cos, const float* rope_sin, const int32_t* pos,
                      const int32_t* block_table, int bt_stride, int seq_stride, void* kcache, void* vcache,
                      void* qout, int nh, int nkv, int T, void* stream);
 
-/* Fused ln2 RMSNorm + Q8_1 + gate_up GEMV (rows interleaved gate, up) + SwiGLU + Q8_1 of the result.
- * N2 = 2 * FFN rows; output mq int8 [T][N2/2], mds half2 [T][N2/64].
- * Replaces gemv_source('swiglu') (lab/qwen_kernels.py:21-28) and 'swiglu_q8' (lab/qwen_batched.py:1363-1396). */
-int q355_ffn_gate_up(const uint8_t* qs, const void* d, int N2, int K, const float* h, const float* nw, float eps,
-                     int8_t* mq, void* mds, int T, void* stream);
+/* Fused ln2 RMSNorm + Q8_1 + gate_up GEMV (rows interleaved gate, up) + SwiGLU: m fp32 [T][N2/2].
+ * Replaces gemv_source('swiglu') (lab/qwen_kernels.py:21-28). K <= 1536. */
+int q355_ffn_gate_up(const uint8_t* qs, const void* d, int N2, int K, const int64_t* h, const float* nw, float eps,
+                     float* m, int T, void* stream);
+
+/* Fused Q8_1 of m + down GEMV + residual: h[T][N] += Wd . Q8_1(m) (4 K slices, fixed-point atomics).
+ * Replaces swiglu_q8's quantizer (lab/qwen_batched.py:1363-1396) + gemv_source('resid') for down (:34).
+ * K % 128 == 0, K <= 9216. */
+int q355_ffn_down(const uint8_t* qs, const void* d, int N, int K, const float* m, int64_t* h, int T, void* stream);
 
 /* Final RMSNorm + Q8_1 + tied Q4_0 head: logits fp32 [T][V] and per-workgroup (max, lowest index)
  * partials pmax/pidx [T][q355_head_nparts(V)]. Replaces gemv_q6_source / 'logits'
  * (lab/qwen_kernels.py:608-678, 36) and the first stage of FINISH_MB (250-270). */
-int q355_head_logits(const uint8_t* qs, const void* d, int V, int K, const float* h, const float* nw, float eps,
+int q355_head_logits(const uint8_t* qs, const void* d, int V, int K, const int64_t* h, const float* nw, float eps,
                      float* logits, float* pmax, int32_t* pidx, int T, void* stream);
 int q355_head_nparts(int V);
 
@@ -83,19 +89,27 @@ int q355_head_nparts(int V);
 int q355_finish(const float* pmax, const int32_t* pidx, int nparts, int32_t* tok, int32_t* pos, int T,
                 void* stream);
 
-/* Embedding lookup from the tied Q4_0 table: h[j] = dequant(E[tok[j]]).
+/* Embedding lookup from the tied Q4_0 table into the fixed-point residual stream: h[j] = dequant(E[tok[j]]).
  * Replaces EMBED_F32 (lab/qwen_kernels.py:284-290). */
-int q355_embed_q4_0(const uint8_t* qs, const void* d, int V, int H, const int32_t* tok, float* h, int T,
+int q355_embed_q4_0(const uint8_t* qs, const void* d, int V, int H, const int32_t* tok, int64_t* h, int T,
                     void* stream);
 
 /* Decode GQA attention, split-K over 64-position pages: token j attends to positions 0..pos[j] of its
- * sequence (block_table row j). Output: Q8_1 oq/ods [T][nh*128] for the O projection and optionally
- * fp32 o32 (may be NULL). Scratch: part fp32 [T][nh][max_chunks][130], counter uint32 [T][nkv]
- * (zero before the first call; the kernel leaves it zero). max_chunks >= (max pos)/64 + 1.
+ * sequence (block_table row j). Writes the unnormalised partials part fp32 [T][nh][max_chunks][130]
+ * (o[128], running max, sum) of every live chunk; max_chunks >= (max pos)/64 + 1, <= 64.
+ * If oq/ods are given it also merges them (second launch): Q8_1 oq int8 [T][nh*128], ods half2
+ * [T][nh*4], and optionally fp32 o32 [T][nh*128]. GQA group nh/nkv in {4, 6, 8}.
  * Replaces ATTN2 / ATTN4 (lab/qwen_kernels.py:358-442, 517-605). */
 int q355_attn_decode(const void* q, const void* kcache, const void* vcache, const int32_t* pos,
                      const int32_t* block_table, int bt_stride, int nh, int nkv, int max_chunks, float scale,
-                     float* part, uint32_t* counter, int8_t* oq, void* ods, float* o32, int T, void* stream);
+                     float* part, int8_t* oq, void* ods, float* o32, int T, void* stream);
+
+/* Fused attention merge + Q8_1 + O-projection GEMV + residual: h[T][N] += Wo . Q8_1(merge(part))
+ * (3 K slices of nh/3 heads, fixed-point atomics). part / max_chunks / pos as written by
+ * q355_attn_decode; nh % 3 == 0, K = nh * 128 <= 1536.
+ * Replaces the ATTN2 last-block combine (lab/qwen_kernels.py:424-440) + gemv_source('resid') for o (:34). */
+int q355_attn_o_resid(const uint8_t* qs, const void* d, int N, const float* part, int max_chunks,
+                      const int32_t* pos, int nh, int64_t* h, int T, void* stream);
 
 #ifdef __cplusplus
 }
