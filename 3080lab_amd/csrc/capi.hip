@@ -16,6 +16,8 @@ __global__ void k_blockdots(const uint8_t*, int, int, const int8_t*, int, int*);
 template <int G>
 __global__ void k_attn_decode(const AttnArgs);
 __global__ void k_attn_merge(const AttnArgs);
+__global__ void k_rmsnorm_fix_q8_1(const long long*, const float*, int8_t*, half2*, int, float);
+__global__ void k_qkv_finish(GemvArgs, long long*);
 }  // namespace q355
 
 using namespace q355;
@@ -246,4 +248,93 @@ extern "C" int q355_attn_o_resid(const uint8_t* qs, const void* d, int N, const 
   a.attn_part = part; a.attn_max_chunks = max_chunks; a.pos = pos; a.nh = nh; a.yfix = (long long*)h;
   // 3 K slices of nh/3 heads (16 blocks for nh = 12): 16 k-lanes x 1 block per lane
   return launch_gemv<PRO_ATTN, EPI_RESID_FIX, 1, 4, 1>(a, 3, (hipStream_t)stream);
+}
+
+// ------------------------------------------------------------------------------------------------
+// MFMA path (batched decode, prefill)
+
+extern "C" int q355_rmsnorm_fix_q8_1(const int64_t* h, const float* w, int8_t* xq, void* xds, int T, int H, float eps,
+                                     void* stream) {
+  REQUIRE(h && w && xq && xds, "rmsnorm_fix_q8_1: null pointer");
+  REQUIRE(T > 0 && H > 0 && H % 32 == 0 && H <= 2048, "rmsnorm_fix_q8_1: T=%d H=%d (H %% 32 == 0, <= 2048)", T, H);
+  hipLaunchKernelGGL(k_rmsnorm_fix_q8_1, dim3(T), dim3(256), 0, (hipStream_t)stream, (const long long*)h, w, xq,
+                     (half2*)xds, H, eps);
+  return launched("rmsnorm_fix_q8_1");
+}
+
+template <int TG, int EPI>
+static int launch_mmq(GemvArgs a, int KS, hipStream_t s) {
+  constexpr int NT = 4, NW = 4, TT = 16 * TG;
+  constexpr size_t LDS_MAX = 65536;
+  const int nb = a.K / 32, per = (nb + KS - 1) / KS;
+  // activation chunk: TT rows of (32 B per block + 16 B pad) + 8 B (d, sum) per block, within 64 KB
+  const int ch_max = (int)((LDS_MAX - (size_t)TT * 16) / ((size_t)TT * 40));
+  const int nchunks = (per + ch_max - 1) / ch_max;
+  a.mmq_chunk = (per + nchunks - 1) / nchunks;
+  const size_t xb = (size_t)TT * (a.mmq_chunk * 32 + 16) + (size_t)TT * a.mmq_chunk * 8;
+  const size_t pb = (size_t)NW * NT * TT * 16 * 4;
+  const size_t lds = xb > pb ? xb : pb;
+  if (lds > LDS_MAX) return fail(Q355_EINVAL, "mmq: %zu B of LDS for %d tokens", lds, TT);
+  const dim3 grid(a.N / (16 * NT), KS, (a.T + TT - 1) / TT);
+  hipLaunchKernelGGL((k_mmq<TG, NT, NW, EPI>), grid, dim3(NW * 64), lds, s, a);
+  return launched("mmq");
+}
+
+template <int EPI>
+static int launch_mmq_tg(const GemvArgs& a, int KS, hipStream_t s) {
+  return a.T <= 16 ? launch_mmq<1, EPI>(a, KS, s) : launch_mmq<2, EPI>(a, KS, s);
+}
+
+extern "C" int q355_mmq_q4_0_q8_1(const uint8_t* qs, const void* d, int N, int K, const int8_t* xq, const void* xds,
+                                  int T, int epi, float* y, int64_t* yfix, int8_t* oq, void* ods, float* pmax,
+                                  int32_t* pidx, void* stream) {
+  if (int e = check_mat("mmq_q4_0_q8_1", qs, d, N, K)) return e;
+  REQUIRE(xq && xds, "mmq_q4_0_q8_1: null activation pointer");
+  REQUIRE(T >= 1 && T <= 65535 * 32, "mmq_q4_0_q8_1: T=%d", T);
+  REQUIRE(N % 64 == 0, "mmq_q4_0_q8_1: N=%d must be a multiple of 64", N);
+  GemvArgs a = {};
+  a.qs = qs; a.d = (const __half*)d; a.N = N; a.K = K; a.T = T; a.xq = xq; a.xds = (const half2*)xds;
+  hipStream_t s = (hipStream_t)stream;
+  const int nb = K / 32, groups = N / 64;
+  switch (epi) {
+    case 0:
+      REQUIRE(y, "mmq_q4_0_q8_1: store needs y");
+      a.y = y;
+      return launch_mmq_tg<EPI_STORE>(a, 1, s);
+    case 6: {
+      REQUIRE(yfix, "mmq_q4_0_q8_1: resid_fix needs yfix");
+      a.yfix = (long long*)yfix;
+      int KS = 384 / groups;
+      KS = KS < 1 ? 1 : (KS > nb / 4 ? nb / 4 : KS);
+      if (KS < 1) KS = 1;
+      return launch_mmq_tg<EPI_RESID_FIX>(a, KS, s);
+    }
+    case 7:
+      REQUIRE(oq && ods, "mmq_q4_0_q8_1: swiglu_q8 needs oq/ods");
+      a.oq = oq; a.ods = (half2*)ods;
+      return launch_mmq_tg<EPI_SWIGLU_Q8>(a, 1, s);
+    case 5:
+      REQUIRE(y && pmax && pidx, "mmq_q4_0_q8_1: logits needs y, pmax, pidx");
+      a.y = y; a.pmax = pmax; a.pidx = pidx;
+      return launch_mmq_tg<EPI_LOGITS>(a, 1, s);
+    default:
+      return fail(Q355_EINVAL, "mmq_q4_0_q8_1: epi=%d (0 store, 5 logits, 6 resid_fix, 7 swiglu_q8)", epi);
+  }
+}
+
+extern "C" int q355_mmq_nparts(int N) { return N / 64; }
+
+extern "C" int q355_qkv_finish(int64_t* acc, const float* bias, const float* rope_cos, const float* rope_sin,
+                               const int32_t* pos, const int32_t* block_table, int bt_stride, int seq_stride,
+                               void* kcache, void* vcache, void* qout, int nh, int nkv, int T, void* stream) {
+  REQUIRE(acc && bias && rope_cos && rope_sin && pos && block_table && kcache && vcache && qout,
+          "qkv_finish: null pointer");
+  REQUIRE(nh > 0 && nkv > 0 && T > 0 && bt_stride > 0 && (seq_stride == 0 || seq_stride == 1),
+          "qkv_finish: nh=%d nkv=%d T=%d bt_stride=%d seq_stride=%d", nh, nkv, T, bt_stride, seq_stride);
+  GemvArgs a = {};
+  a.aux = bias; a.rope_cos = rope_cos; a.rope_sin = rope_sin; a.pos = pos; a.block_table = block_table;
+  a.bt_stride = bt_stride; a.seq_stride = seq_stride;
+  a.kcache = (__half*)kcache; a.vcache = (__half*)vcache; a.qout = (__half*)qout; a.nh = nh; a.nkv = nkv;
+  hipLaunchKernelGGL(k_qkv_finish, dim3(T), dim3(256), 0, (hipStream_t)stream, a, (long long*)acc);
+  return launched("qkv_finish");
 }

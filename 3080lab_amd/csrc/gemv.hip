@@ -302,6 +302,20 @@ __device__ __forceinline__ void epilogue(const GemvArgs& a, float (&part)[NW][NT
     }
     return;
   }
+  if (EPI == EPI_SWIGLU_Q8) {
+    // NT == 4: 64 interleaved rows (g0, u0, g1, u1, ...) -> 32 outputs = one Q8_1 block per token
+    for (int e = threadIdx.x; e < 32 * T; e += blockDim.x) {   // 32-lane groups: one token each
+      const int j = e >> 5, k = e & 31;
+      if (j >= a.T) break;                                      // uniform per 32-lane group
+      const int rg = 2 * k, ru = 2 * k + 1;
+      const float g = row_value<NW, T, NT>(part, rg >> 4, j, rg & 15);
+      const float u = row_value<NW, T, NT>(part, ru >> 4, j, ru & 15);
+      const int Nout = N / 2;
+      const int q = q8_1_lane32(silu_mul(g, u), a.ods + (size_t)j * (Nout / 32) + blockIdx.x, k == 0);
+      a.oq[(size_t)j * Nout + blockIdx.x * 32 + k] = (int8_t)q;
+    }
+    return;
+  }
   if (EPI == EPI_SWIGLU) {
     // rows interleaved (g0, u0, g1, u1, ...): one thread per output pair
     for (int e = threadIdx.x; e < NT * T * 8; e += blockDim.x) {
@@ -329,7 +343,7 @@ __device__ __forceinline__ void epilogue(const GemvArgs& a, float (&part)[NW][NT
       v += a.aux[row];
       const int nq = a.nh * HD, nk = a.nkv * HD;
       const int pos = a.pos[j];
-      const int seq = j * a.seq_stride;
+      const int seq = (a.tok_base + j) * a.seq_stride;
       const int pg = a.block_table[(size_t)seq * a.bt_stride + pos / PAGE];
       if (row < nq + nk) {
         const float v2 = row_value<NW, T, NT>(part, t, j, r ^ 1) + a.aux[row ^ 1];
@@ -494,6 +508,77 @@ __global__ void __launch_bounds__(256) k_finish(const float* __restrict__ pmax, 
       if (bv[w] > v || (bv[w] == v && bi[w] < idx)) { v = bv[w]; idx = bi[w]; }
     tok[j] = idx;
     pos[j] += 1;
+  }
+}
+
+// RMSNorm of the fixed-point residual stream -> Q8_1, one token per workgroup (batched / prefill path).
+__global__ void __launch_bounds__(256) k_rmsnorm_fix_q8_1(const long long* __restrict__ h, const float* __restrict__ w,
+                                                          int8_t* __restrict__ xq, half2* __restrict__ xds, int H,
+                                                          float eps) {
+  __shared__ float red[4];
+  const int tok = blockIdx.x;
+  const int g = threadIdx.x;                       // 8 consecutive values per thread, H / 8 <= 256
+  const bool act = g < H / 8;
+  float x[8];
+  float ss = 0.f;
+#pragma unroll
+  for (int u = 0; u < 8; ++u) {
+    x[u] = act ? from_fix(h[(size_t)tok * H + 8 * g + u]) : 0.f;
+    ss = fmaf(x[u], x[u], ss);
+  }
+  ss = wave_sum_fast(ss);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+  __syncthreads();
+  const float r = 1.0f / sqrtf((red[0] + red[1] + red[2] + red[3]) / (float)H + eps);
+  if (act) {
+    const float4 w0 = ((const float4*)w)[2 * g], w1 = ((const float4*)w)[2 * g + 1];
+    const float wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+#pragma unroll
+    for (int u = 0; u < 8; ++u) x[u] = x[u] * r * wv[u];
+  }
+  float df;
+  int sq;
+  const uint2 pk = q8_1_x8(x, df, sq);              // H / 8 % 4 == 0: quads stay whole
+  if (act) {
+    *(uint2*)(xq + (size_t)tok * H + 8 * g) = pk;
+    if ((g & 3) == 0) xds[(size_t)tok * (H / 32) + (g >> 2)] = __halves2half2(__float2half_rn(df), __float2half_rn(df * (float)sq));
+  }
+}
+
+// QKV finish for the MFMA path: the K-sliced QKV product accumulated in int64 fixed point [T][nqkv]
+// (device row order: q/k heads pair-interleaved) -> + bias, RoPE, fp16 q out, fp16 K/V cache write;
+// the accumulator is cleared for the next use. One workgroup per token, one thread per row pair.
+__global__ void __launch_bounds__(256) k_qkv_finish(GemvArgs a, long long* __restrict__ acc) {
+  const int j = blockIdx.x;
+  const int nq = a.nh * HD, nk = a.nkv * HD, N = nq + nk + nk;
+  const int pos = a.pos[j];
+  const int seq = j * a.seq_stride;
+  const int pg = a.block_table[(size_t)seq * a.bt_stride + pos / PAGE];
+  for (int p = threadIdx.x; p < N / 2; p += blockDim.x) {
+    const int row = 2 * p;
+    long long* ap = acc + (size_t)j * N + row;
+    const float v0 = from_fix(ap[0]) + a.aux[row], v1 = from_fix(ap[1]) + a.aux[row + 1];
+    ap[0] = 0;
+    ap[1] = 0;
+    if (row < nq + nk) {
+      const int i = (row % HD) >> 1;               // pair (dim i, dim i + 64)
+      const float c = a.rope_cos[(size_t)pos * (HD / 2) + i], s = a.rope_sin[(size_t)pos * (HD / 2) + i];
+      const __half lo = __float2half_rn(v0 * c - v1 * s), hi = __float2half_rn(v1 * c + v0 * s);
+      if (row < nq) {
+        __half* q = a.qout + (size_t)j * nq + (row / HD) * HD;
+        q[i] = lo;
+        q[i + HD / 2] = hi;
+      } else {
+        __half* k = a.kcache + (((size_t)pg * a.nkv + (row - nq) / HD) * PAGE + pos % PAGE) * HD;
+        k[i] = lo;
+        k[i + HD / 2] = hi;
+      }
+    } else {
+      const int rv = row - nq - nk;
+      __half* v = a.vcache + (((size_t)pg * a.nkv + rv / HD) * PAGE + pos % PAGE) * HD + rv % HD;
+      v[0] = __float2half_rn(v0);
+      v[1] = __float2half_rn(v1);
+    }
   }
 }
 

@@ -15,6 +15,7 @@ enum Epilogue {
   EPI_SWIGLU = 4,      // rows interleaved (gate, up): y[row / 2] = silu(g) * u (fp32)
   EPI_LOGITS = 5,      // y = acc and per-workgroup (max, lowest index) partials
   EPI_RESID_FIX = 6,   // fixed-point residual: yfix += round(acc * 2^32) (int64 atomics; any K split)
+  EPI_SWIGLU_Q8 = 7,   // as SWIGLU, quantized to Q8_1 (oq, ods): NT == 4 (64 rows -> one 32-output block)
 };
 
 constexpr int HD = 128;        // head dim (Qwen2.5-1.5B)
@@ -56,11 +57,16 @@ struct GemvArgs {
   const int* pos;              // [T] position of each token
   const int* block_table;      // [n_seq][bt_stride] page ids
   int bt_stride;
-  int seq_stride;              // token j belongs to sequence j * seq_stride (1: batched decode, 0: one sequence)
+  int seq_stride;              // token j belongs to sequence (tok_base + j) * seq_stride (1: batched, 0: one sequence)
+  int tok_base;                // index of token 0 of this launch's token group (MFMA kernels offset per group)
+  int mmq_chunk;               // MFMA kernels: K blocks of activations staged in LDS at a time
   __half* kcache;              // [n_pages][nkv][PAGE][HD]
   __half* vcache;
   __half* qout;                // [T][nh*HD]
   int nh, nkv;
+  // SWIGLU_Q8 output: Q8_1 of silu(g) * u, [T][N/2] and [T][N/64]
+  int8_t* oq;
+  half2* ods;
   // LOGITS: per-workgroup (max, index) partials [T][gridDim.x]
   float* pmax;
   int* pidx;
@@ -83,5 +89,7 @@ struct AttnArgs {
 
 template <int T, int NT, int NW, int KPL, int PRO, int EPI>
 __global__ void k_gemv(const GemvArgs a);
+template <int TG, int NT, int NW, int EPI>
+__global__ void k_mmq(const GemvArgs a);
 
 }  // namespace q355

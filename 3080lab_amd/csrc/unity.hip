@@ -1,3 +1,4 @@
 // Single translation unit of libqwen355.so (the kernel templates are instantiated by the C ABI layer).
 #include "gemv.hip"
+#include "mmq.hip"
 #include "capi.hip"

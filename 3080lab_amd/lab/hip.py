@@ -32,9 +32,13 @@ _SIGS = {
     "q355_embed_q4_0": [_P, _P, c_int, c_int, _P, _P, c_int, _P],
     "q355_attn_decode": [_P, _P, _P, _P, _P, c_int, c_int, c_int, c_int, c_float, _P, _P, _P, _P, c_int, _P],
     "q355_attn_o_resid": [_P, _P, c_int, _P, c_int, _P, c_int, _P, c_int, _P],
+    "q355_rmsnorm_fix_q8_1": [_P, _P, _P, _P, c_int, c_int, c_float, _P],
+    "q355_mmq_q4_0_q8_1": [_P, _P, c_int, c_int, _P, _P, c_int, c_int, _P, _P, _P, _P, _P, _P, _P],
+    "q355_mmq_nparts": [c_int],
+    "q355_qkv_finish": [_P, _P, _P, _P, _P, _P, c_int, c_int, _P, _P, _P, c_int, c_int, c_int, _P],
 }
 # entry points returning something other than an int status
-_VALUE_FUNCS = {"q355_head_nparts"}
+_VALUE_FUNCS = {"q355_head_nparts", "q355_mmq_nparts"}
 
 _lib = None
 

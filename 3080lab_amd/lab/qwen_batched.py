@@ -1,0 +1,190 @@
+"""Batched decode on int8 MFMA and the reference's lab/qwen_batched.py names.
+
+The reference's batched step (scripts/qwen_batched_decode.py:156-187) runs B sequences per step with
+tensor-core GEMVs over bf16 activations (gemv_v2_source) and per-sequence contiguous bf16 KV caches.
+Here B sequences share one step with:
+  rmsnorm_fix_q8_1       RMSNorm of the fixed-point residual stream -> Q8_1 (per token)
+  mmq (resid_fix)        QKV on v_mfma_i32_16x16x32_i8, K-sliced into an int64 accumulator
+  qkv_finish             bias + RoPE + fp16 q + paged fp16 K/V write (clears the accumulator)
+  attn_decode + merge    split-K GQA attention over 64-position pages of every sequence -> Q8_1
+  mmq (resid_fix)        O projection into the residual stream
+  rmsnorm_fix_q8_1, mmq (swiglu_q8)   gate_up + SwiGLU, output already Q8_1
+  mmq (resid_fix)        down projection into the residual stream
+then rmsnorm + mmq (logits) over the tied Q4_0 head + finish (argmax per sequence, pos += 1).
+The KV cache is paged: a shared pool of 64-position pages, one block-table row per sequence.
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, field
+
+import numpy as np
+
+from .hip import call, ptr
+from .qwen_model import PAGE, Config, DeviceModel
+
+
+@dataclass(frozen=True)
+class KernelSpec:
+    symbol: str
+    params: dict = field(default_factory=dict)
+
+
+# reference generator names (lab/qwen_batched.py) -> the C-ABI entry points that replace them
+def gemv_v2_source(WM=1, WK=1, MT=1, B=8, epi="store", PF=1, KS=1, ACC16=False) -> KernelSpec:
+    """Batched decode GEMV (lab/qwen_batched.py:467-641) -> q355_mmq_q4_0_q8_1 (int8 MFMA); epi store /
+    resid (fixed-point residual) / swiglu (-> swiglu_q8) / biasf (-> resid_fix + q355_qkv_finish)."""
+    code = {"store": 0, "logits": 5, "resid": 6, "biasf": 6, "swiglu": 7, "swiglu_q8": 7}[epi]
+    return KernelSpec("q355_mmq_q4_0_q8_1", {"epi": code})
+
+
+def gemm_q4i8_ms_source(WM=4, WN=2, MT=2, NT=4, epi="store", KB=4, NSTG=2, MINB=1, ABL=None) -> KernelSpec:
+    """Prefill MMQ (lab/qwen_batched.py:1271-1561) -> the same int8 MFMA entry point (epi as above)."""
+    e = epi.split(":")[0]
+    code = {"store": 0, "resid": 6, "biasf": 6, "biasf_kv": 6, "swiglu": 7, "swiglu_q8": 7}[e]
+    return KernelSpec("q355_mmq_q4_0_q8_1", {"epi": code})
+
+
+gemm_q4i8_source = gemm_q4i8_ms_source
+QUANT_Q8 = KernelSpec("q355_quant_q8_1")
+
+
+def rmsnorm_q8_source(H: int) -> KernelSpec:
+    """RMSNorm + Q8 quantizer (lab/qwen_batched.py:1044-1091) over the fixed-point residual stream."""
+    return KernelSpec("q355_rmsnorm_fix_q8_1", {"H": H})
+
+
+def pack_q4_i8(W, S):
+    """The reference repacks Q4_0 into mma fragment order (lab/qwen_batched.py:987-1013). The MI355X
+    layout (16-row tiled planes, lab.gguf.tile_q4_0) already is the MFMA A-operand order, so this is the
+    identity on (qs, d) planes."""
+    return W, S
+
+
+pack_q4_mma = pack_q4_i8
+
+
+class BatchedDecoder:
+    """B sequences decoded together over a paged fp16 KV cache (scripts/qwen_batched_decode.py:86-187).
+
+    ctx_pages: pages per sequence (max context / 64). Pages come from one pool and are assigned to the
+    sequences in a seeded random order (the block table is a permutation), so the kernels are exercised
+    on non-contiguous pages."""
+
+    def __init__(self, m: DeviceModel, B: int, max_ctx: int, page_seed: int = 0):
+        import torch
+        c = m.cfg
+        self.m, self.cfg, self.B = m, c, B
+        dev = m.device
+        self.max_chunks = -(-max_ctx // PAGE)
+        n_pages = B * self.max_chunks
+        order = np.random.default_rng(page_seed).permutation(n_pages).astype(np.int32)
+        self.block_table = torch.from_numpy(order.reshape(B, self.max_chunks)).to(dev)
+        self.kc = [torch.zeros(n_pages, c.NKV, PAGE, c.HD, dtype=torch.float16, device=dev) for _ in range(c.L)]
+        self.vc = [torch.zeros_like(k) for k in self.kc]
+        H = c.H
+        self.h = torch.zeros(B, H, dtype=torch.int64, device=dev)
+        self.xq = torch.zeros(B, max(H, c.FFN), dtype=torch.int8, device=dev)
+        self.xds = torch.zeros(B, max(H, c.FFN) // 32, 2, dtype=torch.float16, device=dev)
+        self.mq = torch.zeros(B, c.FFN, dtype=torch.int8, device=dev)
+        self.mds = torch.zeros(B, c.FFN // 32, 2, dtype=torch.float16, device=dev)
+        self.qkv_acc = torch.zeros(B, c.nqkv, dtype=torch.int64, device=dev)
+        self.q = torch.zeros(B, c.NH * c.HD, dtype=torch.float16, device=dev)
+        self.part = torch.zeros(B, c.NH, self.max_chunks, c.HD + 2, dtype=torch.float32, device=dev)
+        self.aq = torch.zeros(B, c.NH * c.HD, dtype=torch.int8, device=dev)
+        self.ads = torch.zeros(B, c.NH * c.HD // 32, 2, dtype=torch.float16, device=dev)
+        self.logits = torch.zeros(B, c.V, dtype=torch.float32, device=dev)
+        self.nparts = call("q355_mmq_nparts", c.V)
+        self.pmax = torch.zeros(B, self.nparts, dtype=torch.float32, device=dev)
+        self.pidx = torch.zeros(B, self.nparts, dtype=torch.int32, device=dev)
+        self.tok = torch.zeros(B, dtype=torch.int32, device=dev)
+        self.pos = torch.zeros(B, dtype=torch.int32, device=dev)
+        self.scale = 1.0 / math.sqrt(c.HD)
+
+    def h_f32(self):
+        import torch
+        return (self.h.to(torch.float64) * 2.0 ** -32).to(torch.float32)
+
+    def _norm(self, w):
+        c = self.cfg
+        call("q355_rmsnorm_fix_q8_1", ptr(self.h), ptr(w), ptr(self.xq), ptr(self.xds), self.B, c.H, c.eps)
+
+    def _mmq(self, W, xq, xds, epi, y=None, yfix=None, oq=None, ods=None, pmax=None, pidx=None):
+        call("q355_mmq_q4_0_q8_1", ptr(W.qs), ptr(W.d), W.N, W.K, ptr(xq), ptr(xds), self.B, epi,
+             ptr(y), ptr(yfix), ptr(oq), ptr(ods), ptr(pmax), ptr(pidx))
+
+    def layer(self, i: int):
+        m, c, B = self.m, self.cfg, self.B
+        L = m.layers[i]
+        self._norm(L["ln1"])
+        self._mmq(L["qkv"], self.xq, self.xds, 6, yfix=self.qkv_acc)
+        call("q355_qkv_finish", ptr(self.qkv_acc), ptr(L["qkv_b"]), ptr(m.cos), ptr(m.sin), ptr(self.pos),
+             ptr(self.block_table), self.max_chunks, 1, ptr(self.kc[i]), ptr(self.vc[i]), ptr(self.q),
+             c.NH, c.NKV, B)
+        call("q355_attn_decode", ptr(self.q), ptr(self.kc[i]), ptr(self.vc[i]), ptr(self.pos), ptr(self.block_table),
+             self.max_chunks, c.NH, c.NKV, self.max_chunks, self.scale, ptr(self.part), ptr(self.aq), ptr(self.ads),
+             None, B)
+        self._mmq(L["o"], self.aq, self.ads, 6, yfix=self.h)
+        self._norm(L["ln2"])
+        self._mmq(L["gu"], self.xq, self.xds, 7, oq=self.mq, ods=self.mds)
+        self._mmq(L["down"], self.mq, self.mds, 6, yfix=self.h)
+
+    def step(self):
+        c, m = self.cfg, self.m
+        e = m.embed
+        call("q355_embed_q4_0", ptr(e.qs), ptr(e.d), e.N, e.K, ptr(self.tok), ptr(self.h), self.B)
+        for i in range(c.L):
+            self.layer(i)
+        self._norm(m.norm)
+        self._mmq(e, self.xq, self.xds, 5, y=self.logits, pmax=self.pmax, pidx=self.pidx)
+        call("q355_finish", ptr(self.pmax), ptr(self.pidx), self.nparts, ptr(self.tok), ptr(self.pos), self.B)
+
+    def capture(self):
+        import torch
+        pos0, tok0 = self.pos.clone(), self.tok.clone()
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            self.step()
+        torch.cuda.current_stream().wait_stream(side)
+        self.pos.copy_(pos0)
+        self.tok.copy_(tok0)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            self.step()
+        self.pos.copy_(pos0)
+        self.tok.copy_(tok0)
+        torch.cuda.synchronize()
+        self.graph = g
+        return g
+
+    def prefill_tokens(self, ids):
+        """ids int [B, P]: feed the prompts token by token through step() (scripts/qwen_batched_decode.py:205-208)."""
+        import torch
+        ids = np.asarray(ids)
+        for t in range(ids.shape[1]):
+            self.tok.copy_(torch.from_numpy(ids[:, t].astype(np.int32)))
+            self.step()
+
+    def fill_random_context(self, ctx_lens, seed: int = 0):
+        """Synthetic contexts: positions 0..ctx-1 of every sequence and layer filled with
+        N(0, 1) fp16 K/V; pos[b] = ctx_lens[b]. Generated on the GPU (torch, seeded)."""
+        import torch
+        g = torch.Generator(device=self.m.device).manual_seed(seed)
+        for i in range(self.cfg.L):
+            self.kc[i].normal_(generator=g)
+            self.vc[i].normal_(generator=g)
+        self.pos.copy_(torch.as_tensor(np.asarray(ctx_lens, np.int32)))
+
+    def generate(self, n: int, use_graph: bool = True):
+        import torch
+        out = [self.tok.clone()]
+        if use_graph and not hasattr(self, "graph"):
+            self.capture()
+        for _ in range(n - 1):
+            if use_graph:
+                self.graph.replay()
+            else:
+                self.step()
+            out.append(self.tok.clone())
+        return torch.stack(out, 1).cpu().numpy()

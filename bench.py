@@ -40,20 +40,29 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def time_launches(fn, reps: int) -> float:
-    """Average ms per call of fn() over `reps` calls, HIP events on the current (launch) stream."""
+def time_launches(fn, n: int, reps: int = 20) -> float:
+    """Average ms per launch of fn(0..n-1), captured back to back in one hipGraph and replayed `reps` times,
+    timed with HIP events on the launch stream (the same per-launch duration rocprofv3 reports, plus the
+    graph's inter-node gap)."""
     import torch
-    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    fn(0)
     torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for i in range(n):
+            fn(i)
+    g.replay()
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     s.record()
-    for i in range(reps):
-        fn(i)
+    for _ in range(reps):
+        g.replay()
     e.record()
     torch.cuda.synchronize()
-    return s.elapsed_time(e) / reps
+    return s.elapsed_time(e) / (reps * n)
 
 
-def gate_up_roofline(dm, dec, reps: int = 112) -> dict:
+def gate_up_roofline(dm, dec) -> dict:
     from lab.hip import call, ptr
     c = dm.cfg
     gu0 = dm.layers[0]["gu"]
@@ -64,15 +73,14 @@ def gate_up_roofline(dm, dec, reps: int = 112) -> dict:
         g = L["gu"]
         call("q355_ffn_gate_up", ptr(g.qs), ptr(g.d), g.N, g.K, ptr(dec.h), ptr(L["ln2"]), c.eps,
              ptr(dec.mlp), 1)
-    run(0)
-    ms = time_launches(run, reps)
+    ms = time_launches(run, c.L)
     ach = algo / (ms * 1e-3) / 1e9
     return {"kernel": "q355_ffn_gate_up (k_gemv<1,1,4,3,PRO_RMS,EPI_SWIGLU>)", "bound": "hbm",
             "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4),
             "traffic": None, "algorithmic_bytes": int(algo), "avg_us": round(ms * 1e3, 3)}
 
 
-def gemv_config0(copies: int = 64, reps: int = 256) -> dict:
+def gemv_config0(copies: int = 64) -> dict:
     import torch
     from lab import gguf
     from lab import qwen_model as QM
@@ -97,13 +105,46 @@ def gemv_config0(copies: int = 64, reps: int = 256) -> dict:
 
     def run_hot(i):
         call("q355_gemv_q4_0_q8_1", ptr(qs[0]), ptr(ds[0]), N, K, ptr(xq), ptr(xds), 1, ptr(y), None, 0)
-    run(0)
-    cold = time_launches(run, reps)
-    hot = time_launches(run_hot, reps)
+    cold = time_launches(run, copies)
+    hot = time_launches(run_hot, copies)
     return {"shape": "8960x1536 Q4_0 x Q8_1, batch 1", "algorithmic_bytes": GEMV0_BYTES,
             "cold_us": round(cold * 1e3, 3), "cold_GBps": round(GEMV0_BYTES / (cold * 1e-3) / 1e9, 1),
             "hot_mall_us": round(hot * 1e3, 3), "hot_mall_GBps": round(GEMV0_BYTES / (hot * 1e-3) / 1e9, 1),
             "weight_copies": copies}
+
+
+def batched_decode(dm, B: int, steps: int = 32, warmup: int = 2) -> dict:
+    """B sequences with contexts uniform in [256, 2048] (seed 3), paged fp16 KV filled
+    with N(0, 1), one hipGraph per step on the int8 MFMA path; tok/s = B * steps / time."""
+    import torch
+    from lab import qwen_batched as QB
+    rng = np.random.default_rng(3)
+    ctx = rng.integers(256, 2049, B)
+    bd = QB.BatchedDecoder(dm, B=B, max_ctx=2048 + warmup + steps + 1, page_seed=B)
+    bd.fill_random_context(ctx, seed=B)
+    bd.tok.copy_(torch.from_numpy(rng.integers(0, dm.cfg.V, B).astype(np.int32)))
+    pos0, tok0 = bd.pos.clone(), bd.tok.clone()
+    g = bd.capture()
+    for _ in range(warmup):
+        g.replay()
+    bd.pos.copy_(pos0)
+    bd.tok.copy_(tok0)
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(steps):
+        g.replay()
+    e.record()
+    torch.cuda.synchronize()
+    ms = s.elapsed_time(e) / steps
+    kv = int(28_672 * (ctx.sum() + B * steps / 2))          # mean K+V bytes read per step
+    wbytes = dm.weight_bytes_per_token()
+    out = {"B": B, "tok_per_s": round(B * 1e3 / ms, 1), "ms_per_step": round(ms, 4),
+           "ctx_mean": float(ctx.mean()), "bytes_per_step": wbytes + kv,
+           "hbm_GBps": round((wbytes + kv) / (ms * 1e-3) / 1e9, 1)}
+    del bd
+    torch.cuda.empty_cache()
+    return out
 
 
 def cpu_baseline(w, cfg, prompt, n_steps: int = 3) -> dict:
@@ -187,6 +228,8 @@ def main():
            "decode_hbm_GBps": round(algo / (ms * 1e-3) / 1e9, 1),
            "decode_roofline_frac": round(algo / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
     if not args.quick:
+        out["batched"] = [batched_decode(dm, B) for B in (8, 32)]
+        log("batched:", out["batched"])
         out["roofline"] = gate_up_roofline(dm, dec)
         out["gemv"] = gemv_config0()
         if not args.no_cpu:

@@ -111,6 +111,31 @@ int q355_attn_decode(const void* q, const void* kcache, const void* vcache, cons
 int q355_attn_o_resid(const uint8_t* qs, const void* d, int N, const float* part, int max_chunks,
                       const int32_t* pos, int nh, int64_t* h, int T, void* stream);
 
+/* ---- int8 MFMA path: batched decode (config 3) and prefill (config 4) ---- */
+
+/* RMSNorm of the fixed-point residual stream -> Q8_1 (one token per workgroup).
+ * Replaces rmsnorm_q8_source (lab/qwen_batched.py:1044-1091) / RMSNORM_F32W_1P batched by blockIdx.y. */
+int q355_rmsnorm_fix_q8_1(const int64_t* h, const float* w, int8_t* xq, void* xds, int T, int H, float eps,
+                          void* stream);
+
+/* Q4_0 x Q8_1 product of T tokens on v_mfma_i32_16x16x32_i8 (exact int32 block dots), N % 64 == 0.
+ * epi 0: y fp32 [T][N] = W x;  5: logits y [T][N] + argmax partials pmax/pidx [T][q355_mmq_nparts(N)];
+ * 6: yfix [T][N] += W x (int64 fixed point, K-sliced, integer atomics);
+ * 7: rows interleaved (gate, up): Q8_1 of silu(g) * u into oq [T][N/2], ods [T][N/64].
+ * Replaces gemv_v2_source (lab/qwen_batched.py:467-641; batched decode, fp16 tensor cores there) and
+ * gemm_q4i8_source / gemm_q4i8_ms_source with epilogues resid / swiglu_q8 (lab/qwen_batched.py:1093-1561). */
+int q355_mmq_q4_0_q8_1(const uint8_t* qs, const void* d, int N, int K, const int8_t* xq, const void* xds, int T,
+                       int epi, float* y, int64_t* yfix, int8_t* oq, void* ods, float* pmax, int32_t* pidx,
+                       void* stream);
+int q355_mmq_nparts(int N);
+
+/* QKV epilogue of the MFMA path: acc int64 fixed point [T][nqkv] (device row order) -> + bias, RoPE, fp16
+ * q out [T][nh*128], fp16 K/V cache rows at pos[j] of sequence j * seq_stride; acc is zeroed.
+ * Replaces 'biasf_kv' (lab/qwen_batched.py:1316-1362) and the RoPE/KV-write head of ATTN4. */
+int q355_qkv_finish(int64_t* acc, const float* bias, const float* rope_cos, const float* rope_sin,
+                    const int32_t* pos, const int32_t* block_table, int bt_stride, int seq_stride, void* kcache,
+                    void* vcache, void* qout, int nh, int nkv, int T, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
