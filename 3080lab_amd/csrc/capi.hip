@@ -16,7 +16,7 @@ __global__ void k_blockdots(const uint8_t*, int, int, const int8_t*, int, int*);
 template <int G>
 __global__ void k_attn_decode(const AttnArgs);
 __global__ void k_attn_merge(const AttnArgs);
-__global__ void k_rmsnorm_fix_q8_1(const long long*, const float*, int8_t*, half2*, int, float);
+__global__ void k_rmsnorm_fix_q8_1(const long long*, const float*, int8_t*, half2*, int, double);
 __global__ void k_qkv_finish(GemvArgs, long long*);
 }  // namespace q355
 
@@ -53,7 +53,7 @@ static int launch_gemv(const GemvArgs& a, int KS, hipStream_t s) {
   if (per > 4 * NW * KPL) return fail(Q355_EINVAL, "gemv: K=%d slice of %d blocks exceeds %d", a.K, per, 4 * NW * KPL);
   const dim3 grid(tiles / NT, KS);
   size_t lds = (size_t)a.T * a.K + (size_t)a.T * nb * 8;
-  if (PRO == PRO_ATTN) lds += (size_t)(2 * a.nh * a.attn_max_chunks + a.nh * HD) * 4;
+  if (PRO == PRO_ATTN) lds += 8 + (size_t)(2 * a.nh * a.attn_max_chunks + a.nh * HD) * 8;  // 8: f64 alignment
   switch (a.T) {
     case 1: hipLaunchKernelGGL((k_gemv<1, NT, NW, KPL, PRO, EPI>), grid, dim3(NW * 64), lds, s, a); break;
     case 2: hipLaunchKernelGGL((k_gemv<2, NT, NW, KPL, PRO, EPI>), grid, dim3(NW * 64), lds, s, a); break;
@@ -126,7 +126,7 @@ extern "C" int q355_gemv_blockdots(const uint8_t* qs, int N, int K, const int8_t
   return launched("gemv_blockdots");
 }
 
-extern "C" int q355_qkv_rope_kv(const uint8_t* qs, const void* d, int K, const int64_t* h, const float* nw, float eps,
+extern "C" int q355_qkv_rope_kv(const uint8_t* qs, const void* d, int K, const int64_t* h, const float* nw, double eps,
                                 const float* bias, const float* rope_cos, const float* rope_sin, const int32_t* pos,
                                 const int32_t* block_table, int bt_stride, int seq_stride, void* kcache,
                                 void* vcache, void* qout, int nh, int nkv, int T, void* stream) {
@@ -149,7 +149,7 @@ extern "C" int q355_qkv_rope_kv(const uint8_t* qs, const void* d, int K, const i
 }
 
 extern "C" int q355_ffn_gate_up(const uint8_t* qs, const void* d, int N2, int K, const int64_t* h, const float* nw,
-                                float eps, float* m, int T, void* stream) {
+                                double eps, float* m, int T, void* stream) {
   if (int e = check_mat("ffn_gate_up", qs, d, N2, K)) return e;
   REQUIRE(K <= 1536, "ffn_gate_up: K=%d > 1536 (fused RMSNorm prologue)", K);
   REQUIRE(h && nw && m, "ffn_gate_up: null pointer");
@@ -176,7 +176,7 @@ extern "C" int q355_ffn_down(const uint8_t* qs, const void* d, int N, int K, con
 extern "C" int q355_head_nparts(int V) { return V / 128; }
 
 extern "C" int q355_head_logits(const uint8_t* qs, const void* d, int V, int K, const int64_t* h, const float* nw,
-                                float eps, float* logits, float* pmax, int32_t* pidx, int T, void* stream) {
+                                double eps, float* logits, float* pmax, int32_t* pidx, int T, void* stream) {
   if (int e = check_mat("head_logits", qs, d, V, K)) return e;
   REQUIRE(V % 128 == 0, "head_logits: V=%d must be a multiple of 128", V);
   REQUIRE(K <= 1536, "head_logits: K=%d > 1536 (fused RMSNorm prologue)", K);
@@ -207,7 +207,7 @@ extern "C" int q355_embed_q4_0(const uint8_t* qs, const void* d, int V, int H, c
 
 extern "C" int q355_attn_decode(const void* q, const void* kcache, const void* vcache, const int32_t* pos,
                                 const int32_t* block_table, int bt_stride, int nh, int nkv, int max_chunks,
-                                float scale, float* part, int8_t* oq, void* ods, float* o32, int T, void* stream) {
+                                double scale, double* part, int8_t* oq, void* ods, float* o32, int T, void* stream) {
   REQUIRE(q && kcache && vcache && pos && block_table && part, "attn_decode: null pointer");
   REQUIRE(nh > 0 && nkv > 0 && nh % nkv == 0, "attn_decode: nh=%d nkv=%d", nh, nkv);
   REQUIRE(nh / nkv == 6 || nh / nkv == 4 || nh / nkv == 8, "attn_decode: GQA group %d (4, 6 or 8 supported)", nh / nkv);
@@ -230,12 +230,12 @@ extern "C" int q355_attn_decode(const void* q, const void* kcache, const void* v
   }
   if (int e = launched("attn_decode")) return e;
   if (!oq) return Q355_OK;
-  const size_t lds = (size_t)(2 * nh * max_chunks + nh * HD) * 4;
+  const size_t lds = (size_t)(2 * nh * max_chunks + nh * HD) * 8;
   hipLaunchKernelGGL(k_attn_merge, dim3(T), dim3(256), lds, s, a);
   return launched("attn_merge");
 }
 
-extern "C" int q355_attn_o_resid(const uint8_t* qs, const void* d, int N, const float* part, int max_chunks,
+extern "C" int q355_attn_o_resid(const uint8_t* qs, const void* d, int N, const double* part, int max_chunks,
                                  const int32_t* pos, int nh, int64_t* h, int T, void* stream) {
   const int K = nh * HD;
   if (int e = check_mat("attn_o_resid", qs, d, N, K)) return e;
@@ -253,7 +253,7 @@ extern "C" int q355_attn_o_resid(const uint8_t* qs, const void* d, int N, const 
 // ------------------------------------------------------------------------------------------------
 // MFMA path (batched decode, prefill)
 
-extern "C" int q355_rmsnorm_fix_q8_1(const int64_t* h, const float* w, int8_t* xq, void* xds, int T, int H, float eps,
+extern "C" int q355_rmsnorm_fix_q8_1(const int64_t* h, const float* w, int8_t* xq, void* xds, int T, int H, double eps,
                                      void* stream) {
   REQUIRE(h && w && xq && xds, "rmsnorm_fix_q8_1: null pointer");
   REQUIRE(T > 0 && H > 0 && H % 32 == 0 && H <= 2048, "rmsnorm_fix_q8_1: T=%d H=%d (H %% 32 == 0, <= 2048)", T, H);

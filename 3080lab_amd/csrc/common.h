@@ -89,6 +89,13 @@ __device__ __forceinline__ float wave_sum_fast(float v) {
 // Q8_1 of 8 consecutive values held by one lane; 4 lanes form a 32-block (lane groups aligned to 4).
 // Bit-exact with the oracle (d = fp16(amax/127), q = roundf(x / d16) clamped, 0 when d16 == 0).
 // Returns the 8 int8 packed in a uint2; d (as float) and the block's sum of q through the references.
+// f64 -> fp16 with ONE round to nearest even (no intermediate fp32 rounding, which can land exactly on an
+// fp16 midpoint and then break the tie the other way).
+__device__ __forceinline__ __half half_rn(double v) {
+  const _Float16 h = (_Float16)v;
+  return *reinterpret_cast<const __half*>(&h);
+}
+
 __device__ __forceinline__ uint2 q8_1_x8(const float (&x)[8], float& df, int& sq) {
   float amax = 0.f;
 #pragma unroll
@@ -112,6 +119,21 @@ __device__ __forceinline__ uint2 q8_1_x8(const float (&x)[8], float& df, int& sq
   pk.x = (q[0] & 255) | ((q[1] & 255) << 8) | ((q[2] & 255) << 16) | ((unsigned)(q[3] & 255) << 24);
   pk.y = (q[4] & 255) | ((q[5] & 255) << 8) | ((q[6] & 255) << 16) | ((unsigned)(q[7] & 255) << 24);
   return pk;
+}
+
+// f64 wave reductions (the batch-1 decode path accumulates in f64 so that every Q8_1 quantizer input
+// agrees with the f64 oracle to ~1e-14; CDNA4 runs f64 FMA at the fp32 vector rate).
+template <int WIDTH = 64>
+__device__ __forceinline__ double wave_sum_d(double v) {
+#pragma unroll
+  for (int o = WIDTH / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+template <int WIDTH = 64>
+__device__ __forceinline__ double wave_max_d(double v) {
+#pragma unroll
+  for (int o = WIDTH / 2; o > 0; o >>= 1) v = fmax(v, __shfl_xor(v, o, 64));
+  return v;
 }
 
 // Wave64 reductions (xor butterfly over all 64 lanes, or over `width` lanes).

@@ -170,64 +170,67 @@ struct XLoad {
                                         char* extra) {
     const int K = a.K, nb = K / 32;
     if (PRO == PRO_ATTN) {
-      // merge the split-K attention partials of the heads in this K slice, then Q8_1 into LDS
-      float* wgt = (float*)extra;
-      float* ob = wgt + 2 * a.nh * a.attn_max_chunks;
+      // merge the split-K attention partials of the heads in this K slice (f64), then Q8_1 into LDS
+      double* wgt = (double*)extra;
+      double* ob = wgt + 2 * a.nh * a.attn_max_chunks;
       const int h0 = ks.b0 * 32 / HD, nhs = (ks.b1 - ks.b0) * 32 / HD;
       for (int j = 0; j < a.T; ++j) {
         const int nch = a.pos[j] / PAGE + 1;
         attn_merge_token<NTH>(a.attn_part + ((size_t)j * a.nh + h0) * a.attn_max_chunks * (HD + 2), nhs,
                               a.attn_max_chunks, nch, wgt, ob);
         for (int g = threadIdx.x; g < nhs * HD / 8; g += NTH) {   // quads stay whole (HD / 8 % 4 == 0)
-          const float4 u0 = ((const float4*)ob)[2 * g], u1 = ((const float4*)ob)[2 * g + 1];
-          const float x[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
+          float x[8];
+#pragma unroll
+          for (int u = 0; u < 8; ++u) x[u] = (float)ob[8 * g + u];
           stage_x8(st, K, j, h0 * HD / 8 + g, x);
         }
         __syncthreads();
       }
     } else if (R) {
+      // RMSNorm in f64: the quantizer input x = h * rsqrt(mean(h^2) + eps) * w matches the f64 oracle
       const int ng = K / 8, ntask = a.T * ng;
-      float hv[P8][8];
-      float ss[T];
+      double ss[T];
 #pragma unroll
-      for (int j = 0; j < T; ++j) ss[j] = 0.f;
+      for (int j = 0; j < T; ++j) ss[j] = 0.0;
 #pragma unroll
       for (int p = 0; p < P8; ++p) {
         const int task = threadIdx.x + NTH * p;
-        float v = 0.f;
+        double v = 0.0;
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
-          hv[p][u] = from_fix(hl[p][u]);
-          v = fmaf(hv[p][u], hv[p][u], v);
+          const double hv = from_fix(hl[p][u]);
+          v = fma(hv, hv, v);
         }
 #pragma unroll
-        for (int j = 0; j < T; ++j) ss[j] += (task < ntask && task / ng == j) ? v : 0.f;
+        for (int j = 0; j < T; ++j) ss[j] += (task < ntask && task / ng == j) ? v : 0.0;
       }
+      double* redd = (double*)red;
 #pragma unroll
       for (int j = 0; j < T; ++j) {
-        const float w = wave_sum_fast(ss[j]);
-        if ((threadIdx.x & 63) == 0) red[(threadIdx.x >> 6) * T + j] = w;
+        const double w = wave_sum_d(ss[j]);
+        if ((threadIdx.x & 63) == 0) redd[(threadIdx.x >> 6) * T + j] = w;
       }
       __syncthreads();
-      float rs[T];
+      double rs[T];
 #pragma unroll
       for (int j = 0; j < T; ++j) {
-        float t = 0.f;
+        double t = 0.0;
 #pragma unroll
-        for (int w = 0; w < NW; ++w) t += red[w * T + j];
-        rs[j] = 1.0f / sqrtf(t / (float)K + a.eps);
+        for (int w = 0; w < NW; ++w) t += redd[w * T + j];
+        rs[j] = 1.0 / sqrt(t / (double)K + a.eps);
       }
 #pragma unroll
       for (int p = 0; p < P8; ++p) {
         const int task = threadIdx.x + NTH * p;
         if (task < ntask) {
           const int j = task / ng, g = task % ng;
-          float r = rs[0];
+          double r = rs[0];
 #pragma unroll
           for (int jj = 1; jj < T; ++jj) r = (j == jj) ? rs[jj] : r;
-          const float x[8] = {hv[p][0] * r * xa[p].x, hv[p][1] * r * xa[p].y, hv[p][2] * r * xa[p].z,
-                              hv[p][3] * r * xa[p].w, hv[p][4] * r * xb[p].x, hv[p][5] * r * xb[p].y,
-                              hv[p][6] * r * xb[p].z, hv[p][7] * r * xb[p].w};
+          const float wv[8] = {xa[p].x, xa[p].y, xa[p].z, xa[p].w, xb[p].x, xb[p].y, xb[p].z, xb[p].w};
+          float x[8];
+#pragma unroll
+          for (int u = 0; u < 8; ++u) x[u] = (float)(from_fix(hl[p][u]) * r * (double)wv[u]);
           stage_x8(st, K, j, g, x);
         }
       }
@@ -262,29 +265,30 @@ struct XLoad {
 };
 
 // ---------------------------------------------------------------------------------------------
-// Epilogues. part[w][t][j][r] holds wave w's partial of row (tile0 + t) * 16 + r for token j.
-template <int NW, int T, int NT>
-__device__ __forceinline__ float row_value(float (&part)[NW][NT][T][16], int t, int j, int r) {
-  float v = part[0][t][j][r];
+// Epilogues. part[w][t][j][r] holds wave w's partial of row (tile0 + t) * 16 + r for token j (f64 on the
+// batch-1 path, fp32 on the MFMA path); everything after the reduction is computed in f64.
+template <int NW, int T, int NT, typename A>
+__device__ __forceinline__ double row_value(A (&part)[NW][NT][T][16], int t, int j, int r) {
+  double v = part[0][t][j][r];
 #pragma unroll
   for (int w = 1; w < NW; ++w) v += part[w][t][j][r];
   return v;
 }
 
-__device__ __forceinline__ float silu_mul(float g, float u) { return g / (1.0f + expf(-g)) * u; }
+__device__ __forceinline__ double silu_mul(double g, double u) { return g / (1.0 + exp(-g)) * u; }
 
-template <int NW, int T, int NT, int EPI>
-__device__ __forceinline__ void epilogue(const GemvArgs& a, float (&part)[NW][NT][T][16], int tile0) {
+template <int NW, int T, int NT, int EPI, typename A>
+__device__ __forceinline__ void epilogue(const GemvArgs& a, A (&part)[NW][NT][T][16], int tile0) {
   const int N = a.N;
   if (EPI == EPI_LOGITS) {
-    // one wave computes the (value, row) argmax of the NT * 16 rows, lowest row on ties
+    // one wave computes the (value, row) argmax of the NT * 16 rows, lowest row on ties (fp32 logits)
     if (threadIdx.x < 64) {
       const int l = threadIdx.x;
       for (int j = 0; j < T && j < a.T; ++j) {
         float v = -INFINITY;
         int idx = 0x7fffffff;
         for (int rr = l; rr < NT * 16; rr += 64) {   // rows in increasing order: strict '>' keeps the lowest
-          const float x = row_value<NW, T, NT>(part, rr >> 4, j, rr & 15);
+          const float x = (float)row_value<NW, T, NT>(part, rr >> 4, j, rr & 15);
           a.y[(size_t)j * N + tile0 * 16 + rr] = x;
           if (x > v) { v = x; idx = tile0 * 16 + rr; }
         }
@@ -308,10 +312,10 @@ __device__ __forceinline__ void epilogue(const GemvArgs& a, float (&part)[NW][NT
       const int j = e >> 5, k = e & 31;
       if (j >= a.T) break;                                      // uniform per 32-lane group
       const int rg = 2 * k, ru = 2 * k + 1;
-      const float g = row_value<NW, T, NT>(part, rg >> 4, j, rg & 15);
-      const float u = row_value<NW, T, NT>(part, ru >> 4, j, ru & 15);
+      const double g = row_value<NW, T, NT>(part, rg >> 4, j, rg & 15);
+      const double u = row_value<NW, T, NT>(part, ru >> 4, j, ru & 15);
       const int Nout = N / 2;
-      const int q = q8_1_lane32(silu_mul(g, u), a.ods + (size_t)j * (Nout / 32) + blockIdx.x, k == 0);
+      const int q = q8_1_lane32((float)silu_mul(g, u), a.ods + (size_t)j * (Nout / 32) + blockIdx.x, k == 0);
       a.oq[(size_t)j * Nout + blockIdx.x * 32 + k] = (int8_t)q;
     }
     return;
@@ -321,8 +325,8 @@ __device__ __forceinline__ void epilogue(const GemvArgs& a, float (&part)[NW][NT
     for (int e = threadIdx.x; e < NT * T * 8; e += blockDim.x) {
       const int t = e / (T * 8), j = (e >> 3) % T, k = e & 7;
       if (j >= a.T) continue;
-      const float g = row_value<NW, T, NT>(part, t, j, 2 * k), u = row_value<NW, T, NT>(part, t, j, 2 * k + 1);
-      a.y[(size_t)j * (N / 2) + (tile0 + t) * 8 + k] = silu_mul(g, u);
+      const double g = row_value<NW, T, NT>(part, t, j, 2 * k), u = row_value<NW, T, NT>(part, t, j, 2 * k + 1);
+      a.y[(size_t)j * (N / 2) + (tile0 + t) * 8 + k] = (float)silu_mul(g, u);
     }
     return;
   }
@@ -330,37 +334,38 @@ __device__ __forceinline__ void epilogue(const GemvArgs& a, float (&part)[NW][NT
     const int t = e / (T * 16), j = (e >> 4) % T, r = e & 15;
     if (j >= a.T) continue;
     const int row = (tile0 + t) * 16 + r;
-    float v = row_value<NW, T, NT>(part, t, j, r);
+    double v = row_value<NW, T, NT>(part, t, j, r);
     if (EPI == EPI_STORE) {
-      a.y[(size_t)j * N + row] = v;
+      a.y[(size_t)j * N + row] = (float)v;
     } else if (EPI == EPI_RESID) {
-      a.y[(size_t)j * N + row] += v;
+      a.y[(size_t)j * N + row] += (float)v;
     } else if (EPI == EPI_RESID_FIX) {
       atomicAdd((unsigned long long*)(a.yfix + (size_t)j * N + row), (unsigned long long)to_fix(v));
     } else if (EPI == EPI_BIAS) {
-      a.y[(size_t)j * N + row] = v + a.aux[row];
+      a.y[(size_t)j * N + row] = (float)(v + (double)a.aux[row]);
     } else if (EPI == EPI_QKV) {
-      v += a.aux[row];
+      // f64: bias, RoPE; q, k and v rounded f64 -> fp16 once
+      v += (double)a.aux[row];
       const int nq = a.nh * HD, nk = a.nkv * HD;
       const int pos = a.pos[j];
       const int seq = (a.tok_base + j) * a.seq_stride;
       const int pg = a.block_table[(size_t)seq * a.bt_stride + pos / PAGE];
       if (row < nq + nk) {
-        const float v2 = row_value<NW, T, NT>(part, t, j, r ^ 1) + a.aux[row ^ 1];
+        const double v2 = row_value<NW, T, NT>(part, t, j, r ^ 1) + (double)a.aux[row ^ 1];
         const int e2 = row % HD, i = e2 >> 1, hi = e2 & 1;
-        const float c = a.rope_cos[(size_t)pos * (HD / 2) + i], s = a.rope_sin[(size_t)pos * (HD / 2) + i];
-        const float lo_v = hi ? v2 : v, hi_v = hi ? v : v2;
-        const float out = hi ? (hi_v * c + lo_v * s) : (lo_v * c - hi_v * s);
+        const double c = a.rope_cos[(size_t)pos * (HD / 2) + i], s = a.rope_sin[(size_t)pos * (HD / 2) + i];
+        const double lo_v = hi ? v2 : v, hi_v = hi ? v : v2;
+        const double out = hi ? (hi_v * c + lo_v * s) : (lo_v * c - hi_v * s);
         const int dim = i + (HD / 2) * hi;
         if (row < nq) {
-          a.qout[(size_t)j * nq + (row / HD) * HD + dim] = __float2half_rn(out);
+          a.qout[(size_t)j * nq + (row / HD) * HD + dim] = half_rn(out);
         } else {
           const int kvh = (row - nq) / HD;
-          a.kcache[(((size_t)pg * a.nkv + kvh) * PAGE + pos % PAGE) * HD + dim] = __float2half_rn(out);
+          a.kcache[(((size_t)pg * a.nkv + kvh) * PAGE + pos % PAGE) * HD + dim] = half_rn(out);
         }
       } else {
         const int rv = row - nq - nk, kvh = rv / HD, dim = rv % HD;
-        a.vcache[(((size_t)pg * a.nkv + kvh) * PAGE + pos % PAGE) * HD + dim] = __float2half_rn(v);
+        a.vcache[(((size_t)pg * a.nkv + kvh) * PAGE + pos % PAGE) * HD + dim] = half_rn(v);
       }
     }
   }
@@ -372,8 +377,8 @@ __device__ __forceinline__ void epilogue(const GemvArgs& a, float (&part)[NW][NT
 template <int T, int NT, int NW, int KPL, int PRO, int EPI>
 __global__ void __launch_bounds__(NW * 64) k_gemv(const GemvArgs a) {
   extern __shared__ __align__(16) char lds[];
-  __shared__ float red[NW * T];
-  __shared__ float part[NW][NT][T][16];
+  __shared__ double red[NW * T];
+  __shared__ double part[NW][NT][T][16];
   constexpr int NKL = 4 * NW;  // k-lanes
   const int K = a.K, nb = K / 32;
   const KSlice ks(nb);
@@ -409,14 +414,15 @@ __global__ void __launch_bounds__(NW * 64) k_gemv(const GemvArgs a) {
 #pragma unroll
     for (int t = 0; t < NT; ++t) dh[t][i] = (ks.b0 + kl + NKL * i < ks.b1) ? dh[t][i] : 0u;
 
-  xl.stage(a, ks, st, red, lds + (size_t)T * K + (size_t)T * nb * 8);
+  xl.stage(a, ks, st, (float*)red, lds + (size_t)T * K + (size_t)T * nb * 8);
   __syncthreads();
 
-  float acc[NT][T];
+  // f64 accumulation: each block term d_w * d_x * (dot - 8 sum q) is exact in f64 (22 + 21 bits)
+  double acc[NT][T];
 #pragma unroll
   for (int t = 0; t < NT; ++t)
 #pragma unroll
-    for (int j = 0; j < T; ++j) acc[t][j] = 0.f;
+    for (int j = 0; j < T; ++j) acc[t][j] = 0.0;
 #pragma unroll
   for (int i = 0; i < KPL; ++i) {
     const int b = min(ks.b0 + kl + NKL * i, ks.b1 - 1);   // lanes past the slice re-read a valid block, scale 0
@@ -431,7 +437,8 @@ __global__ void __launch_bounds__(NW * 64) k_gemv(const GemvArgs a) {
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
           const int dot = q4_block_dot(w[t][i], xv);
-          acc[t][j] = fmaf(__half2float(__ushort_as_half((unsigned short)dh[t][i])) * dx, (float)(dot - s8), acc[t][j]);
+          const double sc = (double)__half2float(__ushort_as_half((unsigned short)dh[t][i])) * (double)dx;
+          acc[t][j] = fma(sc, (double)(dot - s8), acc[t][j]);
         }
       }
     }
@@ -441,7 +448,7 @@ __global__ void __launch_bounds__(NW * 64) k_gemv(const GemvArgs a) {
   for (int t = 0; t < NT; ++t)
 #pragma unroll
     for (int j = 0; j < T; ++j) {
-      float v = acc[t][j];
+      double v = acc[t][j];
       v += __shfl_xor(v, 16, 64);
       v += __shfl_xor(v, 32, 64);
       if (lane < 16) part[wv][t][j][r] = v;
@@ -473,8 +480,8 @@ __global__ void __launch_bounds__(64) k_embed_q4_0(const uint8_t* __restrict__ q
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
       const unsigned byte = (ws[i >> 2] >> (8 * (i & 3))) & 0xFFu;
-      out[i] = to_fix(dw * (float)((int)(byte & 15u) - 8));
-      out[i + 16] = to_fix(dw * (float)((int)(byte >> 4) - 8));
+      out[i] = to_fix((double)dw * (double)((int)(byte & 15u) - 8));
+      out[i + 16] = to_fix((double)dw * (double)((int)(byte >> 4) - 8));
     }
   }
 }
@@ -514,27 +521,28 @@ __global__ void __launch_bounds__(256) k_finish(const float* __restrict__ pmax, 
 // RMSNorm of the fixed-point residual stream -> Q8_1, one token per workgroup (batched / prefill path).
 __global__ void __launch_bounds__(256) k_rmsnorm_fix_q8_1(const long long* __restrict__ h, const float* __restrict__ w,
                                                           int8_t* __restrict__ xq, half2* __restrict__ xds, int H,
-                                                          float eps) {
-  __shared__ float red[4];
+                                                          double eps) {
+  __shared__ double red[4];
   const int tok = blockIdx.x;
   const int g = threadIdx.x;                       // 8 consecutive values per thread, H / 8 <= 256
   const bool act = g < H / 8;
-  float x[8];
-  float ss = 0.f;
+  double hv[8];
+  double ss = 0.0;
 #pragma unroll
   for (int u = 0; u < 8; ++u) {
-    x[u] = act ? from_fix(h[(size_t)tok * H + 8 * g + u]) : 0.f;
-    ss = fmaf(x[u], x[u], ss);
+    hv[u] = act ? from_fix(h[(size_t)tok * H + 8 * g + u]) : 0.0;
+    ss = fma(hv[u], hv[u], ss);
   }
-  ss = wave_sum_fast(ss);
+  ss = wave_sum_d(ss);
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
   __syncthreads();
-  const float r = 1.0f / sqrtf((red[0] + red[1] + red[2] + red[3]) / (float)H + eps);
+  const double r = 1.0 / sqrt((red[0] + red[1] + red[2] + red[3]) / (double)H + eps);
+  float x[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   if (act) {
     const float4 w0 = ((const float4*)w)[2 * g], w1 = ((const float4*)w)[2 * g + 1];
     const float wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
 #pragma unroll
-    for (int u = 0; u < 8; ++u) x[u] = x[u] * r * wv[u];
+    for (int u = 0; u < 8; ++u) x[u] = (float)(hv[u] * r * (double)wv[u]);
   }
   float df;
   int sq;
@@ -557,13 +565,13 @@ __global__ void __launch_bounds__(256) k_qkv_finish(GemvArgs a, long long* __res
   for (int p = threadIdx.x; p < N / 2; p += blockDim.x) {
     const int row = 2 * p;
     long long* ap = acc + (size_t)j * N + row;
-    const float v0 = from_fix(ap[0]) + a.aux[row], v1 = from_fix(ap[1]) + a.aux[row + 1];
+    const double v0 = from_fix(ap[0]) + (double)a.aux[row], v1 = from_fix(ap[1]) + (double)a.aux[row + 1];
     ap[0] = 0;
     ap[1] = 0;
     if (row < nq + nk) {
       const int i = (row % HD) >> 1;               // pair (dim i, dim i + 64)
-      const float c = a.rope_cos[(size_t)pos * (HD / 2) + i], s = a.rope_sin[(size_t)pos * (HD / 2) + i];
-      const __half lo = __float2half_rn(v0 * c - v1 * s), hi = __float2half_rn(v1 * c + v0 * s);
+      const double c = a.rope_cos[(size_t)pos * (HD / 2) + i], s = a.rope_sin[(size_t)pos * (HD / 2) + i];
+      const __half lo = half_rn(v0 * c - v1 * s), hi = half_rn(v1 * c + v0 * s);
       if (row < nq) {
         __half* q = a.qout + (size_t)j * nq + (row / HD) * HD;
         q[i] = lo;
@@ -576,8 +584,8 @@ __global__ void __launch_bounds__(256) k_qkv_finish(GemvArgs a, long long* __res
     } else {
       const int rv = row - nq - nk;
       __half* v = a.vcache + (((size_t)pg * a.nkv + rv / HD) * PAGE + pos % PAGE) * HD + rv % HD;
-      v[0] = __float2half_rn(v0);
-      v[1] = __float2half_rn(v1);
+      v[0] = half_rn(v0);
+      v[1] = half_rn(v1);
     }
   }
 }

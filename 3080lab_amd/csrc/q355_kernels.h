@@ -14,20 +14,21 @@ enum Epilogue {
   EPI_QKV = 3,         // + bias, RoPE, fp16 q out, fp16 K/V cache write
   EPI_SWIGLU = 4,      // rows interleaved (gate, up): y[row / 2] = silu(g) * u (fp32)
   EPI_LOGITS = 5,      // y = acc and per-workgroup (max, lowest index) partials
-  EPI_RESID_FIX = 6,   // fixed-point residual: yfix += round(acc * 2^32) (int64 atomics; any K split)
+  EPI_RESID_FIX = 6,   // fixed-point residual: yfix += round(acc * 2^48) (int64 atomics; any K split)
   EPI_SWIGLU_Q8 = 7,   // as SWIGLU, quantized to Q8_1 (oq, ods): NT == 4 (64 rows -> one 32-output block)
 };
 
 constexpr int HD = 128;        // head dim (Qwen2.5-1.5B)
 constexpr int PAGE = 64;       // KV cache page: 64 positions of one KV head, [PAGE][HD] fp16
-constexpr float FIX_SCALE = 4294967296.0f;        // residual stream fixed point: value * 2^32 as int64
-constexpr double FIX_INV = 1.0 / 4294967296.0;
+constexpr double FIX_SCALE = 281474976710656.0;    // residual stream fixed point: value * 2^48 as int64
+constexpr double FIX_INV = 1.0 / 281474976710656.0;
 
-// The residual stream h is kept as int64 fixed point (2^-32 resolution, |h| < 2^31). Split-K
+// The residual stream h is kept as int64 fixed point (2^-48 resolution, |h| < 2^15). Split-K
 // producers add their partial sums with integer atomics, which are associative, so the stream is
-// bitwise independent of the order in which workgroups finish.
-__device__ __forceinline__ long long to_fix(float v) { return __float2ll_rn(v * FIX_SCALE); }
-__device__ __forceinline__ float from_fix(long long v) { return (float)((double)v * FIX_INV); }
+// bitwise independent of the order in which workgroups finish; 2^-48 is finer than the f64
+// accumulation it receives, so the stream tracks an f64 residual to ~1e-14.
+__device__ __forceinline__ long long to_fix(double v) { return __double2ll_rn(v * FIX_SCALE); }
+__device__ __forceinline__ double from_fix(long long v) { return (double)v * FIX_INV; }
 
 // Everything a GEMV-family launch may need; unused fields are null/zero.
 struct GemvArgs {
@@ -40,12 +41,12 @@ struct GemvArgs {
   // PRO_RMS input
   const long long* hfix;       // [T][K] residual stream, int64 fixed point
   const float* nw;             // [K] RMSNorm weight
-  float eps;
+  double eps;
   // PRO_F32 input (quantized to Q8_1 in the prologue)
   const float* xf;             // [T][K]
   // PRO_ATTN input: split-K attention partials [T][nh][attn_max_chunks][HD + 2], merged and quantized
   // in the prologue (K == nh * HD); the token positions come from `pos`
-  const float* attn_part;
+  const double* attn_part;
   int attn_max_chunks;
   // STORE / RESID / BIAS / SWIGLU / LOGITS output
   float* y;                    // [T][N] ([T][N/2] for SWIGLU)
@@ -80,8 +81,8 @@ struct AttnArgs {
   const int* block_table;      // [T][bt_stride]
   int bt_stride;
   int nh, nkv, max_chunks;     // chunk = one page
-  float scale;
-  float* part;                 // [T][nh][max_chunks][HD + 2] partial (o, m, l)
+  double scale;
+  double* part;                // [T][nh][max_chunks][HD + 2] partial (o, m, l), f64
   int8_t* oq;                  // [T][nh*HD] Q8_1 output for the O projection (standalone merge)
   half2* ods;                  // [T][nh*HD/32]
   float* o32;                  // optional fp32 output [T][nh*HD] (tests), may be null

@@ -10,7 +10,7 @@ There is no CPU fallback: if the library is missing or fails to load, `lib()` ra
 from __future__ import annotations
 
 import ctypes
-from ctypes import POINTER, c_char_p, c_float, c_int, c_uint32, c_void_p
+from ctypes import c_char_p, c_double, c_float, c_int, c_void_p
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parents[1] / "lib" / "libqwen355.so"
@@ -22,17 +22,17 @@ _SIGS = {
     "q355_rmsnorm_q8_1": [_P, _P, _P, _P, c_int, c_int, c_float, _P],
     "q355_gemv_q4_0_q8_1": [_P, _P, c_int, c_int, _P, _P, c_int, _P, _P, c_int, _P],
     "q355_gemv_blockdots": [_P, c_int, c_int, _P, c_int, _P, _P],
-    "q355_qkv_rope_kv": [_P, _P, c_int, _P, _P, c_float, _P, _P, _P, _P, _P, c_int, c_int, _P, _P, _P,
+    "q355_qkv_rope_kv": [_P, _P, c_int, _P, _P, c_double, _P, _P, _P, _P, _P, c_int, c_int, _P, _P, _P,
                          c_int, c_int, c_int, _P],
-    "q355_ffn_gate_up": [_P, _P, c_int, c_int, _P, _P, c_float, _P, c_int, _P],
+    "q355_ffn_gate_up": [_P, _P, c_int, c_int, _P, _P, c_double, _P, c_int, _P],
     "q355_ffn_down": [_P, _P, c_int, c_int, _P, _P, c_int, _P],
-    "q355_head_logits": [_P, _P, c_int, c_int, _P, _P, c_float, _P, _P, _P, c_int, _P],
+    "q355_head_logits": [_P, _P, c_int, c_int, _P, _P, c_double, _P, _P, _P, c_int, _P],
     "q355_head_nparts": [c_int],
     "q355_finish": [_P, _P, c_int, _P, _P, c_int, _P],
     "q355_embed_q4_0": [_P, _P, c_int, c_int, _P, _P, c_int, _P],
-    "q355_attn_decode": [_P, _P, _P, _P, _P, c_int, c_int, c_int, c_int, c_float, _P, _P, _P, _P, c_int, _P],
+    "q355_attn_decode": [_P, _P, _P, _P, _P, c_int, c_int, c_int, c_int, c_double, _P, _P, _P, _P, c_int, _P],
     "q355_attn_o_resid": [_P, _P, c_int, _P, c_int, _P, c_int, _P, c_int, _P],
-    "q355_rmsnorm_fix_q8_1": [_P, _P, _P, _P, c_int, c_int, c_float, _P],
+    "q355_rmsnorm_fix_q8_1": [_P, _P, _P, _P, c_int, c_int, c_double, _P],
     "q355_mmq_q4_0_q8_1": [_P, _P, c_int, c_int, _P, _P, c_int, c_int, _P, _P, _P, _P, _P, _P, _P],
     "q355_mmq_nparts": [c_int],
     "q355_qkv_finish": [_P, _P, _P, _P, _P, _P, c_int, c_int, _P, _P, _P, c_int, c_int, c_int, _P],

@@ -21,7 +21,7 @@ from dataclasses import dataclass, field
 import numpy as np
 
 from .hip import call, ptr
-from .qwen_model import PAGE, Config, DeviceModel
+from .qwen_model import FIX_SCALE, PAGE, Config, DeviceModel
 
 
 @dataclass(frozen=True)
@@ -90,7 +90,7 @@ class BatchedDecoder:
         self.mds = torch.zeros(B, c.FFN // 32, 2, dtype=torch.float16, device=dev)
         self.qkv_acc = torch.zeros(B, c.nqkv, dtype=torch.int64, device=dev)
         self.q = torch.zeros(B, c.NH * c.HD, dtype=torch.float16, device=dev)
-        self.part = torch.zeros(B, c.NH, self.max_chunks, c.HD + 2, dtype=torch.float32, device=dev)
+        self.part = torch.zeros(B, c.NH, self.max_chunks, c.HD + 2, dtype=torch.float64, device=dev)
         self.aq = torch.zeros(B, c.NH * c.HD, dtype=torch.int8, device=dev)
         self.ads = torch.zeros(B, c.NH * c.HD // 32, 2, dtype=torch.float16, device=dev)
         self.logits = torch.zeros(B, c.V, dtype=torch.float32, device=dev)
@@ -103,7 +103,7 @@ class BatchedDecoder:
 
     def h_f32(self):
         import torch
-        return (self.h.to(torch.float64) * 2.0 ** -32).to(torch.float32)
+        return (self.h.to(torch.float64) / FIX_SCALE).to(torch.float32)
 
     def _norm(self, w):
         c = self.cfg

@@ -8,8 +8,10 @@ scripts/qwen_gguf.py:63-144) re-cut for gfx950 into 5 fused launches per layer:
   attn_o_resid  merge of the partials + Q8_1 + O GEMV (3 K slices), h += ...
   ffn_gate_up   RMSNorm(ln2) + Q8_1 + gate_up GEMV + SwiGLU -> m (fp32)
   ffn_down      Q8_1(m) + down GEMV (4 K slices), h += ...
-The residual stream h is int64 fixed point (value * 2^32): the K-sliced projections add into it with
-integer atomics, so results do not depend on workgroup timing.
+The residual stream h is int64 fixed point (value * 2^48): the K-sliced projections add into it with
+integer atomics, so results do not depend on workgroup timing. GEMV accumulation, RMSNorm, RoPE, attention
+and SwiGLU run in f64 on this batch-1 path, so every Q8_1 quantizer input agrees with the f64 oracle to
+~1e-14 and greedy decoding reproduces the oracle's tokens.
 then head_logits (final RMSNorm + tied Q4_0 head + per-workgroup argmax partials) and finish
 (argmax, tok <- idx, pos += 1). The whole step is captured once in a torch.cuda.CUDAGraph (a hipGraph)
 and replayed per token, as run_fused does (scripts/qwen_fused.py:148-180).
@@ -27,6 +29,7 @@ from . import gguf
 from .hip import call, ptr
 
 PAGE = 64
+FIX_SCALE = 2.0 ** 48        # residual stream: int64 fixed point, value * 2^48
 
 
 @dataclass(frozen=True)
@@ -165,28 +168,32 @@ class Decoder:
         # sequence j owns pages [j*max_chunks, (j+1)*max_chunks) (identity block table; paged layout)
         self.block_table = torch.arange(n_pages, dtype=torch.int32, device=dev).reshape(T, self.max_chunks)
         H = cfg.H
-        self.h = torch.zeros(T, H, dtype=torch.int64, device=dev)       # fixed point, value * 2^32
+        self.h = torch.zeros(T, H, dtype=torch.int64, device=dev)       # fixed point, value * 2^48
         self.q = torch.zeros(T, cfg.NH * cfg.HD, dtype=torch.float16, device=dev)
         self.mlp = torch.zeros(T, cfg.FFN, dtype=torch.float32, device=dev)
         self.logits = torch.zeros(T, cfg.V, dtype=torch.float32, device=dev)
         self.nparts = call("q355_head_nparts", cfg.V)
         self.pmax = torch.zeros(T, self.nparts, dtype=torch.float32, device=dev)
         self.pidx = torch.zeros(T, self.nparts, dtype=torch.int32, device=dev)
-        self.part = torch.zeros(T, cfg.NH, self.max_chunks, cfg.HD + 2, dtype=torch.float32, device=dev)
+        self.part = torch.zeros(T, cfg.NH, self.max_chunks, cfg.HD + 2, dtype=torch.float64, device=dev)
         self.tok = torch.zeros(T, dtype=torch.int32, device=dev)
         self.pos = torch.zeros(T, dtype=torch.int32, device=dev)
         self.scale = 1.0 / math.sqrt(cfg.HD)
 
     # -- residual stream as fp32 (host-side views for tests and debugging) --
+    def h_f64(self):
+        import torch
+        return self.h.to(torch.float64) / FIX_SCALE
+
     def h_f32(self):
         import torch
-        return (self.h.to(torch.float64) * 2.0 ** -32).to(torch.float32)
+        return self.h_f64().to(torch.float32)
 
     def set_h(self, h):
         """Set the residual stream from fp32 values [T, H] (numpy or torch)."""
         import torch
         t = torch.as_tensor(np.asarray(h, np.float32)).to(self.h.device)
-        self.h.copy_(torch.round(t.to(torch.float64) * 2.0 ** 32).to(torch.int64))
+        self.h.copy_(torch.round(t.to(torch.float64) * FIX_SCALE).to(torch.int64))
 
     # -- per-layer ops (each is one library call) --
     def layer(self, i: int):

@@ -12,7 +12,7 @@
  *   Q8_1 activations [T, K]: xq int8 [T][K], xds half2 [T][K/32] = (d, s = d * sum q).
  *   KV cache (per layer): fp16 [n_pages][nkv][64][128]; block_table int32 [n_seq][bt_stride] page ids.
  *   RoPE tables: fp32 [maxlen][64] (cos, sin). Token positions and ids are int32.
- *   Residual stream h [T][H]: int64 fixed point, value = h * 2^-32 (|h| < 2^31). K-split projections add
+ *   Residual stream h [T][H]: int64 fixed point, value = h * 2^-48 (|h| < 2^15). K-split projections add
  *   into it with integer atomics, so every result is bitwise independent of workgroup timing.
  *
  * Each declaration names the reference interface it replaces (paths relative to the reference
@@ -62,14 +62,14 @@ int q355_gemv_blockdots(const uint8_t* qs, int N, int K, const int8_t* xq, int T
  * bias in the same order. Replaces RMSNORM_F32W_1P + gemv_source('biasf') + the RoPE/KV-write head of
  * ATTN4 (lab/qwen_kernels.py:33, 517-546) and gemm 'biasf_kv' (lab/qwen_batched.py:1316-1362).
  * Token j (j < T <= 4) is at position pos[j] of sequence j * seq_stride. K <= 1536. */
-int q355_qkv_rope_kv(const uint8_t* qs, const void* d, int K, const int64_t* h, const float* nw, float eps,
+int q355_qkv_rope_kv(const uint8_t* qs, const void* d, int K, const int64_t* h, const float* nw, double eps,
                      const float* bias, const float* rope_cos, const float* rope_sin, const int32_t* pos,
                      const int32_t* block_table, int bt_stride, int seq_stride, void* kcache, void* vcache,
                      void* qout, int nh, int nkv, int T, void* stream);
 
 /* Fused ln2 RMSNorm + Q8_1 + gate_up GEMV (rows interleaved gate, up) + SwiGLU: m fp32 [T][N2/2].
  * Replaces gemv_source('swiglu') (lab/qwen_kernels.py:21-28). K <= 1536. */
-int q355_ffn_gate_up(const uint8_t* qs, const void* d, int N2, int K, const int64_t* h, const float* nw, float eps,
+int q355_ffn_gate_up(const uint8_t* qs, const void* d, int N2, int K, const int64_t* h, const float* nw, double eps,
                      float* m, int T, void* stream);
 
 /* Fused Q8_1 of m + down GEMV + residual: h[T][N] += Wd . Q8_1(m) (4 K slices, fixed-point atomics).
@@ -80,7 +80,7 @@ int q355_ffn_down(const uint8_t* qs, const void* d, int N, int K, const float* m
 /* Final RMSNorm + Q8_1 + tied Q4_0 head: logits fp32 [T][V] and per-workgroup (max, lowest index)
  * partials pmax/pidx [T][q355_head_nparts(V)]. Replaces gemv_q6_source / 'logits'
  * (lab/qwen_kernels.py:608-678, 36) and the first stage of FINISH_MB (250-270). */
-int q355_head_logits(const uint8_t* qs, const void* d, int V, int K, const int64_t* h, const float* nw, float eps,
+int q355_head_logits(const uint8_t* qs, const void* d, int V, int K, const int64_t* h, const float* nw, double eps,
                      float* logits, float* pmax, int32_t* pidx, int T, void* stream);
 int q355_head_nparts(int V);
 
@@ -95,27 +95,27 @@ int q355_embed_q4_0(const uint8_t* qs, const void* d, int V, int H, const int32_
                     void* stream);
 
 /* Decode GQA attention, split-K over 64-position pages: token j attends to positions 0..pos[j] of its
- * sequence (block_table row j). Writes the unnormalised partials part fp32 [T][nh][max_chunks][130]
+ * sequence (block_table row j), in f64. Writes the unnormalised partials part f64 [T][nh][max_chunks][130]
  * (o[128], running max, sum) of every live chunk; max_chunks >= (max pos)/64 + 1, <= 64.
  * If oq/ods are given it also merges them (second launch): Q8_1 oq int8 [T][nh*128], ods half2
  * [T][nh*4], and optionally fp32 o32 [T][nh*128]. GQA group nh/nkv in {4, 6, 8}.
  * Replaces ATTN2 / ATTN4 (lab/qwen_kernels.py:358-442, 517-605). */
 int q355_attn_decode(const void* q, const void* kcache, const void* vcache, const int32_t* pos,
-                     const int32_t* block_table, int bt_stride, int nh, int nkv, int max_chunks, float scale,
-                     float* part, int8_t* oq, void* ods, float* o32, int T, void* stream);
+                     const int32_t* block_table, int bt_stride, int nh, int nkv, int max_chunks, double scale,
+                     double* part, int8_t* oq, void* ods, float* o32, int T, void* stream);
 
 /* Fused attention merge + Q8_1 + O-projection GEMV + residual: h[T][N] += Wo . Q8_1(merge(part))
  * (3 K slices of nh/3 heads, fixed-point atomics). part / max_chunks / pos as written by
  * q355_attn_decode; nh % 3 == 0, K = nh * 128 <= 1536.
  * Replaces the ATTN2 last-block combine (lab/qwen_kernels.py:424-440) + gemv_source('resid') for o (:34). */
-int q355_attn_o_resid(const uint8_t* qs, const void* d, int N, const float* part, int max_chunks,
+int q355_attn_o_resid(const uint8_t* qs, const void* d, int N, const double* part, int max_chunks,
                       const int32_t* pos, int nh, int64_t* h, int T, void* stream);
 
 /* ---- int8 MFMA path: batched decode (config 3) and prefill (config 4) ---- */
 
 /* RMSNorm of the fixed-point residual stream -> Q8_1 (one token per workgroup).
  * Replaces rmsnorm_q8_source (lab/qwen_batched.py:1044-1091) / RMSNORM_F32W_1P batched by blockIdx.y. */
-int q355_rmsnorm_fix_q8_1(const int64_t* h, const float* w, int8_t* xq, void* xds, int T, int H, float eps,
+int q355_rmsnorm_fix_q8_1(const int64_t* h, const float* w, int8_t* xq, void* xds, int T, int H, double eps,
                           void* stream);
 
 /* Q4_0 x Q8_1 product of T tokens on v_mfma_i32_16x16x32_i8 (exact int32 block dots), N % 64 == 0.

@@ -19,8 +19,9 @@ with this build's operand formats (Q8_1 activations, fp16 KV cache, tied Q4_0 em
   logits = E Q8_1(rmsnorm(h) * norm); tok = argmax (lowest index wins ties); pos += 1
                                                FINISH / FINISH_MB (lab/qwen_kernels.py:222-282)
 
-Storage points follow the product: h, logits, att, m are fp32; q, K, V are fp16; every GEMV input
-is Q8_1. Arithmetic inside an op is float64 (the ideal value of the quantized operands).
+Rounding points follow the product: every GEMV input is Q8_1 of an fp32 value (x, att, m), q/K/V are
+rounded f64 -> fp16 once (round to nearest even), logits are fp32; everything else (GEMV outputs, the residual stream h,
+RMSNorm, RoPE, attention, SwiGLU) is float64.
 GEMVs use gemv_q4_0_q8_1 semantics; mode "f64" computes them as a float64 BLAS product of the
 exactly dequantized operands (identical mathematics, pinned against the int32 block-dot form on
 small shapes), which makes full-model runs practical on the CPU.
@@ -139,12 +140,12 @@ class Linear:
         return self._w
 
     def __call__(self, x: np.ndarray) -> np.ndarray:
-        """x fp32 [T, K] -> quantize Q8_1 -> y fp32 [T, N]."""
+        """x fp32 [T, K] -> quantize Q8_1 -> y float64 [T, N]."""
         qx, dx, _ = Q.quantize_q8_1(np.asarray(x, np.float32))
         if self.mode == "int":
-            return Q.gemv_q4_0_q8_1(self.b, self.N, self.K, qx, dx)
+            return Q.gemv_q4_0_q8_1(self.b, self.N, self.K, qx, dx, out_dtype=np.float64)
         xf = Q.dequant_q8_1(qx, dx).astype(np.float64)
-        return (xf @ self.dense().T).astype(np.float32)
+        return xf @ self.dense().T
 
 
 @dataclass
@@ -180,7 +181,7 @@ class Model:
         return np.stack(rows).astype(np.float32)
 
     def layer(self, i: int, h: np.ndarray, pos0: int, cache) -> np.ndarray:
-        """One decoder layer for P tokens at positions pos0..pos0+P-1 of one sequence; h fp32 [P, H] -> new h.
+        """One decoder layer for P tokens at positions pos0..pos0+P-1 of one sequence; h [P, H] -> new h (float64).
         Writes the layer's K/V rows into cache["K"][i], cache["V"][i]."""
         c = self.cfg
         L, lin = self.w["layers"][i], self.lin[i]
@@ -193,23 +194,23 @@ class Model:
         for t in range(P):
             p = pos0 + t
             cs, sn = self.cos[p], self.sin[p]
-            qh[t] = rope(q[t].reshape(c.NH, c.HD), cs, sn).astype(np.float32).astype(np.float16)
-            cache["K"][i, :, p] = rope(k[t].reshape(c.NKV, c.HD), cs, sn).astype(np.float32).astype(np.float16)
+            qh[t] = rope(q[t].reshape(c.NH, c.HD), cs, sn).astype(np.float16)
+            cache["K"][i, :, p] = rope(k[t].reshape(c.NKV, c.HD), cs, sn).astype(np.float16)
             cache["V"][i, :, p] = v[t].reshape(c.NKV, c.HD).astype(np.float16)
         if P == 1:
             att = attn_decode(qh[0], cache["K"][i], cache["V"][i], pos0 + 1, c.NH, c.NKV)[None]
         else:
             att = attn_prefill(qh, cache["K"][i], cache["V"][i], pos0, c.NH, c.NKV)
         self.last = {"q": qh, "att": att}
-        h = (h.astype(np.float64) + lin["o"](att)).astype(np.float32)
+        h = np.asarray(h, np.float64) + lin["o"](att)
         x = rmsnorm(h, L["ln2"], c.eps).astype(np.float32)
         m = silu_mul(lin["g"](x), lin["u"](x)).astype(np.float32)
         self.last["m"] = m
-        return (h.astype(np.float64) + lin["d"](m)).astype(np.float32)
+        return h + lin["d"](m)
 
     def forward(self, toks, pos0: int, cache) -> np.ndarray:
         """P tokens at positions pos0..pos0+P-1 of one sequence (P = 1: decode step; P > 1: prefill).
-        Writes K/V rows into `cache`; returns the final hidden state h fp32 [P, H]."""
+        Writes K/V rows into `cache`; returns the final hidden state h float64 [P, H]."""
         h = self.embed(toks)
         for i in range(len(self.w["layers"])):
             h = self.layer(i, h, pos0, cache)
@@ -218,7 +219,7 @@ class Model:
     def logits(self, h: np.ndarray) -> np.ndarray:
         """Final RMSNorm + tied Q4_0 head -> fp32 [T, V]."""
         x = rmsnorm(h, self.w["norm"], self.cfg.eps).astype(np.float32)
-        return self.head(x)
+        return self.head(x).astype(np.float32)
 
     def greedy(self, prompt, n_gen: int, cache=None):
         """Prefill the prompt (one forward over all prompt tokens), then n_gen greedy decode steps.

@@ -97,8 +97,10 @@ def block_dots(qw: np.ndarray, qx: np.ndarray) -> np.ndarray:
     return np.einsum("nbi,tbi->tnb", a, b, optimize=True).astype(np.int32)
 
 
-def gemv_q4_0_q8_1(wbytes: np.ndarray, N: int, K: int, qx: np.ndarray, dx: np.ndarray) -> np.ndarray:
-    """Y[T, N] = sum_b d_w[n,b] d_x[t,b] (dot_b - 8 sum(q_x,b)), accumulated in float64, returned fp32.
+def gemv_q4_0_q8_1(wbytes: np.ndarray, N: int, K: int, qx: np.ndarray, dx: np.ndarray,
+                   out_dtype=np.float32) -> np.ndarray:
+    """Y[T, N] = sum_b d_w[n,b] d_x[t,b] (dot_b - 8 sum(q_x,b)), accumulated in float64 (each term is exact),
+    returned as out_dtype (fp32 by default).
     wbytes: GGUF Q4_0 bytes of W [N, K] (row-major); qx int8 [T, K], dx fp16 [T, K/32].
     pinned by: equality (to fp64 rounding) with the dequantize-then-matmul form
     (d_w (q_w - 8)) @ (d_x q_x)^T, which has no int32 dot and no -8 sum(q) correction term."""
@@ -110,7 +112,7 @@ def gemv_q4_0_q8_1(wbytes: np.ndarray, N: int, K: int, qx: np.ndarray, dx: np.nd
     sq = qx.reshape(T, K // QK, QK).astype(np.int64).sum(axis=2)    # [T, nb]
     sumi = dots - 8 * sq[:, None, :]
     y = np.einsum("tnb,nb,tb->tn", sumi.astype(np.float64), dw, dx.astype(np.float64), optimize=True)
-    return y.astype(np.float32)
+    return y.astype(out_dtype)
 
 
 def gemv_dequant_f64(wbytes: np.ndarray, N: int, K: int, qx: np.ndarray, dx: np.ndarray) -> np.ndarray:

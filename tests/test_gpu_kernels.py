@@ -246,7 +246,7 @@ def test_attn_decode(cuda, positions):
     bt = rng.permutation(n_pages).astype(np.int32).reshape(T, max_chunks)   # scattered pages
     q = (rng.standard_normal((T, c.NH * c.HD)) * 2).astype(np.float16)
     pos = np.array(positions, np.int32)
-    part = torch.zeros(T, c.NH, max_chunks, c.HD + 2, device=cuda)
+    part = torch.zeros(T, c.NH, max_chunks, c.HD + 2, dtype=torch.float64, device=cuda)
     oq = torch.zeros(T, c.NH * c.HD, dtype=torch.int8, device=cuda)
     ods = torch.zeros(T, c.NH * c.HD // 32, 2, dtype=torch.float16, device=cuda)
     o32 = torch.zeros(T, c.NH * c.HD, device=cuda)
@@ -264,12 +264,12 @@ def test_attn_decode(cuda, positions):
     # fused merge + Q8_1 + O projection + residual (the decode path) against the merged output
     W, b = mat_dev(c.H, c.NH * c.HD, seed=31)
     h0 = rng.standard_normal((T, c.H), dtype=np.float32)
-    h = to_dev(np.round(h0.astype(np.float64) * 2.0 ** 32).astype(np.int64))
+    h = to_dev(np.round(h0.astype(np.float64) * QM.FIX_SCALE).astype(np.int64))
     call("q355_attn_o_resid", ptr(W.qs), ptr(W.d), c.H, ptr(part), max_chunks, ptr(to_dev(pos)), c.NH, ptr(h), T)
     sync()
     rq, rd, _ = OQ.quantize_q8_1(o32.cpu().numpy())
     ref = OQ.gemv_q4_0_q8_1(b, c.H, c.NH * c.HD, rq, rd)
-    assert relerr(h.cpu().numpy() * 2.0 ** -32 - h0, ref) < REL
+    assert relerr(h.cpu().numpy() / QM.FIX_SCALE - h0, ref) < REL
 
 
 def test_finish_ties(cuda):

@@ -70,10 +70,10 @@ def test_mmq_resid_fix(cuda, N, K, T):
     x = rng.standard_normal((T, K), dtype=np.float32)
     xq, xds, q, d = q8(x)
     h0 = rng.standard_normal((T, N), dtype=np.float32)
-    h = dev(np.round(h0.astype(np.float64) * 2.0 ** 32).astype(np.int64))
+    h = dev(np.round(h0.astype(np.float64) * QM.FIX_SCALE).astype(np.int64))
     call("q355_mmq_q4_0_q8_1", ptr(W.qs), ptr(W.d), N, K, ptr(xq), ptr(xds), T, 6, None, ptr(h), None, None, None, None)
     sync()
-    got = h.cpu().numpy() * 2.0 ** -32 - h0
+    got = h.cpu().numpy() / QM.FIX_SCALE - h0
     assert relerr(got, OQ.gemv_q4_0_q8_1(b, N, K, q, d)) < REL
 
 
