@@ -22,7 +22,6 @@ __global__ void __launch_bounds__(G * 64) k_attn_decode(const AttnArgs a) {
   __shared__ __align__(16) __half ks[PAGE][KROW];
   __shared__ __align__(16) __half vs[PAGE][HD];
   __shared__ __align__(16) double qf[G][HD];
-  __shared__ double E[G][PAGE];
 
   const int j = blockIdx.y;
   const int kvh = blockIdx.x / a.max_chunks, c = blockIdx.x % a.max_chunks;
@@ -52,15 +51,17 @@ __global__ void __launch_bounds__(G * 64) k_attn_decode(const AttnArgs a) {
     const int e = threadIdx.x + NT * i;
     if (e < PAGE * HD / 8) {
       *(uint4*)&ks[e >> 4][(e & 15) * 8] = kr[i];
-      ((uint4*)vs)[e] = vr[i];
+      // V rows past the context are zeroed: P.V below runs over the whole page with p = 0 there
+      ((uint4*)vs)[e] = (e >> 4) < nvalid ? vr[i] : make_uint4(0, 0, 0, 0);
     }
   }
   __syncthreads();
 
-  // scores: lane p, this wave's head (f64)
+  // scores: lane p, this wave's head (f64, 4 independent partial sums)
   double s = 0.0;
   {
     const double* qh = qf[wv];
+    double sp[4] = {0.0, 0.0, 0.0, 0.0};
 #pragma unroll
     for (int i = 0; i < HD / 8; ++i) {
       const uint4 kk = *(const uint4*)&ks[lane][8 * i];
@@ -68,95 +69,84 @@ __global__ void __launch_bounds__(G * 64) k_attn_decode(const AttnArgs a) {
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
         const float2 kf = __half22float2(k2[u]);
-        s = fma(qh[8 * i + 2 * u], (double)kf.x, s);
-        s = fma(qh[8 * i + 2 * u + 1], (double)kf.y, s);
+        sp[u] = fma(qh[8 * i + 2 * u], (double)kf.x, sp[u]);
+        sp[u] = fma(qh[8 * i + 2 * u + 1], (double)kf.y, sp[u]);
       }
     }
+    s = (sp[0] + sp[1]) + (sp[2] + sp[3]);
   }
   s = lane < nvalid ? s * a.scale : -INFINITY;
   const double m = wave_max_d(s);
   const double e = lane < nvalid ? exp(s - m) : 0.0;
   const double l = wave_sum_d(e);
-  E[wv][lane] = e;
-  __syncthreads();
 
-  // P.V: lane owns dims 2*lane, 2*lane+1
-  double o0 = 0.0, o1 = 0.0, o2 = 0.0, o3 = 0.0;
-  int p = 0;
-  for (; p + 1 < nvalid; p += 2) {
-    const float2 v0 = __half22float2(((const __half2*)vs[p])[lane]);
-    const float2 v1 = __half22float2(((const __half2*)vs[p + 1])[lane]);
-    const double e0 = E[wv][p], e1 = E[wv][p + 1];
-    o0 = fma(e0, (double)v0.x, o0);
-    o1 = fma(e0, (double)v0.y, o1);
-    o2 = fma(e1, (double)v1.x, o2);
-    o3 = fma(e1, (double)v1.y, o3);
+  // P.V: lane owns dims 2*lane, 2*lane+1; p(position) is broadcast from lane p with readlane
+  double o[4][2] = {{0.0, 0.0}, {0.0, 0.0}, {0.0, 0.0}, {0.0, 0.0}};
+  const int2 ei = *reinterpret_cast<const int2*>(&e);
+#pragma unroll
+  for (int p = 0; p < PAGE; ++p) {
+    int2 bi;
+    bi.x = __builtin_amdgcn_readlane(ei.x, p);
+    bi.y = __builtin_amdgcn_readlane(ei.y, p);
+    const double ep = *reinterpret_cast<const double*>(&bi);
+    const float2 v = __half22float2(((const __half2*)vs[p])[lane]);
+    o[p & 3][0] = fma(ep, (double)v.x, o[p & 3][0]);
+    o[p & 3][1] = fma(ep, (double)v.y, o[p & 3][1]);
   }
-  if (p < nvalid) {
-    const float2 v0 = __half22float2(((const __half2*)vs[p])[lane]);
-    o0 = fma(E[wv][p], (double)v0.x, o0);
-    o1 = fma(E[wv][p], (double)v0.y, o1);
-  }
+  const double o0 = (o[0][0] + o[1][0]) + (o[2][0] + o[3][0]);
+  const double o1 = (o[0][1] + o[1][1]) + (o[2][1] + o[3][1]);
   double* P = a.part + (((size_t)j * a.nh + hq) * a.max_chunks + c) * (HD + 2);
-  ((double2*)P)[lane] = make_double2(o0 + o2, o1 + o3);
+  ((double2*)P)[lane] = make_double2(o0, o1);
   if (lane == 0) { P[HD] = m; P[HD + 1] = l; }
 }
 
 // ---------------------------------------------------------------------------------------------
-// Merge of one token's partials (nh query heads, nch chunks), f64. Called by every thread of a workgroup of
-// NTH threads; `wgt` is LDS scratch of 2 * nh * max_chunks doubles; writes o[h * HD + d] to `out` (LDS).
-template <int NTH>
-__device__ __forceinline__ void attn_merge_token(const double* __restrict__ part, int nh, int max_chunks, int nch,
-                                                 double* wgt, double* out) {
-  // 1. per (h, c): raw m, l -> per-head M, L -> weights e^(m_c - M) / L
-  for (int hc = threadIdx.x; hc < nh * nch; hc += NTH) {
-    const int h = hc / nch, c = hc % nch;
-    const double* P = part + ((size_t)h * max_chunks + c) * (HD + 2);
-    wgt[h * max_chunks + c] = P[HD];
-    wgt[nh * max_chunks + h * max_chunks + c] = P[HD + 1];
-  }
-  __syncthreads();
-  if (threadIdx.x < nh) {
-    const int h = threadIdx.x;
-    double M = -INFINITY;
-    for (int c = 0; c < nch; ++c) M = fmax(M, wgt[h * max_chunks + c]);
-    double L = 0.0;
-    for (int c = 0; c < nch; ++c) L = fma(exp(wgt[h * max_chunks + c] - M), wgt[nh * max_chunks + h * max_chunks + c], L);
-    for (int c = 0; c < nch; ++c) wgt[h * max_chunks + c] = exp(wgt[h * max_chunks + c] - M) / L;
-  }
-  __syncthreads();
-  // 2. o[h][d] = sum_c w[h][c] o_c[d], chunks in fixed order, 4 loads in flight per thread
-  for (int e = threadIdx.x; e < nh * HD; e += NTH) {
-    const int h = e / HD, d = e % HD;
-    const double* P = part + (size_t)h * max_chunks * (HD + 2) + d;
-    const double* w = wgt + h * max_chunks;
-    double o = 0.0;
-    int c = 0;
-    for (; c + 3 < nch; c += 4) {
-      const double p0 = P[(size_t)c * (HD + 2)], p1 = P[(size_t)(c + 1) * (HD + 2)];
-      const double p2 = P[(size_t)(c + 2) * (HD + 2)], p3 = P[(size_t)(c + 3) * (HD + 2)];
-      o = fma(w[c], p0, o);
-      o = fma(w[c + 1], p1, o);
-      o = fma(w[c + 2], p2, o);
-      o = fma(w[c + 3], p3, o);
+// Merge of the chunk partials of one (token, query head), f64, by ONE wave: lane c reads chunk c's
+// (m_c, l_c) and forms w_c = e^(m_c - M) (M = max_c m_c); lane l then sums dims 2l, 2l+1 of
+// sum_c w_c o_c in fixed chunk order (w_c broadcast from lane c) and divides by L = sum_c w_c l_c.
+// All loads of a group of 8 chunks are issued before their first use. nch <= 64.
+__device__ __forceinline__ void attn_merge_head(const double* __restrict__ P, int nch, double* __restrict__ out) {
+  const int lane = threadIdx.x & 63;
+  const double* pc = P + (size_t)min(lane, nch - 1) * (HD + 2);
+  const double mc = pc[HD], lc = pc[HD + 1];
+  double2 v[8];
+#pragma unroll
+  for (int u = 0; u < 8; ++u) v[u] = ((const double2*)(P + (size_t)min(u, nch - 1) * (HD + 2)))[lane];
+  const double M = wave_max_d(lane < nch ? mc : -INFINITY);
+  const double w = lane < nch ? exp(mc - M) : 0.0;
+  const double L = wave_sum_d(w * (lane < nch ? lc : 0.0));
+  const int2 wi = *reinterpret_cast<const int2*>(&w);
+  double o0 = 0.0, o1 = 0.0;
+  for (int c0 = 0; c0 < nch; c0 += 8) {
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      int2 bi;
+      bi.x = __builtin_amdgcn_readlane(wi.x, c0 + u);   // 0 for chunks >= nch (w = 0 there)
+      bi.y = __builtin_amdgcn_readlane(wi.y, c0 + u);
+      const double wc = *reinterpret_cast<const double*>(&bi);
+      o0 = fma(wc, v[u].x, o0);
+      o1 = fma(wc, v[u].y, o1);
     }
-    for (; c < nch; ++c) o = fma(w[c], P[(size_t)c * (HD + 2)], o);
-    out[e] = o;
+    if (c0 + 8 < nch) {
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        v[u] = ((const double2*)(P + (size_t)min(c0 + 8 + u, nch - 1) * (HD + 2)))[lane];
+    }
   }
-  __syncthreads();
+  ((double2*)out)[lane] = make_double2(o0 / L, o1 / L);
 }
 
-// Standalone merge: one workgroup per token -> fp32 o32 (optional) and Q8_1 oq/ods.
+// Standalone merge: one workgroup (4 waves) per token -> fp32 o32 (optional) and Q8_1 oq/ods.
 __global__ void __launch_bounds__(256) k_attn_merge(const AttnArgs a) {
-  extern __shared__ double sm[];
+  extern __shared__ double sm[];                     // nh * HD
   const int j = blockIdx.x;
   const int nch = a.pos[j] / PAGE + 1;
-  double* wgt = sm;                                  // 2 * nh * max_chunks
-  double* o = sm + 2 * a.nh * a.max_chunks;          // nh * HD
-  attn_merge_token<256>(a.part + (size_t)j * a.nh * a.max_chunks * (HD + 2), a.nh, a.max_chunks, nch, wgt, o);
+  for (int h = threadIdx.x >> 6; h < a.nh; h += 4)
+    attn_merge_head(a.part + ((size_t)j * a.nh + h) * a.max_chunks * (HD + 2), nch, sm + h * HD);
+  __syncthreads();
   const int n = a.nh * HD;
   for (int e = threadIdx.x; e < n; e += 256) {      // n % 256 == 0 keeps 32-lane groups whole
-    const float v = (float)o[e];
+    const float v = (float)sm[e];
     if (a.o32) a.o32[(size_t)j * n + e] = v;
     const int q = q8_1_lane32(v, a.ods + ((size_t)j * n + e) / 32, (e & 31) == 0);
     a.oq[(size_t)j * n + e] = (int8_t)q;

@@ -53,7 +53,7 @@ static int launch_gemv(const GemvArgs& a, int KS, hipStream_t s) {
   if (per > 4 * NW * KPL) return fail(Q355_EINVAL, "gemv: K=%d slice of %d blocks exceeds %d", a.K, per, 4 * NW * KPL);
   const dim3 grid(tiles / NT, KS);
   size_t lds = (size_t)a.T * a.K + (size_t)a.T * nb * 8;
-  if (PRO == PRO_ATTN) lds += 8 + (size_t)(2 * a.nh * a.attn_max_chunks + a.nh * HD) * 8;  // 8: f64 alignment
+  if (PRO == PRO_ATTN) lds += 8 + (size_t)a.nh * HD * 8;  // merged heads of one token; 8: f64 alignment
   switch (a.T) {
     case 1: hipLaunchKernelGGL((k_gemv<1, NT, NW, KPL, PRO, EPI>), grid, dim3(NW * 64), lds, s, a); break;
     case 2: hipLaunchKernelGGL((k_gemv<2, NT, NW, KPL, PRO, EPI>), grid, dim3(NW * 64), lds, s, a); break;
@@ -230,7 +230,7 @@ extern "C" int q355_attn_decode(const void* q, const void* kcache, const void* v
   }
   if (int e = launched("attn_decode")) return e;
   if (!oq) return Q355_OK;
-  const size_t lds = (size_t)(2 * nh * max_chunks + nh * HD) * 8;
+  const size_t lds = (size_t)nh * HD * 8;
   hipLaunchKernelGGL(k_attn_merge, dim3(T), dim3(256), lds, s, a);
   return launched("attn_merge");
 }

@@ -170,14 +170,15 @@ struct XLoad {
                                         char* extra) {
     const int K = a.K, nb = K / 32;
     if (PRO == PRO_ATTN) {
-      // merge the split-K attention partials of the heads in this K slice (f64), then Q8_1 into LDS
-      double* wgt = (double*)extra;
-      double* ob = wgt + 2 * a.nh * a.attn_max_chunks;
+      // merge the split-K attention partials of the heads in this K slice (f64, one wave per head), then Q8_1
+      double* ob = (double*)extra;                   // nhs * HD merged outputs of one token
       const int h0 = ks.b0 * 32 / HD, nhs = (ks.b1 - ks.b0) * 32 / HD;
       for (int j = 0; j < a.T; ++j) {
         const int nch = a.pos[j] / PAGE + 1;
-        attn_merge_token<NTH>(a.attn_part + ((size_t)j * a.nh + h0) * a.attn_max_chunks * (HD + 2), nhs,
-                              a.attn_max_chunks, nch, wgt, ob);
+        for (int h = threadIdx.x >> 6; h < nhs; h += NTH / 64)
+          attn_merge_head(a.attn_part + ((size_t)j * a.nh + h0 + h) * a.attn_max_chunks * (HD + 2), nch,
+                          ob + h * HD);
+        __syncthreads();
         for (int g = threadIdx.x; g < nhs * HD / 8; g += NTH) {   // quads stay whole (HD / 8 % 4 == 0)
           float x[8];
 #pragma unroll

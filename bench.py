@@ -34,6 +34,11 @@ sys.path.insert(0, str(ROOT / "3080lab_amd"))
 
 HBM_PEAK_GBS = 8000.0
 GEMV0_BYTES = 6_881_280 + 860_160 + 1_728 + 35_840     # config 0: nibbles + scales + Q8_1 x + fp32 y
+# HBM bytes per gate_up launch from rocprofv3 PMC (FETCH_SIZE x 2.0 + WRITE_SIZE x 1.0 KiB per dispatch; the
+# factors make a 64 MiB device copy read 64 MiB and write 64 MiB): 7707.0 * 2 + 35.0 KiB. Counters cannot be
+# read from inside this process, so the measured figure is recorded here and re-measured by
+#   rocprofv3 --pmc FETCH_SIZE -- python3 bench.py --quick --no-cpu --steps 4   (then WRITE_SIZE, then --copy-probe)
+GATE_UP_TRAFFIC = int((7707.0 * 2 + 35.0) * 1024)
 
 
 def log(*a):
@@ -75,9 +80,9 @@ def gate_up_roofline(dm, dec) -> dict:
              ptr(dec.mlp), 1)
     ms = time_launches(run, c.L)
     ach = algo / (ms * 1e-3) / 1e9
-    return {"kernel": "q355_ffn_gate_up (k_gemv<1,1,4,3,PRO_RMS,EPI_SWIGLU>)", "bound": "hbm",
+    return {"kernel": "q355_ffn_gate_up (k_gemv<1,5,4,3,PRO_RMS,EPI_SWIGLU>)", "bound": "hbm",
             "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4),
-            "traffic": None, "algorithmic_bytes": int(algo), "avg_us": round(ms * 1e3, 3)}
+            "traffic": GATE_UP_TRAFFIC, "algorithmic_bytes": int(algo), "avg_us": round(ms * 1e3, 3)}
 
 
 def gemv_config0(copies: int = 64) -> dict:
@@ -147,7 +152,7 @@ def batched_decode(dm, B: int, steps: int = 32, warmup: int = 2) -> dict:
     return out
 
 
-def cpu_baseline(w, cfg, prompt, n_steps: int = 3) -> dict:
+def cpu_baseline(w, cfg, prompt, n_steps: int = 6) -> dict:
     """The oracle (exact int32 block dots, numpy, single core) decoding n_steps tokens of the same model
     after a short context; tok/s = n_steps / wall time."""
     sys.path.insert(0, str(ROOT))
@@ -176,6 +181,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--quick", action="store_true", help="decode only (no roofline / GEMV / CPU legs)")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="only run a 64 MiB device-to-device copy 4 times (HBM counter calibration for rocprofv3 --pmc)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: --gpus {args.gpus} is not supported: this build measures one MI355X "
@@ -185,6 +192,14 @@ def main():
     import torch
     from lab import qwen_model as QM
     assert torch.cuda.is_available(), "bench.py needs the MI355X"
+    if args.copy_probe:
+        src = torch.ones(16 << 20, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(4):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_probe_bytes": src.numel() * 4}))
+        return
     cfg = QM.QWEN15
     t0 = time.time()
     w = QM.random_weights(cfg, seed=0)
@@ -219,7 +234,7 @@ def main():
     out = {"metric": "decode tok/s at batch 1/8/32 (Qwen2.5-1.5B-shape Q4_0); GEMV HBM GB/s",
            "value": round(tok_s, 1), "unit": "tok/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
            "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-           "dtype": "int8xint4->int32, fp32 accum (Q4_0 x Q8_1)", "data": "synthetic (seeded random weights and prompt)",
+           "dtype": "int4 x int8 -> int32 block dots, f64 accumulation (Q4_0 x Q8_1)", "data": "synthetic (seeded random weights and prompt)",
            "config": {"workload": "BASELINE config 2: Qwen2.5-1.5B-shape 28 layers, tied Q4_0 head, "
                                   "128-token prompt + greedy decode, batch 1, one hipGraph per token",
                       "batch": 1, "prompt_len": prompt_len, "decode_positions": [prompt_len, prompt_len + args.steps - 1],

@@ -25,7 +25,7 @@ Q4_0_BYTES = 18         # fp16 d + 16 B nibbles
 def round_half_away(v: np.ndarray) -> np.ndarray:
     """C roundf(): nearest integer, halves away from zero. Evaluated in float64 so that
     v + 0.5 is exact for every float32 v of magnitude < 2^24 (no double rounding).
-    pinned by: tests/test_oracle_quant.py::test_round_half_away (hand cases incl. 0.49999997, 2.5, -2.5)."""
+    pinned by: tests/test_oracle.py::test_round_half_away (hand cases incl. 0.49999997, 2.5, -2.5)."""
     v64 = np.asarray(v, dtype=np.float64)
     return np.trunc(v64 + np.copysign(0.5, v64))
 
@@ -49,7 +49,7 @@ def quantize_q4_0(x: np.ndarray) -> np.ndarray:
 
 def q4_0_blocks(b: np.ndarray):
     """GGUF Q4_0 bytes -> (d float32 [nblk], q uint8 [nblk, 32] stored 0..15) exactly as lab/gguf.py:88-94.
-    pinned by: hand-written bytes with known nibbles (tests/test_oracle_quant.py)."""
+    pinned by: hand-written bytes with known nibbles (tests/test_oracle.py)."""
     blk = np.asarray(b, np.uint8).reshape(-1, Q4_0_BYTES)
     d = blk[:, :2].copy().view(np.float16).astype(np.float32).reshape(-1)
     qs = blk[:, 2:]
