@@ -304,7 +304,7 @@ extern "C" int q355_mmq_q4_0_q8_1(const uint8_t* qs, const void* d, int N, int K
     case 6: {
       REQUIRE(yfix, "mmq_q4_0_q8_1: resid_fix needs yfix");
       a.yfix = (long long*)yfix;
-      int KS = 384 / groups;
+      int KS = T >= 256 ? 1 : 384 / groups;           // prefill sizes have parallelism enough
       KS = KS < 1 ? 1 : (KS > nb / 4 ? nb / 4 : KS);
       if (KS < 1) KS = 1;
       return launch_mmq_tg<EPI_RESID_FIX>(a, KS, s);
@@ -337,4 +337,16 @@ extern "C" int q355_qkv_finish(int64_t* acc, const float* bias, const float* rop
   a.kcache = (__half*)kcache; a.vcache = (__half*)vcache; a.qout = (__half*)qout; a.nh = nh; a.nkv = nkv;
   hipLaunchKernelGGL(k_qkv_finish, dim3(T), dim3(256), 0, (hipStream_t)stream, a, (long long*)acc);
   return launched("qkv_finish");
+}
+
+extern "C" int q355_attn_prefill(const void* q, const void* kcache, const void* vcache, const int32_t* block_table,
+                                 int pos0, int P, int nh, int nkv, float scale, float* out, void* stream) {
+  REQUIRE(q && kcache && vcache && block_table && out, "attn_prefill: null pointer");
+  REQUIRE(P >= 1 && pos0 >= 0, "attn_prefill: P=%d pos0=%d", P, pos0);
+  REQUIRE(nh > 0 && nkv > 0 && nh % nkv == 0 && nh <= 65535, "attn_prefill: nh=%d nkv=%d", nh, nkv);
+  PrefillAttnArgs a = {};
+  a.q = (const __half*)q; a.kcache = (const __half*)kcache; a.vcache = (const __half*)vcache;
+  a.block_table = block_table; a.pos0 = pos0; a.P = P; a.nh = nh; a.nkv = nkv; a.scale = scale; a.out = out;
+  hipLaunchKernelGGL(k_attn_prefill, dim3((P + 63) / 64, nh), dim3(256), 0, (hipStream_t)stream, a);
+  return launched("attn_prefill");
 }

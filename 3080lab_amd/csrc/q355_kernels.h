@@ -73,6 +73,17 @@ struct GemvArgs {
   int* pidx;
 };
 
+// Causal prefill attention over one sequence's paged KV cache (keys 0 .. pos0 + P - 1 already written).
+struct PrefillAttnArgs {
+  const __half* q;             // [P][nh*HD] RoPE'd fp16 queries of positions pos0 .. pos0 + P - 1
+  const __half* kcache;        // [n_pages][nkv][PAGE][HD]
+  const __half* vcache;
+  const int* block_table;      // the sequence's page ids, >= (pos0 + P - 1) / PAGE + 1 entries
+  int pos0, P, nh, nkv;
+  float scale;
+  float* out;                  // [P][nh*HD] fp32
+};
+
 struct AttnArgs {
   const __half* q;             // [T][nh*HD] RoPE'd fp16 queries
   const __half* kcache;        // [n_pages][nkv][PAGE][HD]

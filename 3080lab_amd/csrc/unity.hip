@@ -1,4 +1,5 @@
 // Single translation unit of libqwen355.so (the kernel templates are instantiated by the C ABI layer).
 #include "gemv.hip"
 #include "mmq.hip"
+#include "flash.hip"
 #include "capi.hip"

@@ -35,6 +35,7 @@ _SIGS = {
     "q355_rmsnorm_fix_q8_1": [_P, _P, _P, _P, c_int, c_int, c_double, _P],
     "q355_mmq_q4_0_q8_1": [_P, _P, c_int, c_int, _P, _P, c_int, c_int, _P, _P, _P, _P, _P, _P, _P],
     "q355_mmq_nparts": [c_int],
+    "q355_attn_prefill": [_P, _P, _P, _P, c_int, c_int, c_int, c_int, c_float, _P, _P],
     "q355_qkv_finish": [_P, _P, _P, _P, _P, _P, c_int, c_int, _P, _P, _P, c_int, c_int, c_int, _P],
 }
 # entry points returning something other than an int status

@@ -188,3 +188,89 @@ class BatchedDecoder:
                 self.step()
             out.append(self.tok.clone())
         return torch.stack(out, 1).cpu().numpy()
+
+
+def flash_prefill_v3_source(maxlen: int = 4096, q8: bool = True) -> KernelSpec:
+    """Causal prefill flash attention (lab/qwen_batched.py:1795-2037) -> q355_attn_prefill (fp16 MFMA,
+    fp32 accumulation); its output is quantized to Q8_1 by QUANT_Q8 for the O projection."""
+    return KernelSpec("q355_attn_prefill")
+
+
+class Prefill:
+    """Chunked prefill of one sequence into a batch-1 Decoder's paged KV cache (scripts/qwen_prefill.py:196-246).
+
+    chunk(ids, pos0) runs P prompt tokens at positions pos0 .. pos0 + P - 1 through all layers at once:
+      embed -> per layer: rmsnorm_fix_q8_1, MMQ qkv (int64 accumulator), qkv_finish (bias, RoPE, K/V write),
+      attn_prefill (causal, fp16 MFMA), quant_q8_1, MMQ o (+= h), rmsnorm_fix_q8_1, MMQ gate_up (SwiGLU -> Q8_1),
+      MMQ down (+= h) -> final norm + head on the last token -> dec.tok = argmax, dec.pos = pos0 + P.
+    The decoder then continues greedy decode from that state."""
+
+    def __init__(self, dec, max_chunk: int = 2048):
+        import torch
+        m, c = dec.m, dec.cfg
+        assert dec.T == 1, "prefill fills sequence 0 of a batch-1 decoder"
+        self.dec, self.m, self.cfg, self.P_max = dec, m, c, max_chunk
+        dev = m.device
+        P, H = max_chunk, c.H
+        self.h = torch.zeros(P, H, dtype=torch.int64, device=dev)
+        self.xq = torch.zeros(P, max(H, c.FFN), dtype=torch.int8, device=dev)
+        self.xds = torch.zeros(P, max(H, c.FFN) // 32, 2, dtype=torch.float16, device=dev)
+        self.qkv_acc = torch.zeros(P, c.nqkv, dtype=torch.int64, device=dev)
+        self.q = torch.zeros(P, c.NH * c.HD, dtype=torch.float16, device=dev)
+        self.att = torch.zeros(P, c.NH * c.HD, dtype=torch.float32, device=dev)
+        self.mq = torch.zeros(P, c.FFN, dtype=torch.int8, device=dev)
+        self.mds = torch.zeros(P, c.FFN // 32, 2, dtype=torch.float16, device=dev)
+        self.ids = torch.zeros(P, dtype=torch.int32, device=dev)
+        self.pos = torch.zeros(P, dtype=torch.int32, device=dev)
+        self.fin_pos = torch.zeros(1, dtype=torch.int32, device=dev)
+        self.scale = 1.0 / math.sqrt(c.HD)
+
+    def layer(self, i: int, P: int, pos0: int):
+        m, c, d = self.m, self.cfg, self.dec
+        L = m.layers[i]
+        call("q355_rmsnorm_fix_q8_1", ptr(self.h), ptr(L["ln1"]), ptr(self.xq), ptr(self.xds), P, c.H, c.eps)
+        W = L["qkv"]
+        call("q355_mmq_q4_0_q8_1", ptr(W.qs), ptr(W.d), W.N, W.K, ptr(self.xq), ptr(self.xds), P, 6,
+             None, ptr(self.qkv_acc), None, None, None, None)
+        call("q355_qkv_finish", ptr(self.qkv_acc), ptr(L["qkv_b"]), ptr(m.cos), ptr(m.sin), ptr(self.pos),
+             ptr(d.block_table), d.max_chunks, 0, ptr(d.kc[i]), ptr(d.vc[i]), ptr(self.q), c.NH, c.NKV, P)
+        call("q355_attn_prefill", ptr(self.q), ptr(d.kc[i]), ptr(d.vc[i]), ptr(d.block_table), pos0, P, c.NH, c.NKV,
+             self.scale, ptr(self.att))
+        call("q355_quant_q8_1", ptr(self.att), ptr(self.xq), ptr(self.xds), P, c.NH * c.HD)
+        W = L["o"]
+        call("q355_mmq_q4_0_q8_1", ptr(W.qs), ptr(W.d), W.N, W.K, ptr(self.xq), ptr(self.xds), P, 6,
+             None, ptr(self.h), None, None, None, None)
+        call("q355_rmsnorm_fix_q8_1", ptr(self.h), ptr(L["ln2"]), ptr(self.xq), ptr(self.xds), P, c.H, c.eps)
+        W = L["gu"]
+        call("q355_mmq_q4_0_q8_1", ptr(W.qs), ptr(W.d), W.N, W.K, ptr(self.xq), ptr(self.xds), P, 7,
+             None, None, ptr(self.mq), ptr(self.mds), None, None)
+        W = L["down"]
+        call("q355_mmq_q4_0_q8_1", ptr(W.qs), ptr(W.d), W.N, W.K, ptr(self.mq), ptr(self.mds), P, 6,
+             None, ptr(self.h), None, None, None, None)
+
+    def chunk(self, ids, pos0: int = 0):
+        """Prefill ids (int array, len P <= max_chunk) at positions pos0.. ; leaves dec.tok = the next token."""
+        import torch
+        ids = np.asarray(ids, np.int32).reshape(-1)
+        P = len(ids)
+        c, m, d = self.cfg, self.m, self.dec
+        assert 1 <= P <= self.P_max and pos0 + P <= d.max_chunks * PAGE
+        self.ids[:P].copy_(torch.from_numpy(ids))
+        self.pos[:P].copy_(torch.arange(pos0, pos0 + P, dtype=torch.int32))
+        self.enqueue(P, pos0)
+
+    def enqueue(self, P: int, pos0: int):
+        """The launches of chunk() on the current stream (ids/pos already set; capturable)."""
+        c, m, d = self.cfg, self.m, self.dec
+        e = m.embed
+        call("q355_embed_q4_0", ptr(e.qs), ptr(e.d), e.N, e.K, ptr(self.ids), ptr(self.h), P)
+        for i in range(c.L):
+            self.layer(i, P, pos0)
+        call("q355_head_logits", ptr(e.qs), ptr(e.d), e.N, e.K, ptr(self.h[P - 1:]), ptr(m.norm), c.eps,
+             ptr(d.logits), ptr(d.pmax), ptr(d.pidx), 1)
+        call("q355_finish", ptr(d.pmax), ptr(d.pidx), d.nparts, ptr(d.tok), ptr(self.fin_pos), 1)
+        d.pos.fill_(pos0 + P)
+
+    def hidden_f64(self, P: int):
+        import torch
+        return self.h[:P].to(torch.float64) / FIX_SCALE

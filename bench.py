@@ -152,6 +152,34 @@ def batched_decode(dm, B: int, steps: int = 32, warmup: int = 2) -> dict:
     return out
 
 
+def prefill(dm, P: int = 2048, reps: int = 3) -> dict:
+    """one 2048-token prompt (uniform ids, seed 4) through the chunked prefill path
+    (int8 MFMA MMQ GEMMs at M = P, causal fp16-MFMA flash attention), one chunk; tok/s = P / time."""
+    import torch
+    from lab import qwen_batched as QB
+    from lab import qwen_model as QM
+    c = dm.cfg
+    dec = QM.Decoder(dm, T=1, max_ctx=P + 64)
+    pf = QB.Prefill(dec, max_chunk=P)
+    ids = np.random.default_rng(4).integers(0, c.V, P)
+    pf.chunk(ids, 0)                                   # warm-up (also sets ids / positions)
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(reps):
+        pf.enqueue(P, 0)
+    e.record()
+    torch.cuda.synchronize()
+    ms = s.elapsed_time(e) / reps
+    gemm_ops = 2 * P * (c.nqkv * c.H + c.H * c.NH * c.HD + 2 * c.FFN * c.H + c.H * c.FFN) * c.L
+    attn_flop = 4 * c.NH * c.HD * (P * (P + 1) // 2) * c.L
+    out = {"P": P, "tok_per_s": round(P * 1e3 / ms, 1), "ms": round(ms, 3), "gemm_ops": gemm_ops,
+           "attn_flop": attn_flop, "effective_TOPS": round((gemm_ops + attn_flop) / (ms * 1e-3) / 1e12, 1)}
+    del pf, dec
+    torch.cuda.empty_cache()
+    return out
+
+
 def cpu_baseline(w, cfg, prompt, n_steps: int = 6) -> dict:
     """The oracle (exact int32 block dots, numpy, single core) decoding n_steps tokens of the same model
     after a short context; tok/s = n_steps / wall time."""
@@ -206,7 +234,7 @@ def main():
     log(f"weights generated in {time.time() - t0:.1f} s")
     prompt_len = 128
     maxlen = prompt_len + args.warmup + args.steps + 64
-    dm = QM.DeviceModel(w, cfg, maxlen=max(512, maxlen))
+    dm = QM.DeviceModel(w, cfg, maxlen=max(2048 + 64, maxlen))
     dec = QM.Decoder(dm, T=1, max_ctx=max(512, maxlen))
     prompt = np.random.default_rng(1).integers(0, cfg.V, prompt_len)
     t0 = time.time()
@@ -245,6 +273,8 @@ def main():
     if not args.quick:
         out["batched"] = [batched_decode(dm, B) for B in (8, 32)]
         log("batched:", out["batched"])
+        out["prefill"] = prefill(dm)
+        log("prefill:", out["prefill"])
         out["roofline"] = gate_up_roofline(dm, dec)
         out["gemv"] = gemv_config0()
         if not args.no_cpu:

@@ -136,6 +136,14 @@ int q355_qkv_finish(int64_t* acc, const float* bias, const float* rope_cos, cons
                     const int32_t* pos, const int32_t* block_table, int bt_stride, int seq_stride, void* kcache,
                     void* vcache, void* qout, int nh, int nkv, int T, void* stream);
 
+/* Causal GQA prefill attention (fp16 MFMA, fp32 accumulation) for one sequence: queries q fp16
+ * [P][nh*128] at positions pos0 .. pos0 + P - 1 attend to keys 0 .. their own position in the paged cache
+ * (block_table = the sequence's page ids, >= (pos0 + P - 1) / 64 + 1 of them; K/V of every attended
+ * position already written); out fp32 [P][nh*128] = softmax(q k^T * scale) v.
+ * Replaces flash_prefill_v3_source (lab/qwen_batched.py:1795-2037). */
+int q355_attn_prefill(const void* q, const void* kcache, const void* vcache, const int32_t* block_table, int pos0,
+                      int P, int nh, int nkv, float scale, float* out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

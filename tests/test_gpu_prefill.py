@@ -1,0 +1,122 @@
+"""GPU parity of the prefill path: causal flash attention on fp16 MFMA and the chunked
+prefill driver (MMQ GEMMs + attention), against the numpy oracle."""
+import math
+
+import numpy as np
+import pytest
+
+from lab import qwen_batched as QB
+from lab import qwen_model as QM
+from lab.hip import call, ptr
+from oracle import model as OM
+
+pytestmark = pytest.mark.gpu
+ATT_TOL = 3e-3          # fp16 P (as BASELINE config 4: fp16 inputs, fp32 accumulation) vs the f64 oracle
+NEAR_TIE = 1e-2
+
+
+def relerr(a, b):
+    a, b = np.asarray(a, np.float64), np.asarray(b, np.float64)
+    return float(np.abs(a - b).max() / max(np.abs(b).max(), 1e-30))
+
+
+@pytest.mark.parametrize("P,pos0,nh,nkv", [(1, 0, 12, 2), (64, 0, 12, 2), (100, 0, 12, 2), (200, 37, 12, 2),
+                                           (130, 64, 8, 2), (17, 250, 12, 2)])
+def test_attn_prefill_matches_oracle(cuda, P, pos0, nh, nkv):
+    import torch
+    rng = np.random.default_rng(P * 1000 + pos0)
+    n = pos0 + P
+    n_pages = (n + 63) // 64 + 3
+    K = rng.standard_normal((nkv, n_pages * 64, 128)).astype(np.float16)
+    V = rng.standard_normal((nkv, n_pages * 64, 128)).astype(np.float16)
+    q = (rng.standard_normal((P, nh, 128)) * 0.5).astype(np.float16)
+    # scattered pages: logical page c of the sequence lives in physical page table[c]
+    table = rng.permutation(n_pages).astype(np.int32)
+    kc = np.zeros((n_pages, nkv, 64, 128), np.float16)
+    vc = np.zeros_like(kc)
+    for c in range(n_pages):
+        kc[table[c]] = K[:, 64 * c:64 * (c + 1)]
+        vc[table[c]] = V[:, 64 * c:64 * (c + 1)]
+    # positions past the context hold garbage that the mask must ignore
+    kc_t = torch.from_numpy(kc).cuda()
+    vc_t = torch.from_numpy(vc).cuda()
+    out = torch.zeros(P, nh * 128, device=cuda)
+    q_t = torch.from_numpy(q.reshape(P, -1)).cuda()
+    table_t = torch.from_numpy(table).cuda()
+    call("q355_attn_prefill", ptr(q_t), ptr(kc_t), ptr(vc_t), ptr(table_t), pos0, P, nh, nkv, 1.0 / math.sqrt(128),
+         ptr(out))
+    torch.cuda.synchronize()
+    ref = OM.attn_prefill(q, K, V, pos0, nh, nkv)
+    assert relerr(out.cpu().numpy(), ref) < ATT_TOL
+
+
+def test_attn_prefill_bad_args(cuda):
+    from lab.hip import HipError
+    with pytest.raises(HipError, match="attn_prefill"):
+        call("q355_attn_prefill", 1, 1, 1, 1, 0, 0, 12, 2, 0.1, 1)
+
+
+CFG_S = QM.Config(L=2, V=4096)
+
+
+@pytest.fixture(scope="module")
+def small(cuda):
+    w = QM.random_weights(CFG_S, seed=21)
+    return w, QM.DeviceModel(w, CFG_S, maxlen=512), OM.Model(OM.Config(L=2, V=4096), w, maxlen=512)
+
+
+def test_prefill_matches_oracle(small):
+    """A 150-token prompt in one chunk: final hidden states, the K cache and the next token match the oracle."""
+    import torch
+    w, dm, om = small
+    prompt = np.random.default_rng(5).integers(0, CFG_S.V, 150)
+    dec = QM.Decoder(dm, T=1, max_ctx=512)
+    pf = QB.Prefill(dec, max_chunk=256)
+    pf.chunk(prompt, 0)
+    torch.cuda.synchronize()
+    cache = om.new_cache()
+    h = om.forward(list(prompt), 0, cache)
+    assert relerr(pf.hidden_f64(150).cpu().numpy(), h) < 2e-2
+    k_gpu = dec.kc[1][0:3].permute(1, 0, 2, 3).reshape(2, 192, 128)[:, :150].float().cpu().numpy()
+    assert relerr(k_gpu, cache["K"][1][:, :150]) < 2e-2
+    lg = om.logits(h[-1:])[0]
+    top2 = np.partition(lg, -2)[-2:]
+    if top2[1] - top2[0] >= NEAR_TIE:
+        assert int(dec.tok.item()) == int(np.argmax(lg))
+    assert int(dec.pos.item()) == 150
+
+
+def test_prefill_then_decode_greedy(small):
+    """Prefill, then greedy decode continues from the prefilled cache: tokens match the oracle up to its first
+    near-tie."""
+    w, dm, om = small
+    prompt = list(np.random.default_rng(6).integers(0, CFG_S.V, 70))
+    dec = QM.Decoder(dm, T=1, max_ctx=256)
+    QB.Prefill(dec, max_chunk=128).chunk(prompt, 0)
+    got = dec.generate(12)[0]
+    ref, margins = om.greedy(prompt, 12)
+    for i, (x, y) in enumerate(zip(got, ref)):
+        if margins[i] < NEAR_TIE:
+            break
+        assert x == y, f"token {i}: {x} vs {y} (margin {margins[i]:.3g})"
+
+
+def test_prefill_chunked_equals_one_chunk(small):
+    """Two chunks (64 + 61 tokens, the second at pos0 = 64) leave the same cache and next token as one chunk."""
+    import torch
+    w, dm, om = small
+    prompt = np.random.default_rng(7).integers(0, CFG_S.V, 125)
+    a = QM.Decoder(dm, T=1, max_ctx=256)
+    QB.Prefill(a, max_chunk=128).chunk(prompt, 0)
+    b = QM.Decoder(dm, T=1, max_ctx=256)
+    pb = QB.Prefill(b, max_chunk=128)
+    pb.chunk(prompt[:64], 0)
+    pb.chunk(prompt[64:], 64)
+    torch.cuda.synchronize()
+    for i in range(CFG_S.L):
+        assert relerr(b.kc[i][:2].float().cpu().numpy(), a.kc[i][:2].float().cpu().numpy()) < 1e-2
+    assert int(a.pos.item()) == int(b.pos.item()) == 125
+    lg = om.logits(om.forward(list(prompt), 0, om.new_cache())[-1:])[0]
+    top2 = np.partition(lg, -2)[-2:]
+    if top2[1] - top2[0] >= NEAR_TIE:
+        assert int(a.tok.item()) == int(b.tok.item())
