@@ -350,3 +350,44 @@ extern "C" int q355_attn_prefill(const void* q, const void* kcache, const void* 
   hipLaunchKernelGGL(k_attn_prefill, dim3((P + 63) / 64, nh), dim3(256), 0, (hipStream_t)stream, a);
   return launched("attn_prefill");
 }
+
+// ------------------------------------------------------------------------------------------------
+// Persistent decode step (batch 1).
+extern "C" int64_t q355_mega_ws_bytes(int max_chunks, int L) { return (int64_t)mega_ws_bytes(max_chunks, L); }
+extern "C" int q355_mega_layer_bytes(void) { return (int)sizeof(MegaLayer); }
+
+static constexpr size_t MEGA_LDS = (size_t)MG_FFN + 2 * (MG_FFN / 32) * 4 > (3 * HD + 24 + 12 * HD) * 8
+                                       ? (size_t)MG_FFN + 2 * (MG_FFN / 32) * 4 : (size_t)(3 * HD + 24 + 12 * HD) * 8;
+
+extern "C" int q355_mega_decode(const void* layers, int L, const uint8_t* emb_qs, const void* emb_d, const float* norm,
+                                int V, const float* rope_cos, const float* rope_sin, const int32_t* block_table,
+                                int max_chunks, double eps, int32_t* tok, int32_t* pos, int64_t* h, float* logits,
+                                void* ws, int64_t spin_limit_us, void* stream) {
+  REQUIRE(layers && emb_qs && emb_d && norm && rope_cos && rope_sin && block_table && tok && pos && h && logits && ws,
+          "mega_decode: null pointer");
+  REQUIRE(L >= 1 && L <= 256, "mega_decode: L=%d", L);
+  REQUIRE(V > 0 && V % 16 == 0 && V / 16 >= MG_NWG, "mega_decode: V=%d (multiple of 16, >= %d)", V, 16 * MG_NWG);
+  REQUIRE(max_chunks >= 1 && max_chunks <= 64, "mega_decode: max_chunks=%d (1..64)", max_chunks);
+  REQUIRE(spin_limit_us > 0, "mega_decode: spin_limit_us=%lld", (long long)spin_limit_us);
+  // all MG_NWG workgroups must be resident at once (they wait on each other)
+  static int checked_dev = -1;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return fail(Q355_EINVAL, "mega_decode: no device");
+  if (checked_dev != dev) {
+    int cus = 0, per_cu = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_mega_decode, MG_NTH, MEGA_LDS) != hipSuccess)
+      return fail(Q355_EINVAL, "mega_decode: device query failed");
+    REQUIRE((long)cus * per_cu >= MG_NWG, "mega_decode: %d CUs x %d resident workgroups < %d", cus, per_cu, MG_NWG);
+    checked_dev = dev;
+  }
+  MegaArgs a = {};
+  a.layers = (const MegaLayer*)layers; a.L = L;
+  a.emb_qs = emb_qs; a.emb_d = (const __half*)emb_d; a.norm = norm; a.V = V;
+  a.rope_cos = rope_cos; a.rope_sin = rope_sin; a.block_table = block_table; a.max_chunks = max_chunks;
+  a.eps = eps; a.scale = 1.0 / sqrt((double)HD);
+  a.tok = tok; a.pos = pos; a.h = (long long*)h; a.logits = logits;
+  a.ws = (char*)ws; a.spin_limit = spin_limit_us * 100;      // wall_clock64 runs at 100 MHz
+  hipLaunchKernelGGL(k_mega_decode, dim3(MG_NWG), dim3(MG_NTH), MEGA_LDS, (hipStream_t)stream, a);
+  return launched("mega_decode");
+}

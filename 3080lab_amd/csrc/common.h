@@ -122,18 +122,36 @@ __device__ __forceinline__ uint2 q8_1_x8(const float (&x)[8], float& df, int& sq
 }
 
 // f64 wave reductions (the batch-1 decode path accumulates in f64 so that every Q8_1 quantizer input
-// agrees with the f64 oracle to ~1e-14; CDNA4 runs f64 FMA at the fp32 vector rate).
-template <int WIDTH = 64>
-__device__ __forceinline__ double wave_sum_d(double v) {
-#pragma unroll
-  for (int o = WIDTH / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
+// agrees with the f64 oracle to ~1e-14; CDNA4 runs f64 FMA at the fp32 vector rate). DPP steps inside each
+// 16-lane row (xor 1, xor 2, half-row mirror, row mirror: every lane of the row ends with the row's result),
+// then the four row results are read as scalars and combined in a fixed order: no LDS round trips, and
+// every lane gets the bitwise same value. All 64 lanes must be active.
+template <int CTRL>
+__device__ __forceinline__ double dpp_d(double v) {
+  int2 x = *reinterpret_cast<int2*>(&v);
+  x.x = __builtin_amdgcn_mov_dpp(x.x, CTRL, 0xF, 0xF, true);
+  x.y = __builtin_amdgcn_mov_dpp(x.y, CTRL, 0xF, 0xF, true);
+  return *reinterpret_cast<double*>(&x);
 }
-template <int WIDTH = 64>
+__device__ __forceinline__ double readlane_d(double v, int l) {
+  int2 x = *reinterpret_cast<int2*>(&v);
+  x.x = __builtin_amdgcn_readlane(x.x, l);
+  x.y = __builtin_amdgcn_readlane(x.y, l);
+  return *reinterpret_cast<double*>(&x);
+}
+__device__ __forceinline__ double wave_sum_d(double v) {
+  v += dpp_d<DPP_XOR1>(v);
+  v += dpp_d<DPP_XOR2>(v);
+  v += dpp_d<DPP_HALF_MIRROR>(v);
+  v += dpp_d<DPP_MIRROR>(v);
+  return (readlane_d(v, 0) + readlane_d(v, 16)) + (readlane_d(v, 32) + readlane_d(v, 48));
+}
 __device__ __forceinline__ double wave_max_d(double v) {
-#pragma unroll
-  for (int o = WIDTH / 2; o > 0; o >>= 1) v = fmax(v, __shfl_xor(v, o, 64));
-  return v;
+  v = fmax(v, dpp_d<DPP_XOR1>(v));
+  v = fmax(v, dpp_d<DPP_XOR2>(v));
+  v = fmax(v, dpp_d<DPP_HALF_MIRROR>(v));
+  v = fmax(v, dpp_d<DPP_MIRROR>(v));
+  return fmax(fmax(readlane_d(v, 0), readlane_d(v, 16)), fmax(readlane_d(v, 32), readlane_d(v, 48)));
 }
 
 // Wave64 reductions (xor butterfly over all 64 lanes, or over `width` lanes).

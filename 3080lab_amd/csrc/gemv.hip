@@ -375,8 +375,14 @@ __device__ __forceinline__ void epilogue(const GemvArgs& a, A (&part)[NW][NT][T]
 // ---------------------------------------------------------------------------------------------
 // The GEMV: T tokens (1..4), NT 16-row tiles per workgroup, NW waves splitting the K slice 4*NW ways,
 // KPL K-blocks per lane (compile time, so all weight loads are issued before the first use).
+// Optional timing hooks (defined by instrumented builds only; empty in the library).
+#ifndef Q355_TRACE_POINT
+#define Q355_TRACE_POINT(k)
+#endif
+
 template <int T, int NT, int NW, int KPL, int PRO, int EPI>
 __global__ void __launch_bounds__(NW * 64) k_gemv(const GemvArgs a) {
+  Q355_TRACE_POINT(0);
   extern __shared__ __align__(16) char lds[];
   __shared__ double red[NW * T];
   __shared__ double part[NW][NT][T][16];
@@ -410,6 +416,7 @@ __global__ void __launch_bounds__(NW * 64) k_gemv(const GemvArgs a) {
   }
   // compiler barrier: keep every load above issued here (no sinking into the conditional code below)
   __asm__ __volatile__("" ::: "memory");
+  Q355_TRACE_POINT(1);
 #pragma unroll
   for (int i = 0; i < KPL; ++i)
 #pragma unroll
@@ -417,6 +424,7 @@ __global__ void __launch_bounds__(NW * 64) k_gemv(const GemvArgs a) {
 
   xl.stage(a, ks, st, (float*)red, lds + (size_t)T * K + (size_t)T * nb * 8);
   __syncthreads();
+  Q355_TRACE_POINT(2);
 
   // f64 accumulation: each block term d_w * d_x * (dot - 8 sum q) is exact in f64 (22 + 21 bits)
   double acc[NT][T];
@@ -444,6 +452,7 @@ __global__ void __launch_bounds__(NW * 64) k_gemv(const GemvArgs a) {
       }
     }
   }
+  Q355_TRACE_POINT(3);
   // reduce the 4 slots of each row (lanes r, r+16, r+32, r+48), then the NW waves in fixed order
 #pragma unroll
   for (int t = 0; t < NT; ++t)
@@ -455,7 +464,9 @@ __global__ void __launch_bounds__(NW * 64) k_gemv(const GemvArgs a) {
       if (lane < 16) part[wv][t][j][r] = v;
     }
   __syncthreads();
+  Q355_TRACE_POINT(4);
   epilogue<NW, T, NT, EPI>(a, part, tile0);
+  Q355_TRACE_POINT(5);
 }
 
 }  // namespace q355

@@ -2,4 +2,5 @@
 #include "gemv.hip"
 #include "mmq.hip"
 #include "flash.hip"
+#include "mega.hip"
 #include "capi.hip"

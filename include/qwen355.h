@@ -144,6 +144,27 @@ int q355_qkv_finish(int64_t* acc, const float* bias, const float* rope_cos, cons
 int q355_attn_prefill(const void* q, const void* kcache, const void* vcache, const int32_t* block_table, int pos0,
                       int P, int nh, int nkv, float scale, float* out, void* stream);
 
+/* ---- persistent whole-step decode (batch 1) ---- */
+
+/* Bytes of the workspace q355_mega_decode needs for max_chunks pages and L layers. The caller zeroes it
+ * once; it carries the synchronisation words across launches (do not clear it between steps). */
+int64_t q355_mega_ws_bytes(int max_chunks, int L);
+/* sizeof of one entry of the per-layer pointer table (13 pointers: qkv qs/d/bias, ln1, o qs/d, ln2,
+ * gate_up qs/d, down qs/d, K cache, V cache). */
+int q355_mega_layer_bytes(void);
+
+/* One greedy decode step of the whole model in ONE launch of 256 workgroups (one per CU; fails with
+ * Q355_EINVAL if the device cannot keep 256 resident): embed tok, L layers, final norm + tied Q4_0 head,
+ * tok = argmax (lowest index on ties), pos += 1; logits fp32 [V]; h int64 [1536] receives the final
+ * residual. Shapes: H 1536, 12/2 heads of 128, FFN 8960, V % 16 == 0, max_chunks <= 64, pos < 64 max_chunks.
+ * Waits between workgroups are bounded by spin_limit_us; on expiry (or a bad pos/tok) the workspace error
+ * word is set and the launch completes with invalid outputs.
+ * Replaces mega_source (lab/qwen_mega.py:43-361) and the graph of FusedQwen.step (scripts/qwen_fused.py:113-180). */
+int q355_mega_decode(const void* layers, int L, const uint8_t* emb_qs, const void* emb_d, const float* norm, int V,
+                     const float* rope_cos, const float* rope_sin, const int32_t* block_table, int max_chunks,
+                     double eps, int32_t* tok, int32_t* pos, int64_t* h, float* logits, void* ws,
+                     int64_t spin_limit_us, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

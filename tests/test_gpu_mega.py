@@ -1,0 +1,68 @@
+"""GPU checks of the persistent whole-step decode (q355_mega_decode) against the graph-of-kernels decoder
+and the oracle."""
+import numpy as np
+import pytest
+
+from lab import qwen_mega as QG
+from lab import qwen_model as QM
+from oracle import model as OM
+
+pytestmark = pytest.mark.gpu
+NEAR_TIE = 1e-2
+CFG_S = QM.Config(L=2, V=4096)
+
+
+@pytest.fixture(scope="module")
+def small(cuda):
+    w = QM.random_weights(CFG_S, seed=21)
+    return w, QM.DeviceModel(w, CFG_S, maxlen=512), OM.Model(OM.Config(L=2, V=4096), w, maxlen=512)
+
+
+def test_mega_step_matches_graph_step(small):
+    """Same prompt through both decoders: logits agree to f64 rounding (~1e-9) at every step, tokens equal."""
+    w, dm, om = small
+    prompt = [int(t) for t in np.random.default_rng(22).integers(0, CFG_S.V, 8)]
+    a = QM.Decoder(dm, T=1, max_ctx=256)
+    b = QG.MegaDecoder(dm, max_ctx=256)
+    for t in prompt:
+        a.tok.fill_(t)
+        b.tok.fill_(t)
+        a.step()
+        b.step()
+        la, lb = a.logits[0].cpu().numpy(), b.logits[0].cpu().numpy()
+        assert b.error() == 0
+        assert np.abs(la - lb).max() <= 1e-6 * np.abs(la).max()
+        assert int(a.tok.item()) == int(b.tok.item())
+        assert int(a.pos.item()) == int(b.pos.item())
+    assert np.abs(a.h_f64().cpu().numpy() - b.h_f64().cpu().numpy()).max() < 1e-9
+
+
+def test_mega_greedy_matches_oracle(small):
+    """Greedy decode through graph replays of the persistent step, 70-token prompt (two KV pages)."""
+    w, dm, om = small
+    prompt = list(np.random.default_rng(23).integers(0, CFG_S.V, 70))
+    dec = QG.MegaDecoder(dm, max_ctx=256)
+    dec.prefill_tokens(prompt)
+    got = dec.generate(16)[0]
+    assert dec.error() == 0
+    ref, margins = om.greedy(prompt, 16)
+    for i, (x, y) in enumerate(zip(got, ref)):
+        if margins[i] < NEAR_TIE:
+            break
+        assert x == y, f"token {i}: {x} vs {y} (margin {margins[i]:.3g})"
+
+
+def test_mega_rejects_position_past_cache(small):
+    """pos beyond the cache: the launch returns at once with the error word set (no out-of-range access)."""
+    w, dm, om = small
+    dec = QG.MegaDecoder(dm, max_ctx=128)
+    dec.pos.fill_(128)
+    dec.step()
+    assert dec.error() != 0
+    assert int(dec.pos.item()) == 128
+
+
+def test_mega_source_spec():
+    assert QG.mega_source(28, 2048).symbol == "q355_mega_decode"
+    with pytest.raises(ValueError):
+        QG.mega_source(28, 2048, nw=64)
