@@ -17,11 +17,37 @@ namespace q355 {
 
 constexpr int KROW = HD + 8;  // padded K row in LDS (halves)
 
-template <int G>
+// accumulation-type overloads (f64: the batch-1 path; fp32: the batched path)
+__device__ __forceinline__ double rd_lane(double v, int l) { return readlane_d(v, l); }
+__device__ __forceinline__ float rd_lane(float v, int l) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+}
+__device__ __forceinline__ double wmax(double v) { return wave_max_d(v); }
+__device__ __forceinline__ double wsum(double v) { return wave_sum_d(v); }
+__device__ __forceinline__ float wmax(float v) {
+  v = fmaxf(v, dpp<DPP_XOR1>(v));
+  v = fmaxf(v, dpp<DPP_XOR2>(v));
+  v = fmaxf(v, dpp<DPP_HALF_MIRROR>(v));
+  v = fmaxf(v, dpp<DPP_MIRROR>(v));
+  return fmaxf(fmaxf(rd_lane(v, 0), rd_lane(v, 16)), fmaxf(rd_lane(v, 32), rd_lane(v, 48)));
+}
+__device__ __forceinline__ float wsum(float v) {
+  v += dpp<DPP_XOR1>(v);
+  v += dpp<DPP_XOR2>(v);
+  v += dpp<DPP_HALF_MIRROR>(v);
+  v += dpp<DPP_MIRROR>(v);
+  return (rd_lane(v, 0) + rd_lane(v, 16)) + (rd_lane(v, 32) + rd_lane(v, 48));
+}
+__device__ __forceinline__ double exp_t(double v) { return exp(v); }
+__device__ __forceinline__ float exp_t(float v) { return expf(v); }
+
+// F = double: every step in f64 (the batch-1 decode path, exact against the f64 oracle to ~1e-12);
+// F = float: fp32 scores, softmax and P.V (the batched path, which also accumulates its GEMMs in fp32).
+template <int G, typename F>
 __global__ void __launch_bounds__(G * 64) k_attn_decode(const AttnArgs a) {
   __shared__ __align__(16) __half ks[PAGE][KROW];
   __shared__ __align__(16) __half vs[PAGE][HD];
-  __shared__ __align__(16) double qf[G][HD];
+  __shared__ __align__(16) F qf[G][HD];
 
   const int j = blockIdx.y;
   const int kvh = blockIdx.x / a.max_chunks, c = blockIdx.x % a.max_chunks;
@@ -44,8 +70,8 @@ __global__ void __launch_bounds__(G * 64) k_attn_decode(const AttnArgs a) {
     vr[i] = vp[e];
   }
   const float2 qq = __half22float2(qv);
-  qf[wv][2 * lane] = (double)qq.x;
-  qf[wv][2 * lane + 1] = (double)qq.y;
+  qf[wv][2 * lane] = (F)qq.x;
+  qf[wv][2 * lane + 1] = (F)qq.y;
 #pragma unroll
   for (int i = 0; i < PER; ++i) {
     const int e = threadIdx.x + NT * i;
@@ -57,11 +83,11 @@ __global__ void __launch_bounds__(G * 64) k_attn_decode(const AttnArgs a) {
   }
   __syncthreads();
 
-  // scores: lane p, this wave's head (f64, 4 independent partial sums)
-  double s = 0.0;
+  // scores: lane p, this wave's head (4 independent partial sums)
+  F s = 0;
   {
-    const double* qh = qf[wv];
-    double sp[4] = {0.0, 0.0, 0.0, 0.0};
+    const F* qh = qf[wv];
+    F sp[4] = {0, 0, 0, 0};
 #pragma unroll
     for (int i = 0; i < HD / 8; ++i) {
       const uint4 kk = *(const uint4*)&ks[lane][8 * i];
@@ -69,35 +95,31 @@ __global__ void __launch_bounds__(G * 64) k_attn_decode(const AttnArgs a) {
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
         const float2 kf = __half22float2(k2[u]);
-        sp[u] = fma(qh[8 * i + 2 * u], (double)kf.x, sp[u]);
-        sp[u] = fma(qh[8 * i + 2 * u + 1], (double)kf.y, sp[u]);
+        sp[u] = fma(qh[8 * i + 2 * u], (F)kf.x, sp[u]);
+        sp[u] = fma(qh[8 * i + 2 * u + 1], (F)kf.y, sp[u]);
       }
     }
     s = (sp[0] + sp[1]) + (sp[2] + sp[3]);
   }
-  s = lane < nvalid ? s * a.scale : -INFINITY;
-  const double m = wave_max_d(s);
-  const double e = lane < nvalid ? exp(s - m) : 0.0;
-  const double l = wave_sum_d(e);
+  s = lane < nvalid ? s * (F)a.scale : (F)-INFINITY;
+  const F m = wmax(s);
+  const F e = lane < nvalid ? exp_t(s - m) : (F)0;
+  const F l = wsum(e);
 
-  // P.V: lane owns dims 2*lane, 2*lane+1; p(position) is broadcast from lane p with readlane
-  double o[4][2] = {{0.0, 0.0}, {0.0, 0.0}, {0.0, 0.0}, {0.0, 0.0}};
-  const int2 ei = *reinterpret_cast<const int2*>(&e);
+  // P.V: lane owns dims 2*lane, 2*lane+1; the weight of position p is broadcast from lane p (readlane)
+  F o[4][2] = {{0, 0}, {0, 0}, {0, 0}, {0, 0}};
 #pragma unroll
   for (int p = 0; p < PAGE; ++p) {
-    int2 bi;
-    bi.x = __builtin_amdgcn_readlane(ei.x, p);
-    bi.y = __builtin_amdgcn_readlane(ei.y, p);
-    const double ep = *reinterpret_cast<const double*>(&bi);
+    const F ep = rd_lane(e, p);
     const float2 v = __half22float2(((const __half2*)vs[p])[lane]);
-    o[p & 3][0] = fma(ep, (double)v.x, o[p & 3][0]);
-    o[p & 3][1] = fma(ep, (double)v.y, o[p & 3][1]);
+    o[p & 3][0] = fma(ep, (F)v.x, o[p & 3][0]);
+    o[p & 3][1] = fma(ep, (F)v.y, o[p & 3][1]);
   }
-  const double o0 = (o[0][0] + o[1][0]) + (o[2][0] + o[3][0]);
-  const double o1 = (o[0][1] + o[1][1]) + (o[2][1] + o[3][1]);
+  const F o0 = (o[0][0] + o[1][0]) + (o[2][0] + o[3][0]);
+  const F o1 = (o[0][1] + o[1][1]) + (o[2][1] + o[3][1]);
   double* P = a.part + (((size_t)j * a.nh + hq) * a.max_chunks + c) * (HD + 2);
-  ((double2*)P)[lane] = make_double2(o0, o1);
-  if (lane == 0) { P[HD] = m; P[HD + 1] = l; }
+  ((double2*)P)[lane] = make_double2((double)o0, (double)o1);
+  if (lane == 0) { P[HD] = (double)m; P[HD + 1] = (double)l; }
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -136,17 +158,19 @@ __device__ __forceinline__ void attn_merge_head(const double* __restrict__ P, in
   ((double2*)out)[lane] = make_double2(o0 / L, o1 / L);
 }
 
-// Standalone merge: one workgroup (4 waves) per token -> fp32 o32 (optional) and Q8_1 oq/ods.
-__global__ void __launch_bounds__(256) k_attn_merge(const AttnArgs a) {
-  extern __shared__ double sm[];                     // nh * HD
-  const int j = blockIdx.x;
+// Standalone merge: one wave per (token, query head) -> fp32 o32 (optional) and Q8_1 oq/ods of the head's
+// 128 values (4 blocks).
+__global__ void __launch_bounds__(64) k_attn_merge(const AttnArgs a) {
+  __shared__ double sm[HD];
+  const int j = blockIdx.x, h = blockIdx.y;
   const int nch = a.pos[j] / PAGE + 1;
-  for (int h = threadIdx.x >> 6; h < a.nh; h += 4)
-    attn_merge_head(a.part + ((size_t)j * a.nh + h) * a.max_chunks * (HD + 2), nch, sm + h * HD);
+  attn_merge_head(a.part + ((size_t)j * a.nh + h) * a.max_chunks * (HD + 2), nch, sm);
   __syncthreads();
   const int n = a.nh * HD;
-  for (int e = threadIdx.x; e < n; e += 256) {      // n % 256 == 0 keeps 32-lane groups whole
-    const float v = (float)sm[e];
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {                         // 64 lanes = two 32-value blocks per pass
+    const int e = h * HD + 64 * u + threadIdx.x;
+    const float v = (float)sm[64 * u + threadIdx.x];
     if (a.o32) a.o32[(size_t)j * n + e] = v;
     const int q = q8_1_lane32(v, a.ods + ((size_t)j * n + e) / 32, (e & 31) == 0);
     a.oq[(size_t)j * n + e] = (int8_t)q;

@@ -207,7 +207,8 @@ extern "C" int q355_embed_q4_0(const uint8_t* qs, const void* d, int V, int H, c
 
 extern "C" int q355_attn_decode(const void* q, const void* kcache, const void* vcache, const int32_t* pos,
                                 const int32_t* block_table, int bt_stride, int nh, int nkv, int max_chunks,
-                                double scale, double* part, int8_t* oq, void* ods, float* o32, int T, void* stream) {
+                                double scale, double* part, int8_t* oq, void* ods, float* o32, int T, int fp32,
+                                void* stream) {
   REQUIRE(q && kcache && vcache && pos && block_table && part, "attn_decode: null pointer");
   REQUIRE(nh > 0 && nkv > 0 && nh % nkv == 0, "attn_decode: nh=%d nkv=%d", nh, nkv);
   REQUIRE(nh / nkv == 6 || nh / nkv == 4 || nh / nkv == 8, "attn_decode: GQA group %d (4, 6 or 8 supported)", nh / nkv);
@@ -223,15 +224,22 @@ extern "C" int q355_attn_decode(const void* q, const void* kcache, const void* v
   a.oq = oq; a.ods = (half2*)ods; a.o32 = o32;
   hipStream_t s = (hipStream_t)stream;
   const dim3 grid(nkv * max_chunks, T);
-  switch (nh / nkv) {
-    case 4: hipLaunchKernelGGL(k_attn_decode<4>, grid, dim3(256), 0, s, a); break;
-    case 6: hipLaunchKernelGGL(k_attn_decode<6>, grid, dim3(384), 0, s, a); break;
-    default: hipLaunchKernelGGL(k_attn_decode<8>, grid, dim3(512), 0, s, a); break;
+  if (fp32) {
+    switch (nh / nkv) {
+      case 4: hipLaunchKernelGGL((k_attn_decode<4, float>), grid, dim3(256), 0, s, a); break;
+      case 6: hipLaunchKernelGGL((k_attn_decode<6, float>), grid, dim3(384), 0, s, a); break;
+      default: hipLaunchKernelGGL((k_attn_decode<8, float>), grid, dim3(512), 0, s, a); break;
+    }
+  } else {
+    switch (nh / nkv) {
+      case 4: hipLaunchKernelGGL((k_attn_decode<4, double>), grid, dim3(256), 0, s, a); break;
+      case 6: hipLaunchKernelGGL((k_attn_decode<6, double>), grid, dim3(384), 0, s, a); break;
+      default: hipLaunchKernelGGL((k_attn_decode<8, double>), grid, dim3(512), 0, s, a); break;
+    }
   }
   if (int e = launched("attn_decode")) return e;
   if (!oq) return Q355_OK;
-  const size_t lds = (size_t)nh * HD * 8;
-  hipLaunchKernelGGL(k_attn_merge, dim3(T), dim3(256), lds, s, a);
+  hipLaunchKernelGGL(k_attn_merge, dim3(T, nh), dim3(64), 0, s, a);
   return launched("attn_merge");
 }
 
@@ -262,20 +270,37 @@ extern "C" int q355_rmsnorm_fix_q8_1(const int64_t* h, const float* w, int8_t* x
   return launched("rmsnorm_fix_q8_1");
 }
 
+template <int TG, int KPW, int EPI>
+static int launch_mmq_reg(const GemvArgs& a, dim3 grid, size_t lds, hipStream_t s) {
+  hipLaunchKernelGGL((k_mmq_reg<TG, 4, 4, KPW, EPI>), grid, dim3(256), lds, s, a);
+  return launched("mmq");
+}
+
 template <int TG, int EPI>
 static int launch_mmq(GemvArgs a, int KS, hipStream_t s) {
   constexpr int NT = 4, NW = 4, TT = 16 * TG;
   constexpr size_t LDS_MAX = 65536;
   const int nb = a.K / 32, per = (nb + KS - 1) / KS;
+  const dim3 grid(a.N / (16 * NT), KS, (a.T + TT - 1) / TT);
+  const size_t pb = (size_t)NW * NT * TT * 16 * 4;
+  if (per <= NW * 5) {
+    // decode-sized K slices: the whole slice's weights in registers (KPW blocks per wave), its activations
+    // in LDS (wider slices run faster through the pipelined kernel below)
+    const size_t xb = (size_t)TT * (per * 32 + 16) + (size_t)TT * per * 8;
+    const size_t lds = xb > pb ? xb : pb;
+    if (lds <= LDS_MAX) {
+      if (per <= NW * 1) return launch_mmq_reg<TG, 1, EPI>(a, grid, lds, s);
+      if (per <= NW * 2) return launch_mmq_reg<TG, 2, EPI>(a, grid, lds, s);
+      return launch_mmq_reg<TG, 5, EPI>(a, grid, lds, s);
+    }
+  }
   // activation chunk: TT rows of (32 B per block + 16 B pad) + 8 B (d, sum) per block, within 64 KB
   const int ch_max = (int)((LDS_MAX - (size_t)TT * 16) / ((size_t)TT * 40));
   const int nchunks = (per + ch_max - 1) / ch_max;
   a.mmq_chunk = (per + nchunks - 1) / nchunks;
   const size_t xb = (size_t)TT * (a.mmq_chunk * 32 + 16) + (size_t)TT * a.mmq_chunk * 8;
-  const size_t pb = (size_t)NW * NT * TT * 16 * 4;
   const size_t lds = xb > pb ? xb : pb;
   if (lds > LDS_MAX) return fail(Q355_EINVAL, "mmq: %zu B of LDS for %d tokens", lds, TT);
-  const dim3 grid(a.N / (16 * NT), KS, (a.T + TT - 1) / TT);
   hipLaunchKernelGGL((k_mmq<TG, NT, NW, EPI>), grid, dim3(NW * 64), lds, s, a);
   return launched("mmq");
 }

@@ -174,11 +174,28 @@ __device__ __forceinline__ int wave_isum(int v) {
   return v;
 }
 
+// Reductions over aligned 32-lane groups: four DPP steps inside each 16-lane row, then one exchange
+// between the two rows of the group (every lane of the group gets the result).
+__device__ __forceinline__ float g32_max(float v) {
+  v = fmaxf(v, dpp<DPP_XOR1>(v));
+  v = fmaxf(v, dpp<DPP_XOR2>(v));
+  v = fmaxf(v, dpp<DPP_HALF_MIRROR>(v));
+  v = fmaxf(v, dpp<DPP_MIRROR>(v));
+  return fmaxf(v, __shfl_xor(v, 16, 64));
+}
+__device__ __forceinline__ int g32_isum(int v) {
+  v += dpp<DPP_XOR1>(v);
+  v += dpp<DPP_XOR2>(v);
+  v += dpp<DPP_HALF_MIRROR>(v);
+  v += dpp<DPP_MIRROR>(v);
+  return v + __shfl_xor(v, 16, 64);
+}
+
 // Q8_1 of one value inside a group of 32 lanes that hold one block (lane group aligned to 32).
 // Returns q; writes (d, s) through `ds` from the group's first lane. Bit-exact with the oracle:
 // d = fp16(amax / 127) (IEEE fp32 divide), q = roundf(x / d16) clamped to +-127, q = 0 when d16 == 0.
 __device__ __forceinline__ int q8_1_lane32(float x, half2* ds, bool leader) {
-  float amax = wave_max<32>(fabsf(x));
+  float amax = g32_max(fabsf(x));
   __half d16 = __float2half_rn(amax / 127.0f);
   float df = __half2float(d16);
   int q = 0;
@@ -186,7 +203,7 @@ __device__ __forceinline__ int q8_1_lane32(float x, half2* ds, bool leader) {
     q = (int)roundf(x / df);
     q = q > 127 ? 127 : (q < -127 ? -127 : q);
   }
-  int sq = wave_isum<32>(q);
+  int sq = g32_isum(q);
   if (leader) *ds = __halves2half2(d16, __float2half_rn(df * (float)sq));
   return q;
 }

@@ -26,9 +26,14 @@ __device__ __forceinline__ long nib8(uint2 w, int g) {
   return (long)(((unsigned long)hi << 32) | lo);
 }
 
+#ifndef Q355_TRACE_POINT
+#define Q355_TRACE_POINT(k)
+#endif
+
 template <int TG, int NT, int NW, int EPI>
 __global__ void __launch_bounds__(NW * 64) k_mmq(const GemvArgs a) {
   extern __shared__ __align__(16) char lds[];
+  Q355_TRACE_POINT(0);
   constexpr int TT = 16 * TG;                       // tokens per workgroup
   const int K = a.K, nb = K / 32;
   const KSlice ks(nb);
@@ -86,6 +91,7 @@ __global__ void __launch_bounds__(NW * 64) k_mmq(const GemvArgs a) {
       xd[j * ch + bb] = dx;
     }
     __syncthreads();
+    Q355_TRACE_POINT(1);
 
     auto compute_blk = [&](int bb, const uint2 (&w)[NT], const uint2 (&dv)[NT]) {
 #pragma unroll
@@ -116,8 +122,10 @@ __global__ void __launch_bounds__(NW * 64) k_mmq(const GemvArgs a) {
     if (bb < nbc) compute_blk(bb, wA, dA);
   }
 
+  Q355_TRACE_POINT(2);
   // partials -> LDS (reusing the activation area), then the shared epilogues
   __syncthreads();
+  Q355_TRACE_POINT(3);
   float(&part)[NW][NT][TT][16] = *reinterpret_cast<float(*)[NW][NT][TT][16]>(lds);
 #pragma unroll
   for (int t = 0; t < NT; ++t)
@@ -140,6 +148,122 @@ __global__ void __launch_bounds__(NW * 64) k_mmq(const GemvArgs a) {
     b.tok_base = a.tok_base + tok0;
   }
   epilogue<NW, TT, NT, EPI>(b, part, tile0);
+  Q355_TRACE_POINT(5);
+}
+
+// Decode-sized variant: every weight block of this workgroup's K slice is loaded into registers before
+// the activations are staged (wave wv takes blocks b0 + wv + NW i, i < KPW; the slice must have at most
+// NW * KPW blocks), so the HBM latency is paid once per workgroup instead of once per pipeline step.
+template <int TG, int NT, int NW, int KPW, int EPI>
+__global__ void __launch_bounds__(NW * 64) k_mmq_reg(const GemvArgs a) {
+  extern __shared__ __align__(16) char lds[];
+  Q355_TRACE_POINT(0);
+  constexpr int TT = 16 * TG;
+  const int K = a.K, nb = K / 32;
+  const KSlice ks(nb);
+  const int nbs = ks.b1 - ks.b0;
+  const int tok0 = blockIdx.z * TT;
+  const int ntok = min(TT, a.T - tok0);
+  const int xstride = nbs * 32 + 16;
+  int8_t* xq = (int8_t*)lds;
+  float* xd = (float*)(lds + (size_t)TT * xstride);
+  int* xs = (int*)(xd + TT * nbs);
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int li = lane & 15, lg = lane >> 4;
+  const int tile0 = blockIdx.x * NT;
+  const uint2* __restrict__ qs = (const uint2*)a.qs;
+  const uint2* __restrict__ dd = (const uint2*)a.d;
+  uint2 w[KPW][NT], dv[KPW][NT];
+#pragma unroll
+  for (int i = 0; i < KPW; ++i) {
+    const int bb = wv + NW * i;
+    const int b = ks.b0 + min(bb, nbs - 1);
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      const size_t base = ((size_t)(tile0 + t) * nb + b) * 16;
+      w[i][t] = qs[(base + li) * 2 + (lg & 1)];
+      dv[i][t] = dd[(base >> 2) + lg];
+    }
+  }
+  __asm__ __volatile__("" ::: "memory");
+#pragma unroll
+  for (int i = 0; i < KPW; ++i)
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+      if (wv + NW * i >= nbs) dv[i][t] = make_uint2(0u, 0u);   // blocks past the slice: scale 0
+  // activations of the slice -> LDS: task = (token, block): 32 B + d + sum(q); tokens past T are zero
+  for (int task = threadIdx.x; task < TT * nbs; task += NW * 64) {
+    const int j = task / nbs, bb = task % nbs;
+    int4 q0 = make_int4(0, 0, 0, 0), q1 = q0;
+    float dx = 0.f;
+    if (j < ntok) {
+      const int4* src = (const int4*)(a.xq + (size_t)(tok0 + j) * K + (size_t)(ks.b0 + bb) * 32);
+      q0 = src[0];
+      q1 = src[1];
+      dx = __low2float(a.xds[(size_t)(tok0 + j) * nb + ks.b0 + bb]);
+    }
+    int4* dst = (int4*)(xq + (size_t)j * xstride + bb * 32);
+    dst[0] = q0;
+    dst[1] = q1;
+    const int xv[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+    xs[j * nbs + bb] = sum_i8x32(xv);
+    xd[j * nbs + bb] = dx;
+  }
+  __syncthreads();
+  Q355_TRACE_POINT(1);
+  float acc[NT][TG][4];
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int g = 0; g < TG; ++g)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) acc[t][g][v] = 0.f;
+#pragma unroll
+  for (int i = 0; i < KPW; ++i) {
+    const int bb = min(wv + NW * i, nbs - 1);
+#pragma unroll
+    for (int g = 0; g < TG; ++g) {
+      const int j = 16 * g + li;
+      const long bx = *(const long*)(xq + (size_t)j * xstride + bb * 32 + 8 * lg);
+      const float dx = xd[j * nbs + bb];
+      const int s8 = 8 * xs[j * nbs + bb];
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        const v4i zero = {0, 0, 0, 0};
+        const v4i c = __builtin_amdgcn_mfma_i32_16x16x32_i8(nib8(w[i][t], lg), bx, zero, 0, 0, 0);
+        const __half2 d01 = *(const __half2*)&dv[i][t].x, d23 = *(const __half2*)&dv[i][t].y;
+        const float dw[4] = {__low2float(d01), __high2float(d01), __low2float(d23), __high2float(d23)};
+#pragma unroll
+        for (int v = 0; v < 4; ++v) acc[t][g][v] = fmaf(dw[v] * dx, (float)(c[v] - s8), acc[t][g][v]);
+      }
+    }
+  }
+  Q355_TRACE_POINT(2);
+  __syncthreads();
+  Q355_TRACE_POINT(3);
+  float(&part)[NW][NT][TT][16] = *reinterpret_cast<float(*)[NW][NT][TT][16]>(lds);
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int g = 0; g < TG; ++g)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) part[wv][t][16 * g + li][4 * lg + v] = acc[t][g][v];
+  __syncthreads();
+  GemvArgs b = a;
+  b.T = ntok;
+  if (tok0) {
+    b.y = a.y ? a.y + (size_t)tok0 * (EPI == EPI_SWIGLU ? a.N / 2 : a.N) : nullptr;
+    b.yfix = a.yfix ? a.yfix + (size_t)tok0 * a.N : nullptr;
+    b.pos = a.pos ? a.pos + tok0 : nullptr;
+    b.qout = a.qout ? a.qout + (size_t)tok0 * a.nh * HD : nullptr;
+    b.oq = a.oq ? a.oq + (size_t)tok0 * (a.N / 2) : nullptr;
+    b.ods = a.ods ? a.ods + (size_t)tok0 * (a.N / 64) : nullptr;
+    b.pmax = a.pmax ? a.pmax + (size_t)tok0 * gridDim.x : nullptr;
+    b.pidx = a.pidx ? a.pidx + (size_t)tok0 * gridDim.x : nullptr;
+    b.tok_base = a.tok_base + tok0;
+  }
+  epilogue<NW, TT, NT, EPI>(b, part, tile0);
+  Q355_TRACE_POINT(5);
 }
 
 }  // namespace q355

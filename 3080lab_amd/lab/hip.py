@@ -30,7 +30,7 @@ _SIGS = {
     "q355_head_nparts": [c_int],
     "q355_finish": [_P, _P, c_int, _P, _P, c_int, _P],
     "q355_embed_q4_0": [_P, _P, c_int, c_int, _P, _P, c_int, _P],
-    "q355_attn_decode": [_P, _P, _P, _P, _P, c_int, c_int, c_int, c_int, c_double, _P, _P, _P, _P, c_int, _P],
+    "q355_attn_decode": [_P, _P, _P, _P, _P, c_int, c_int, c_int, c_int, c_double, _P, _P, _P, _P, c_int, c_int, _P],
     "q355_attn_o_resid": [_P, _P, c_int, _P, c_int, _P, c_int, _P, c_int, _P],
     "q355_rmsnorm_fix_q8_1": [_P, _P, _P, _P, c_int, c_int, c_double, _P],
     "q355_mmq_q4_0_q8_1": [_P, _P, c_int, c_int, _P, _P, c_int, c_int, _P, _P, _P, _P, _P, _P, _P],

@@ -6,7 +6,7 @@ Here B sequences share one step with:
   rmsnorm_fix_q8_1       RMSNorm of the fixed-point residual stream -> Q8_1 (per token)
   mmq (resid_fix)        QKV on v_mfma_i32_16x16x32_i8, K-sliced into an int64 accumulator
   qkv_finish             bias + RoPE + fp16 q + paged fp16 K/V write (clears the accumulator)
-  attn_decode + merge    split-K GQA attention over 64-position pages of every sequence -> Q8_1
+  attn_decode + merge    split-K GQA attention (fp32) over 64-position pages of every sequence -> Q8_1
   mmq (resid_fix)        O projection into the residual stream
   rmsnorm_fix_q8_1, mmq (swiglu_q8)   gate_up + SwiGLU, output already Q8_1
   mmq (resid_fix)        down projection into the residual stream
@@ -123,7 +123,7 @@ class BatchedDecoder:
              c.NH, c.NKV, B)
         call("q355_attn_decode", ptr(self.q), ptr(self.kc[i]), ptr(self.vc[i]), ptr(self.pos), ptr(self.block_table),
              self.max_chunks, c.NH, c.NKV, self.max_chunks, self.scale, ptr(self.part), ptr(self.aq), ptr(self.ads),
-             None, B)
+             None, B, 1)
         self._mmq(L["o"], self.aq, self.ads, 6, yfix=self.h)
         self._norm(L["ln2"])
         self._mmq(L["gu"], self.xq, self.xds, 7, oq=self.mq, ods=self.mds)

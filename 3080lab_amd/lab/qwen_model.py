@@ -204,7 +204,7 @@ class Decoder:
              ptr(m.cos), ptr(m.sin), ptr(self.pos), ptr(self.block_table), self.max_chunks, 1,
              ptr(self.kc[i]), ptr(self.vc[i]), ptr(self.q), c.NH, c.NKV, T)
         call("q355_attn_decode", ptr(self.q), ptr(self.kc[i]), ptr(self.vc[i]), ptr(self.pos), ptr(self.block_table),
-             self.max_chunks, c.NH, c.NKV, self.max_chunks, self.scale, ptr(self.part), None, None, None, T)
+             self.max_chunks, c.NH, c.NKV, self.max_chunks, self.scale, ptr(self.part), None, None, None, T, 0)
         call("q355_attn_o_resid", ptr(o.qs), ptr(o.d), o.N, ptr(self.part), self.max_chunks, ptr(self.pos), c.NH,
              ptr(self.h), T)
         call("q355_ffn_gate_up", ptr(gu.qs), ptr(gu.d), gu.N, gu.K, ptr(self.h), ptr(L["ln2"]), c.eps,

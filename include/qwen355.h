@@ -99,10 +99,12 @@ int q355_embed_q4_0(const uint8_t* qs, const void* d, int V, int H, const int32_
  * (o[128], running max, sum) of every live chunk; max_chunks >= (max pos)/64 + 1, <= 64.
  * If oq/ods are given it also merges them (second launch): Q8_1 oq int8 [T][nh*128], ods half2
  * [T][nh*4], and optionally fp32 o32 [T][nh*128]. GQA group nh/nkv in {4, 6, 8}.
+ * fp32 = 0: scores, softmax and P.V in f64 (the batch-1 path, exact against the f64 oracle); fp32 = 1: in fp32
+ * (the batched path, whose projections also accumulate in fp32).
  * Replaces ATTN2 / ATTN4 (lab/qwen_kernels.py:358-442, 517-605). */
 int q355_attn_decode(const void* q, const void* kcache, const void* vcache, const int32_t* pos,
                      const int32_t* block_table, int bt_stride, int nh, int nkv, int max_chunks, double scale,
-                     double* part, int8_t* oq, void* ods, float* o32, int T, void* stream);
+                     double* part, int8_t* oq, void* ods, float* o32, int T, int fp32, void* stream);
 
 /* Fused attention merge + Q8_1 + O-projection GEMV + residual: h[T][N] += Wo . Q8_1(merge(part))
  * (3 K slices of nh/3 heads, fixed-point atomics). part / max_chunks / pos as written by

@@ -233,8 +233,9 @@ def test_ffn_gate_up_down(one_layer):
     assert relerr(dec.h_f32().cpu().numpy() - h, ref) < REL
 
 
+@pytest.mark.parametrize("fp32", [0, 1])
 @pytest.mark.parametrize("positions", [[0, 63], [64, 511], [1000, 5]])
-def test_attn_decode(cuda, positions):
+def test_attn_decode(cuda, positions, fp32):
     import torch
     c = CFG1
     T = len(positions)
@@ -252,7 +253,7 @@ def test_attn_decode(cuda, positions):
     o32 = torch.zeros(T, c.NH * c.HD, device=cuda)
     for rep in range(2):   # repeated calls give identical results (no state carried between calls)
         call("q355_attn_decode", ptr(to_dev(q)), ptr(to_dev(kc)), ptr(to_dev(vc)), ptr(to_dev(pos)), ptr(to_dev(bt)),
-             max_chunks, c.NH, c.NKV, max_chunks, 1 / math.sqrt(c.HD), ptr(part), ptr(oq), ptr(ods), ptr(o32), T)
+             max_chunks, c.NH, c.NKV, max_chunks, 1 / math.sqrt(c.HD), ptr(part), ptr(oq), ptr(ods), ptr(o32), T, fp32)
         sync()
         for j in range(T):
             K = np.concatenate([kc[bt[j, p]] for p in range(max_chunks)], axis=1)     # [nkv, ctx, hd]
