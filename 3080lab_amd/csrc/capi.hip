@@ -284,11 +284,11 @@ static int launch_mmq(GemvArgs a, int KS, hipStream_t s) {
   const dim3 grid(a.N / (16 * NT), KS, (a.T + TT - 1) / TT);
   const size_t pb = (size_t)NW * NT * TT * 16 * 4;
   if (per <= NW * 5) {
-    // decode-sized K slices: the whole slice's weights in registers (KPW blocks per wave), its activations
-    // in LDS (wider slices run faster through the pipelined kernel below)
-    const size_t xb = (size_t)TT * (per * 32 + 16) + (size_t)TT * per * 8;
+    // narrow K slices (decode): the whole slice's nibbles in registers (KPW blocks per wave), its activations
+    // and scales in LDS; wider slices run faster through the pipelined kernel below
+    const size_t xb = (size_t)TT * (per * 32 + 16) + (size_t)TT * per * 8 + (size_t)NT * per * 32;
     const size_t lds = xb > pb ? xb : pb;
-    if (lds <= LDS_MAX) {
+    if (lds <= 160 * 1024) {                          // gfx950: 160 KB of LDS per workgroup
       if (per <= NW * 1) return launch_mmq_reg<TG, 1, EPI>(a, grid, lds, s);
       if (per <= NW * 2) return launch_mmq_reg<TG, 2, EPI>(a, grid, lds, s);
       return launch_mmq_reg<TG, 5, EPI>(a, grid, lds, s);
@@ -307,7 +307,9 @@ static int launch_mmq(GemvArgs a, int KS, hipStream_t s) {
 
 template <int EPI>
 static int launch_mmq_tg(const GemvArgs& a, int KS, hipStream_t s) {
-  return a.T <= 16 ? launch_mmq<1, EPI>(a, KS, s) : launch_mmq<2, EPI>(a, KS, s);
+  // up to 64 tokens (decode batches): 16-token workgroups, several per CU, hide each other's latencies;
+  // prefill sizes: 32-token workgroups reuse every staged weight block twice
+  return a.T <= 64 ? launch_mmq<1, EPI>(a, KS, s) : launch_mmq<2, EPI>(a, KS, s);
 }
 
 extern "C" int q355_mmq_q4_0_q8_1(const uint8_t* qs, const void* d, int N, int K, const int8_t* xq, const void* xds,

@@ -30,6 +30,38 @@ __device__ __forceinline__ long nib8(uint2 w, int g) {
 #define Q355_TRACE_POINT(k)
 #endif
 
+// One K block (LDS column bb) against NT tiles x TG token groups: all NT * TG MFMAs are issued before
+// any of their results is scaled, so the matrix-core latency overlaps instead of stalling each product.
+template <int NT, int TG>
+__device__ __forceinline__ void mmq_block(const uint2 (&w)[NT], const uint2 (&dv)[NT], const int8_t* __restrict__ xq, int xstride,
+                                          const float* xd, const int* xs, int ld, int bb, int li, int lg,
+                                          float (&acc)[NT][TG][4]) {
+  v4i c[NT][TG];
+  float dx[TG];
+  int s8[TG];
+#pragma unroll
+  for (int g = 0; g < TG; ++g) {
+    const int j = 16 * g + li;
+    const long bx = *(const long*)(xq + (size_t)j * xstride + bb * 32 + 8 * lg);
+    dx[g] = xd[j * ld + bb];
+    s8[g] = 8 * xs[j * ld + bb];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      const v4i zero = {0, 0, 0, 0};
+      c[t][g] = __builtin_amdgcn_mfma_i32_16x16x32_i8(nib8(w[t], lg), bx, zero, 0, 0, 0);
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    const __half2 d01 = *(const __half2*)&dv[t].x, d23 = *(const __half2*)&dv[t].y;
+    const float dw[4] = {__low2float(d01), __high2float(d01), __low2float(d23), __high2float(d23)};
+#pragma unroll
+    for (int g = 0; g < TG; ++g)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) acc[t][g][v] = fmaf(dw[v] * dx[g], (float)(c[t][g][v] - s8[g]), acc[t][g][v]);
+  }
+}
+
 template <int TG, int NT, int NW, int EPI>
 __global__ void __launch_bounds__(NW * 64) k_mmq(const GemvArgs a) {
   extern __shared__ __align__(16) char lds[];
@@ -94,22 +126,7 @@ __global__ void __launch_bounds__(NW * 64) k_mmq(const GemvArgs a) {
     Q355_TRACE_POINT(1);
 
     auto compute_blk = [&](int bb, const uint2 (&w)[NT], const uint2 (&dv)[NT]) {
-#pragma unroll
-      for (int g = 0; g < TG; ++g) {
-        const int j = 16 * g + li;
-        const long bx = *(const long*)(xq + (size_t)j * xstride + bb * 32 + 8 * lg);
-        const float dx = xd[j * ch + bb];
-        const int s8 = 8 * xs[j * ch + bb];
-#pragma unroll
-        for (int t = 0; t < NT; ++t) {
-          const v4i zero = {0, 0, 0, 0};
-          const v4i c = __builtin_amdgcn_mfma_i32_16x16x32_i8(nib8(w[t], lg), bx, zero, 0, 0, 0);
-          const __half2 d01 = *(const __half2*)&dv[t].x, d23 = *(const __half2*)&dv[t].y;
-          const float dw[4] = {__low2float(d01), __high2float(d01), __low2float(d23), __high2float(d23)};
-#pragma unroll
-          for (int v = 0; v < 4; ++v) acc[t][g][v] = fmaf(dw[v] * dx, (float)(c[v] - s8), acc[t][g][v]);
-        }
-      }
+      mmq_block<NT, TG>(w, dv, xq, xstride, xd, xs, ch, bb, li, lg, acc);
     };
     // 2-deep pipeline over this wave's blocks wv, wv + NW, ... of the chunk
     int bb = wv;
@@ -153,7 +170,8 @@ __global__ void __launch_bounds__(NW * 64) k_mmq(const GemvArgs a) {
 
 // Decode-sized variant: every weight block of this workgroup's K slice is loaded into registers before
 // the activations are staged (wave wv takes blocks b0 + wv + NW i, i < KPW; the slice must have at most
-// NW * KPW blocks), so the HBM latency is paid once per workgroup instead of once per pipeline step.
+// NW * KPW blocks), so the HBM latency is paid once per workgroup instead of once per pipeline step. The
+// slice's scales go through LDS with the activations (registers hold only the nibbles).
 template <int TG, int NT, int NW, int KPW, int EPI>
 __global__ void __launch_bounds__(NW * 64) k_mmq_reg(const GemvArgs a) {
   extern __shared__ __align__(16) char lds[];
@@ -168,29 +186,25 @@ __global__ void __launch_bounds__(NW * 64) k_mmq_reg(const GemvArgs a) {
   int8_t* xq = (int8_t*)lds;
   float* xd = (float*)(lds + (size_t)TT * xstride);
   int* xs = (int*)(xd + TT * nbs);
+  uint2* wsc = (uint2*)(xs + TT * nbs);                 // [NT][nbs][4] groups of 4 fp16 row scales
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int li = lane & 15, lg = lane >> 4;
   const int tile0 = blockIdx.x * NT;
   const uint2* __restrict__ qs = (const uint2*)a.qs;
   const uint2* __restrict__ dd = (const uint2*)a.d;
-  uint2 w[KPW][NT], dv[KPW][NT];
+  uint2 w[KPW][NT];
 #pragma unroll
   for (int i = 0; i < KPW; ++i) {
-    const int bb = wv + NW * i;
-    const int b = ks.b0 + min(bb, nbs - 1);
+    const int b = ks.b0 + min(wv + NW * i, nbs - 1);
 #pragma unroll
-    for (int t = 0; t < NT; ++t) {
-      const size_t base = ((size_t)(tile0 + t) * nb + b) * 16;
-      w[i][t] = qs[(base + li) * 2 + (lg & 1)];
-      dv[i][t] = dd[(base >> 2) + lg];
-    }
+    for (int t = 0; t < NT; ++t) w[i][t] = qs[(((size_t)(tile0 + t) * nb + b) * 16 + li) * 2 + (lg & 1)];
   }
   __asm__ __volatile__("" ::: "memory");
-#pragma unroll
-  for (int i = 0; i < KPW; ++i)
-#pragma unroll
-    for (int t = 0; t < NT; ++t)
-      if (wv + NW * i >= nbs) dv[i][t] = make_uint2(0u, 0u);   // blocks past the slice: scale 0
+  // scales of the slice -> LDS (zero for blocks past the slice is not needed: those blocks are skipped)
+  for (int e = threadIdx.x; e < NT * nbs * 4; e += NW * 64) {
+    const int t = e / (nbs * 4), bb = (e / 4) % nbs, q = e & 3;
+    wsc[e] = dd[(((size_t)(tile0 + t) * nb + ks.b0 + bb) * 16 >> 2) + q];
+  }
   // activations of the slice -> LDS: task = (token, block): 32 B + d + sum(q); tokens past T are zero
   for (int task = threadIdx.x; task < TT * nbs; task += NW * 64) {
     const int j = task / nbs, bb = task % nbs;
@@ -220,22 +234,12 @@ __global__ void __launch_bounds__(NW * 64) k_mmq_reg(const GemvArgs a) {
       for (int v = 0; v < 4; ++v) acc[t][g][v] = 0.f;
 #pragma unroll
   for (int i = 0; i < KPW; ++i) {
-    const int bb = min(wv + NW * i, nbs - 1);
+    const int bb = wv + NW * i;
+    if (bb < nbs) {                                     // uniform per wave
+      uint2 dv[NT];
 #pragma unroll
-    for (int g = 0; g < TG; ++g) {
-      const int j = 16 * g + li;
-      const long bx = *(const long*)(xq + (size_t)j * xstride + bb * 32 + 8 * lg);
-      const float dx = xd[j * nbs + bb];
-      const int s8 = 8 * xs[j * nbs + bb];
-#pragma unroll
-      for (int t = 0; t < NT; ++t) {
-        const v4i zero = {0, 0, 0, 0};
-        const v4i c = __builtin_amdgcn_mfma_i32_16x16x32_i8(nib8(w[i][t], lg), bx, zero, 0, 0, 0);
-        const __half2 d01 = *(const __half2*)&dv[i][t].x, d23 = *(const __half2*)&dv[i][t].y;
-        const float dw[4] = {__low2float(d01), __high2float(d01), __low2float(d23), __high2float(d23)};
-#pragma unroll
-        for (int v = 0; v < 4; ++v) acc[t][g][v] = fmaf(dw[v] * dx, (float)(c[v] - s8), acc[t][g][v]);
-      }
+      for (int t = 0; t < NT; ++t) dv[t] = wsc[(t * nbs + bb) * 4 + lg];
+      mmq_block<NT, TG>(w[i], dv, xq, xstride, xd, xs, nbs, bb, li, lg, acc);
     }
   }
   Q355_TRACE_POINT(2);
