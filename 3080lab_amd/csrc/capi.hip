@@ -45,7 +45,7 @@ extern "C" const char* q355_version(void) { return "qwen355 0.1 gfx950"; }
 
 // ------------------------------------------------------------------------------------------------
 // GEMV dispatch over (T, NT, NW, KPL, prologue, epilogue); grid = (N/16/NT tiles, KS K-slices).
-template <int PRO, int EPI, int NT, int NW, int KPL>
+template <int PRO, int EPI, int NT, int NW, int KPL, int WF = WF_Q4_0>
 static int launch_gemv(const GemvArgs& a, int KS, hipStream_t s) {
   const int tiles = a.N / 16, nb = a.K / 32;
   if (tiles % NT) return fail(Q355_EINVAL, "gemv: N/16=%d not a multiple of %d tiles per workgroup", tiles, NT);
@@ -55,10 +55,10 @@ static int launch_gemv(const GemvArgs& a, int KS, hipStream_t s) {
   size_t lds = (size_t)a.T * a.K + (size_t)a.T * nb * 8;
   if (PRO == PRO_ATTN) lds += 8 + (size_t)a.nh * HD * 8;  // merged heads of one token; 8: f64 alignment
   switch (a.T) {
-    case 1: hipLaunchKernelGGL((k_gemv<1, NT, NW, KPL, PRO, EPI>), grid, dim3(NW * 64), lds, s, a); break;
-    case 2: hipLaunchKernelGGL((k_gemv<2, NT, NW, KPL, PRO, EPI>), grid, dim3(NW * 64), lds, s, a); break;
-    case 3: hipLaunchKernelGGL((k_gemv<3, NT, NW, KPL, PRO, EPI>), grid, dim3(NW * 64), lds, s, a); break;
-    case 4: hipLaunchKernelGGL((k_gemv<4, NT, NW, KPL, PRO, EPI>), grid, dim3(NW * 64), lds, s, a); break;
+    case 1: hipLaunchKernelGGL((k_gemv<1, NT, NW, KPL, PRO, EPI, WF>), grid, dim3(NW * 64), lds, s, a); break;
+    case 2: hipLaunchKernelGGL((k_gemv<2, NT, NW, KPL, PRO, EPI, WF>), grid, dim3(NW * 64), lds, s, a); break;
+    case 3: hipLaunchKernelGGL((k_gemv<3, NT, NW, KPL, PRO, EPI, WF>), grid, dim3(NW * 64), lds, s, a); break;
+    case 4: hipLaunchKernelGGL((k_gemv<4, NT, NW, KPL, PRO, EPI, WF>), grid, dim3(NW * 64), lds, s, a); break;
     default: return fail(Q355_EINVAL, "gemv: T=%d outside 1..4", a.T);
   }
   return launched("gemv");
@@ -186,6 +186,39 @@ extern "C" int q355_head_logits(const uint8_t* qs, const void* d, int V, int K, 
   a.qs = qs; a.d = (const __half*)d; a.N = V; a.K = K; a.T = T;
   a.hfix = (const long long*)h; a.nw = nw; a.eps = eps; a.y = logits; a.pmax = pmax; a.pidx = pidx;
   return launch_gemv<PRO_RMS, EPI_LOGITS, 8, 4, 3>(a, 1, (hipStream_t)stream);
+}
+
+static int check_q6k(const char* what, const void* lo, const void* hi, const void* sc, const void* d, int N, int K) {
+  REQUIRE(lo && hi && sc && d, "%s: null weight pointer", what);
+  REQUIRE(N > 0 && N % 16 == 0, "%s: N=%d must be a positive multiple of 16", what, N);
+  REQUIRE(K > 0 && K % 256 == 0, "%s: K=%d must be a positive multiple of 256 (Q6_K super-blocks)", what, K);
+  return Q355_OK;
+}
+
+extern "C" int q355_head_logits_q6k(const uint8_t* lo, const uint8_t* hi, const int8_t* sc, const void* d, int V, int K,
+                                    const int64_t* h, const float* nw, double eps, float* logits, float* pmax,
+                                    int32_t* pidx, int T, void* stream) {
+  if (int e = check_q6k("head_logits_q6k", lo, hi, sc, d, V, K)) return e;
+  REQUIRE(V % 128 == 0, "head_logits_q6k: V=%d must be a multiple of 128", V);
+  REQUIRE(K <= 1536, "head_logits_q6k: K=%d > 1536 (fused RMSNorm prologue)", K);
+  REQUIRE(h && nw && logits && pmax && pidx, "head_logits_q6k: null pointer");
+  REQUIRE(T >= 1 && T <= 4, "head_logits_q6k: T=%d outside 1..4", T);
+  GemvArgs a = {};
+  a.qs = lo; a.qhi = hi; a.qsc = (const uint8_t*)sc; a.d = (const __half*)d; a.N = V; a.K = K; a.T = T;
+  a.hfix = (const long long*)h; a.nw = nw; a.eps = eps; a.y = logits; a.pmax = pmax; a.pidx = pidx;
+  return launch_gemv<PRO_RMS, EPI_LOGITS, 8, 4, 3, WF_Q6_K>(a, 1, (hipStream_t)stream);
+}
+
+extern "C" int q355_gemv_q6_k_q8_1(const uint8_t* lo, const uint8_t* hi, const int8_t* sc, const void* d, int N, int K,
+                                   const int8_t* xq, const void* xds, int T, float* y, void* stream) {
+  if (int e = check_q6k("gemv_q6_k_q8_1", lo, hi, sc, d, N, K)) return e;
+  REQUIRE(xq && xds && y, "gemv_q6_k_q8_1: null pointer");
+  REQUIRE(T >= 1 && T <= 4, "gemv_q6_k_q8_1: T=%d outside 1..4", T);
+  REQUIRE(K <= 1536, "gemv_q6_k_q8_1: K=%d > 1536", K);
+  GemvArgs a = {};
+  a.qs = lo; a.qhi = hi; a.qsc = (const uint8_t*)sc; a.d = (const __half*)d; a.N = N; a.K = K; a.T = T;
+  a.xq = xq; a.xds = (const half2*)xds; a.y = y;
+  return launch_gemv<PRO_Q8, EPI_STORE, 1, 4, 3, WF_Q6_K>(a, 1, (hipStream_t)stream);
 }
 
 extern "C" int q355_finish(const float* pmax, const int32_t* pidx, int nparts, int32_t* tok, int32_t* pos, int T,

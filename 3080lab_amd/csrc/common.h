@@ -46,6 +46,30 @@ __device__ __forceinline__ int q4_block_dot(const uint4 w, const int* x) {
   return acc;
 }
 
+// One 32-weight block of the Q6_K planes against 32 int8 values: v = lo | hi << 4 in 0..63, weight value
+// sc[i / 16] * (v - 32); returns sum over the two 16-weight sub-blocks of sc_s * (dot_s - 32 sum x_s)
+// (exact int32; the caller scales by the super-block d and the activation d).
+// lo byte i holds v_i & 15 (bits 0-3) and v_{i+16} & 15 (bits 4-7); hi byte b holds v_{b+8j} >> 4 at bits 2j.
+__device__ __forceinline__ int q6k_block_isum(const uint4 w, const uint2 h, unsigned sc, const int* x) {
+  const unsigned M4 = 0x0F0F0F0Fu, M2 = 0x03030303u;
+  int d0 = 0, d1 = 0, s0 = 0, s1 = 0;
+  d0 = dot4((int)((w.x & M4) | ((h.x & M2) << 4)), x[0], d0);
+  d0 = dot4((int)((w.y & M4) | ((h.y & M2) << 4)), x[1], d0);
+  d0 = dot4((int)((w.z & M4) | (((h.x >> 2) & M2) << 4)), x[2], d0);
+  d0 = dot4((int)((w.w & M4) | (((h.y >> 2) & M2) << 4)), x[3], d0);
+  d1 = dot4((int)(((w.x >> 4) & M4) | (((h.x >> 4) & M2) << 4)), x[4], d1);
+  d1 = dot4((int)(((w.y >> 4) & M4) | (((h.y >> 4) & M2) << 4)), x[5], d1);
+  d1 = dot4((int)(((w.z >> 4) & M4) | (((h.x >> 6) & M2) << 4)), x[6], d1);
+  d1 = dot4((int)(((w.w >> 4) & M4) | (((h.y >> 6) & M2) << 4)), x[7], d1);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    s0 = dot4(x[i], 0x01010101, s0);
+    s1 = dot4(x[4 + i], 0x01010101, s1);
+  }
+  const int c0 = (int)(signed char)(sc & 255), c1 = (int)(signed char)((sc >> 8) & 255);
+  return c0 * (d0 - 32 * s0) + c1 * (d1 - 32 * s1);
+}
+
 __device__ __forceinline__ int sum_i8x32(const int* x) {
   int s = 0;
 #pragma unroll

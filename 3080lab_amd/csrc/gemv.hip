@@ -380,7 +380,7 @@ __device__ __forceinline__ void epilogue(const GemvArgs& a, A (&part)[NW][NT][T]
 #define Q355_TRACE_POINT(k)
 #endif
 
-template <int T, int NT, int NW, int KPL, int PRO, int EPI>
+template <int T, int NT, int NW, int KPL, int PRO, int EPI, int WF>
 __global__ void __launch_bounds__(NW * 64) k_gemv(const GemvArgs a) {
   Q355_TRACE_POINT(0);
   extern __shared__ __align__(16) char lds[];
@@ -399,8 +399,11 @@ __global__ void __launch_bounds__(NW * 64) k_gemv(const GemvArgs a) {
 
   const uint4* __restrict__ qs = (const uint4*)a.qs;
   const unsigned short* __restrict__ dd = (const unsigned short*)a.d;
+  constexpr bool Q6 = WF == WF_Q6_K;
   uint4 w[NT][KPL];
   unsigned dh[NT][KPL];   // fp16 scale bits, zero-extended: 16-bit register halves would serialise the loads
+  uint2 hq[NT][Q6 ? KPL : 1];
+  unsigned sc6[NT][Q6 ? KPL : 1];
   // Unconditional loads (clamped block index, scale zeroed past the slice): straight-line code lets
   // the compiler wait for exactly the loads each use needs instead of draining all of them.
 #pragma unroll
@@ -411,7 +414,13 @@ __global__ void __launch_bounds__(NW * 64) k_gemv(const GemvArgs a) {
     for (int t = 0; t < NT; ++t) {
       const size_t idx = ((size_t)(tile0 + t) * nb + bc) * 16 + r;
       w[t][i] = ld_stream16(qs + idx);
-      dh[t][i] = dd[idx];
+      if constexpr (Q6) {
+        hq[t][i] = ((const uint2*)a.qhi)[idx];
+        sc6[t][i] = ((const unsigned short*)a.qsc)[idx];
+        dh[t][i] = dd[((size_t)(tile0 + t) * (nb / 8) + bc / 8) * 16 + r];
+      } else {
+        dh[t][i] = dd[idx];
+      }
     }
   }
   // compiler barrier: keep every load above issued here (no sinking into the conditional code below)
@@ -445,9 +454,13 @@ __global__ void __launch_bounds__(NW * 64) k_gemv(const GemvArgs a) {
         const int s8 = 8 * st.s[j * nb + b];
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
-          const int dot = q4_block_dot(w[t][i], xv);
           const double sc = (double)__half2float(__ushort_as_half((unsigned short)dh[t][i])) * (double)dx;
-          acc[t][j] = fma(sc, (double)(dot - s8), acc[t][j]);
+          if constexpr (Q6) {
+            acc[t][j] = fma(sc, (double)q6k_block_isum(w[t][i], hq[t][i], sc6[t][i], xv), acc[t][j]);
+          } else {
+            const int dot = q4_block_dot(w[t][i], xv);
+            acc[t][j] = fma(sc, (double)(dot - s8), acc[t][j]);
+          }
         }
       }
     }

@@ -31,9 +31,15 @@ __device__ __forceinline__ long long to_fix(double v) { return __double2ll_rn(v 
 __device__ __forceinline__ double from_fix(long long v) { return (double)v * FIX_INV; }
 
 // Everything a GEMV-family launch may need; unused fields are null/zero.
+// Weight formats of the GEMV: Q4_0 planes, or the Q6_K planes (lo nibbles, 2-bit hi plane, int8 sub-block
+// scales, fp16 super-block scale; 6.5625 bits per weight as in the GGUF file).
+enum { WF_Q4_0 = 0, WF_Q6_K = 1 };
+
 struct GemvArgs {
-  const uint8_t* qs;           // Q4_0 nibble plane [N/16][K/32][16][16]
-  const __half* d;             // Q4_0 scale plane  [N/16][K/32][16]
+  const uint8_t* qs;           // Q4_0 nibble plane [N/16][K/32][16][16] (Q6_K: the lo plane, same shape)
+  const __half* d;             // Q4_0 scale plane  [N/16][K/32][16] (Q6_K: super-block scales [N/16][K/256][16])
+  const uint8_t* qhi;          // Q6_K hi plane [N/16][K/32][16][8]
+  const uint8_t* qsc;          // Q6_K sub-block scales [N/16][K/32][16][2] (int8)
   int N, K, T;
   // PRO_Q8 input
   const int8_t* xq;            // [T][K]
@@ -99,7 +105,7 @@ struct AttnArgs {
   float* o32;                  // optional fp32 output [T][nh*HD] (tests), may be null
 };
 
-template <int T, int NT, int NW, int KPL, int PRO, int EPI>
+template <int T, int NT, int NW, int KPL, int PRO, int EPI, int WF>
 __global__ void k_gemv(const GemvArgs a);
 template <int TG, int NT, int NW, int EPI>
 __global__ void k_mmq(const GemvArgs a);

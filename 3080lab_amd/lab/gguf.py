@@ -188,6 +188,26 @@ def untile_q4_0(qs: np.ndarray, d: np.ndarray) -> np.ndarray:
     return out.reshape(-1, 18)
 
 
+def tile_q6_k(b: np.ndarray, N: int, K: int):
+    """GGUF Q6_K bytes of W [N, K] (K % 256 == 0) -> the library's Q6_K planes, 6.5625 bits per weight as
+    in the file (weights in natural order, v = q + 32 in 0..63):
+      lo uint8 [N/16, K/32, 16, 16]: byte i = (v_i & 15) | (v_{i+16} & 15) << 4 of each 32-weight block
+      hi uint8 [N/16, K/32, 16, 8]:  byte b = sum_j (v_{b+8j} >> 4) << 2j, j = 0..3
+      sc int8  [N/16, K/32, 16, 2]:  the two 16-weight sub-block scales of the block
+      d  fp16  [N/16, K/256, 16]:    the super-block scale
+    so weight i of a block is d * sc[i // 16] * (v_i - 32)."""
+    assert N % 16 == 0 and K % 256 == 0
+    q, sc, d = q6_k_parts(b)
+    v = (q.astype(np.int16) + 32).astype(np.uint8).reshape(N, K // 32, 32)
+    lo = (v[..., :16] & 15) | ((v[..., 16:] & 15) << 4)
+    hv = v >> 4
+    hi = hv[..., 0:8] | (hv[..., 8:16] << 2) | (hv[..., 16:24] << 4) | (hv[..., 24:32] << 6)
+    sc2 = sc.reshape(N, K // 32, 2)
+    dd = d.reshape(N, K // 256)
+    t = lambda a: np.ascontiguousarray(a.reshape(N // 16, 16, *a.shape[1:]).swapaxes(1, 2))  # noqa: E731
+    return t(lo.astype(np.uint8)), t(hi.astype(np.uint8)), t(sc2), t(dd)
+
+
 def rope_row_order(n_heads: int, hd: int = 128) -> np.ndarray:
     """Row permutation that interleaves the RoPE pairs of every head: new row 2i <- dim i,
     new row 2i+1 <- dim i + hd/2 (so one 16-row tile holds 8 complete pairs)."""

@@ -28,6 +28,8 @@ _SIGS = {
     "q355_ffn_down": [_P, _P, c_int, c_int, _P, _P, c_int, _P],
     "q355_head_logits": [_P, _P, c_int, c_int, _P, _P, c_double, _P, _P, _P, c_int, _P],
     "q355_head_nparts": [c_int],
+    "q355_head_logits_q6k": [_P, _P, _P, _P, c_int, c_int, _P, _P, c_double, _P, _P, _P, c_int, _P],
+    "q355_gemv_q6_k_q8_1": [_P, _P, _P, _P, c_int, c_int, _P, _P, c_int, _P, _P],
     "q355_finish": [_P, _P, c_int, _P, _P, c_int, _P],
     "q355_embed_q4_0": [_P, _P, c_int, c_int, _P, _P, c_int, _P],
     "q355_attn_decode": [_P, _P, _P, _P, _P, c_int, c_int, c_int, c_int, c_double, _P, _P, _P, _P, c_int, c_int, _P],

@@ -74,6 +74,8 @@ class BatchedDecoder:
     def __init__(self, m: DeviceModel, B: int, max_ctx: int, page_seed: int = 0):
         import torch
         c = m.cfg
+        if m.head_q6k is not None:
+            raise ValueError("the batched (MMQ) step implements the tied Q4_0 head only")
         self.m, self.cfg, self.B = m, c, B
         dev = m.device
         self.max_chunks = -(-max_ctx // PAGE)

@@ -41,6 +41,8 @@ class MegaDecoder(Decoder):
 
     def __init__(self, m: DeviceModel, max_ctx: int | None = None):
         import torch
+        if m.head_q6k is not None:
+            raise ValueError("the persistent step implements the tied Q4_0 head only")
         super().__init__(m, T=1, max_ctx=max_ctx)
         assert call("q355_mega_layer_bytes") == ctypes.sizeof(MegaLayer)
         # the kernel accepts any pos < max_chunks * 64: the RoPE tables must cover all of them

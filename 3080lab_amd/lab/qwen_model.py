@@ -118,6 +118,61 @@ class Q4Mat:
         return self.qs.numel() + 2 * self.d.numel()
 
 
+class Q6KMat:
+    """A Q6_K matrix (the output head of llama.cpp's Qwen2.5 Q4_0 files) in the library's Q6_K planes."""
+
+    def __init__(self, b: np.ndarray, N: int, K: int, device):
+        import torch
+        lo, hi, sc, d = gguf.tile_q6_k(b, N, K)
+        self.N, self.K = N, K
+        self.lo = torch.from_numpy(lo.reshape(-1)).to(device)
+        self.hi = torch.from_numpy(hi.reshape(-1)).to(device)
+        self.sc = torch.from_numpy(sc.reshape(-1).view(np.uint8)).to(device)
+        self.d = torch.from_numpy(d.reshape(-1).view(np.int16)).to(device)
+
+    @property
+    def nbytes(self):
+        return self.lo.numel() + self.hi.numel() + self.sc.numel() + 2 * self.d.numel()
+
+
+def weights_from_gguf(path) -> tuple:
+    """A Qwen2 GGUF file (llama.cpp tensor names) -> (Config, weight dict) in the random_weights layout
+    (scripts/qwen_gguf.py:63-121): Q4_0 matrices as GGUF bytes, norms and QKV biases fp32, the Q4_0 token
+    embedding; output.weight (Q6_K in llama.cpp's Q4_0 files) becomes w["head_q6k"], else the head is tied.
+    Every matrix of a layer must be Q4_0."""
+    g = gguf.GGUF(path)
+    m = g.meta
+    H, nh, nkv = m["qwen2.embedding_length"], m["qwen2.attention.head_count"], m["qwen2.attention.head_count_kv"]
+    emb_b, emb_t = g.raw("token_embd.weight")
+    if emb_t.type != 2:
+        raise ValueError(f"token_embd.weight is ggml type {emb_t.type}; this path needs Q4_0")
+    cfg = Config(H=H, NH=nh, NKV=nkv, HD=H // nh, FFN=m["qwen2.feed_forward_length"], L=m["qwen2.block_count"],
+                 V=emb_t.dims[1], eps=float(m["qwen2.attention.layer_norm_rms_epsilon"]),
+                 theta=float(m.get("qwen2.rope.freq_base", 1e6)))
+
+    def q4(name):
+        b, t = g.raw(name)
+        if t.type != 2:
+            raise ValueError(f"{name} is ggml type {t.type}; this path needs Q4_0")
+        return np.asarray(b, np.uint8).reshape(-1, 18)
+
+    f32 = lambda name: np.ascontiguousarray(g.f32(name), np.float32).reshape(-1)  # noqa: E731
+    w = {"embed": q4("token_embd.weight"), "norm": f32("output_norm.weight"), "layers": []}
+    for i in range(cfg.L):
+        p = f"blk.{i}."
+        w["layers"].append({
+            "wq": q4(p + "attn_q.weight"), "wk": q4(p + "attn_k.weight"), "wv": q4(p + "attn_v.weight"),
+            "bq": f32(p + "attn_q.bias"), "bk": f32(p + "attn_k.bias"), "bv": f32(p + "attn_v.bias"),
+            "wo": q4(p + "attn_output.weight"), "wg": q4(p + "ffn_gate.weight"), "wu": q4(p + "ffn_up.weight"),
+            "wd": q4(p + "ffn_down.weight"), "ln1": f32(p + "attn_norm.weight"), "ln2": f32(p + "ffn_norm.weight")})
+    if "output.weight" in g.tensors:
+        b, t = g.raw("output.weight")
+        if t.type != 14:
+            raise ValueError(f"output.weight is ggml type {t.type}; Q6_K or a tied head is supported")
+        w["head_q6k"] = np.asarray(b, np.uint8).reshape(-1, 210)
+    return cfg, w
+
+
 class DeviceModel:
     """Weights of the whole model in HBM, in device row orders (QKV pair-interleaved for RoPE,
     gate/up interleaved for SwiGLU)."""
@@ -141,13 +196,14 @@ class DeviceModel:
                 "gu": Q4Mat(gguf.take_rows_q4_0(gu, H, gu_order), 2 * cfg.FFN, H, device),
                 "down": Q4Mat(L["wd"], H, cfg.FFN, device)})
         self.embed = Q4Mat(w["embed"], cfg.V, H, device)
+        self.head_q6k = Q6KMat(w["head_q6k"], cfg.V, H, device) if "head_q6k" in w else None
         self.norm = f32(w["norm"])
         cos, sin = rope_tables(maxlen, cfg.HD, cfg.theta)
         self.cos, self.sin = f32(cos), f32(sin)
 
     def weight_bytes_per_token(self) -> int:
         per = sum(L[n].nbytes for L in self.layers for n in ("qkv", "o", "gu", "down"))
-        return per + self.embed.nbytes
+        return per + (self.head_q6k.nbytes if self.head_q6k is not None else self.embed.nbytes)
 
 
 class Decoder:
@@ -216,9 +272,13 @@ class Decoder:
         call("q355_embed_q4_0", ptr(e.qs), ptr(e.d), e.N, e.K, ptr(self.tok), ptr(self.h), self.T)
 
     def head(self):
-        e = self.m.embed
-        call("q355_head_logits", ptr(e.qs), ptr(e.d), e.N, e.K, ptr(self.h), ptr(self.m.norm), self.cfg.eps,
-             ptr(self.logits), ptr(self.pmax), ptr(self.pidx), self.T)
+        e, q6 = self.m.embed, self.m.head_q6k
+        if q6 is not None:     # llama.cpp's Q6_K output.weight
+            call("q355_head_logits_q6k", ptr(q6.lo), ptr(q6.hi), ptr(q6.sc), ptr(q6.d), q6.N, q6.K, ptr(self.h),
+                 ptr(self.m.norm), self.cfg.eps, ptr(self.logits), ptr(self.pmax), ptr(self.pidx), self.T)
+        else:                  # tied Q4_0 head
+            call("q355_head_logits", ptr(e.qs), ptr(e.d), e.N, e.K, ptr(self.h), ptr(self.m.norm), self.cfg.eps,
+                 ptr(self.logits), ptr(self.pmax), ptr(self.pidx), self.T)
         call("q355_finish", ptr(self.pmax), ptr(self.pidx), self.nparts, ptr(self.tok), ptr(self.pos), self.T)
 
     def step(self):

@@ -84,6 +84,20 @@ int q355_head_logits(const uint8_t* qs, const void* d, int V, int K, const int64
                      float* logits, float* pmax, int32_t* pidx, int T, void* stream);
 int q355_head_nparts(int V);
 
+/* Tied-head variant for llama.cpp's Q6_K output.weight: the same fused final RMSNorm + Q8_1 + logits + argmax
+ * partials over a Q6_K matrix in the library's Q6_K planes (lab/gguf.py:tile_q6_k): lo uint8
+ * [V/16][K/32][16][16], hi uint8 [V/16][K/32][16][8], sc int8 [V/16][K/32][16][2], d fp16 [V/16][K/256][16];
+ * per 16-weight sub-block the int32 dot sc * (sum (v - 32) q_x) is exact. K % 256 == 0, K <= 1536.
+ * Replaces gemv_q6_source / head_v2_source (lab/qwen_kernels.py:608-678, lab/qwen_batched.py:681-833). */
+int q355_head_logits_q6k(const uint8_t* lo, const uint8_t* hi, const int8_t* sc, const void* d, int V, int K,
+                         const int64_t* h, const float* nw, double eps, float* logits, float* pmax, int32_t* pidx,
+                         int T, void* stream);
+
+/* Q6_K x Q8_1 GEMV (store), T = 1..4, K <= 1536: the parity entry point of the Q6_K planes.
+ * Replaces gemv_q6_source's plain form (lab/qwen_kernels.py:608-678). */
+int q355_gemv_q6_k_q8_1(const uint8_t* lo, const uint8_t* hi, const int8_t* sc, const void* d, int N, int K,
+                        const int8_t* xq, const void* xds, int T, float* y, void* stream);
+
 /* Greedy finish: tok[j] = argmax (lowest index on ties) over the head partials, pos[j] += 1.
  * Replaces FINISH / FINISH_MB (lab/qwen_kernels.py:222-282). */
 int q355_finish(const float* pmax, const int32_t* pidx, int nparts, int32_t* tok, int32_t* pos, int T,

@@ -127,6 +127,20 @@ def attn_prefill(q: np.ndarray, K: np.ndarray, V: np.ndarray, pos0: int, nh: int
     return out.reshape(P, nh * hd).astype(np.float32)
 
 
+class LinearQ6K:
+    """A Q6_K matrix (llama.cpp's output.weight) applied to Q8_1 activations, float64."""
+
+    def __init__(self, wbytes: np.ndarray, N: int, K: int):
+        self.b, self.N, self.K = wbytes, N, K
+        self._w = None
+
+    def __call__(self, x: np.ndarray) -> np.ndarray:
+        if self._w is None:
+            self._w = Q.dequant_q6_k(self.b, (self.N, self.K))
+        qx, dx, _ = Q.quantize_q8_1(np.asarray(x, np.float32))
+        return Q.dequant_q8_1(qx, dx).astype(np.float64) @ self._w.T
+
+
 class Linear:
     """One Q4_0 matrix W [N, K] from GGUF bytes, applied to Q8_1 activations."""
 
@@ -167,7 +181,8 @@ class Model:
                 "v": Linear(L["wv"], c.NKV * c.HD, c.H, self.mode), "o": Linear(L["wo"], c.H, c.NH * c.HD, self.mode),
                 "g": Linear(L["wg"], c.FFN, c.H, self.mode), "u": Linear(L["wu"], c.FFN, c.H, self.mode),
                 "d": Linear(L["wd"], c.H, c.FFN, self.mode)})
-        self.head = Linear(self.w["embed"], c.V, c.H, self.mode)
+        self.head = (LinearQ6K(self.w["head_q6k"], c.V, c.H) if "head_q6k" in self.w
+                     else Linear(self.w["embed"], c.V, c.H, self.mode))
 
     def new_cache(self):
         c = self.cfg

@@ -115,6 +115,42 @@ def gemv_q4_0_q8_1(wbytes: np.ndarray, N: int, K: int, qx: np.ndarray, dx: np.nd
     return y.astype(out_dtype)
 
 
+Q6_K_BYTES = 210        # ql[128] + qh[64] + int8 scales[16] + fp16 d, 256 weights
+
+
+def dequant_q6_k(b: np.ndarray, shape) -> np.ndarray:
+    """GGUF Q6_K bytes -> float64 values (llama.cpp block_q6_K; the reference reads it in lab/gguf.py:97-123).
+    Per 256-weight block and 128-weight half n, for l < 32 (v = 6-bit value, scale index is):
+      y[128n + l]      = d sc[8n + l/16]     (((ql[64n + l]      & 15) | ((qh[32n + l]      & 3) << 4)) - 32)
+      y[128n + l + 32] = d sc[8n + l/16 + 2] (((ql[64n + l + 32] & 15) | ((qh[32n + l] >> 2 & 3) << 4)) - 32)
+      y[128n + l + 64] = d sc[8n + l/16 + 4] (((ql[64n + l]      >> 4) | ((qh[32n + l] >> 4 & 3) << 4)) - 32)
+      y[128n + l + 96] = d sc[8n + l/16 + 6] (((ql[64n + l + 32] >> 4) | ((qh[32n + l] >> 6 & 3) << 4)) - 32)
+    pinned by: an element-by-element loop over the same formula on hand-set bytes (tests/test_oracle.py)."""
+    blk = np.asarray(b, np.uint8).reshape(-1, Q6_K_BYTES)
+    ql = blk[:, :128].astype(np.int64)
+    qh = blk[:, 128:192].astype(np.int64)
+    sc = blk[:, 192:208].view(np.int8).astype(np.float64)
+    d = blk[:, 208:210].copy().view(np.float16).astype(np.float64).reshape(-1)
+    y = np.empty((blk.shape[0], 256), np.float64)
+    l = np.arange(32)
+    for n in range(2):
+        a, c, h = ql[:, 64 * n + l], ql[:, 64 * n + 32 + l], qh[:, 32 * n + l]
+        vals = [(a & 15) | ((h & 3) << 4), (c & 15) | (((h >> 2) & 3) << 4),
+                (a >> 4) | (((h >> 4) & 3) << 4), (c >> 4) | (((h >> 6) & 3) << 4)]
+        for k, v in enumerate(vals):
+            s_idx = 8 * n + l // 16 + 2 * k
+            y[:, 128 * n + 32 * k + l] = d[:, None] * sc[:, s_idx] * (v - 32)
+    return y.reshape(shape)
+
+
+def gemv_q6_k_q8_1(wbytes: np.ndarray, N: int, K: int, qx: np.ndarray, dx: np.ndarray) -> np.ndarray:
+    """Y[T, N] = dequant(W_q6k) @ dequant(Q8_1 x)^T in float64 (every product is exact in f64: the sum is
+    the only rounding)."""
+    w = dequant_q6_k(wbytes, (N, K))
+    x = dequant_q8_1(qx, dx).astype(np.float64)
+    return x @ w.T
+
+
 def gemv_dequant_f64(wbytes: np.ndarray, N: int, K: int, qx: np.ndarray, dx: np.ndarray) -> np.ndarray:
     """Independent form of gemv_q4_0_q8_1 (dequantize both operands, float64 matmul); pins it."""
     w = dequant_q4_0(wbytes, (N, K)).astype(np.float64)

@@ -2,12 +2,12 @@
 oracle), the device repack and row orders, the synthetic weight generator, and the C-ABI library
 (loads and exports every symbol declared in include/qwen355.h; no GPU calls)."""
 import re
-import struct
 from pathlib import Path
 
 import numpy as np
 import pytest
 
+from ggufio import random_q6_k, write_gguf, write_qwen_gguf
 from lab import gguf, hip, qwen_kernels
 from lab import qwen_model as QM
 from oracle import quant as OQ
@@ -49,27 +49,6 @@ def test_row_orders():
     assert np.array_equal(t.reshape(4, 36)[0], b.reshape(4, 36)[2])
 
 
-def _write_gguf(path, tensors, meta):
-    """Minimal GGUF v3 writer (test fixture): tensors = {name: (ggml_type, dims, raw bytes)}."""
-    def s(x):
-        e = x.encode()
-        return struct.pack("<Q", len(e)) + e
-    out = bytearray(b"GGUF" + struct.pack("<IQQ", 3, len(tensors), len(meta)))
-    for k, v in meta.items():
-        out += s(k) + struct.pack("<I", 4) + struct.pack("<I", v)
-    off = 0
-    datas = []
-    for name, (typ, dims, raw) in tensors.items():
-        out += s(name) + struct.pack("<I", len(dims)) + struct.pack(f"<{len(dims)}Q", *dims)
-        out += struct.pack("<IQ", typ, off)
-        datas.append(raw)
-        off += -(-len(raw) // 32) * 32
-    out += b"\0" * (-len(out) % 32)
-    for raw in datas:
-        out += raw + b"\0" * (-len(raw) % 32)
-    Path(path).write_bytes(bytes(out))
-
-
 def _q6k_ref(block):
     """Q6_K decode written per element from the ggml block definition (ql[128], qh[64], scales[16], d)."""
     ql, qh = block[:128], block[128:192]
@@ -96,7 +75,7 @@ def test_gguf_reader_and_decoders(tmp_path):
     tensors = {"a.weight": (2, (64, 4), q4.tobytes()), "b": (0, (4, 64), w.tobytes()),
                "c": (1, (8,), f16.tobytes()), "h": (14, (256, 2), q6.tobytes())}
     p = tmp_path / "t.gguf"
-    _write_gguf(p, tensors, {"qwen2.block_count": 28})
+    write_gguf(p, tensors, {"qwen2.block_count": 28})
     g = gguf.GGUF(p)
     assert g.meta["qwen2.block_count"] == 28
     assert g.f32("a.weight").shape == (4, 64)
@@ -154,3 +133,38 @@ def test_missing_library_fails_loudly(monkeypatch, tmp_path):
     monkeypatch.setattr(hip, "_lib", None)
     with pytest.raises(hip.HipError, match="not built"):
         hip.lib()
+
+
+def test_q6_k_planes_decode_to_the_oracle_values():
+    """lab.gguf.tile_q6_k: decoding the planes with their documented bit layout gives the oracle's Q6_K values."""
+    rng = np.random.default_rng(9)
+    N, K = 32, 512
+    b = random_q6_k(N * K // 256, rng, d=0.01)
+    lo, hi, sc, d = gguf.tile_q6_k(b, N, K)
+    ref = OQ.dequant_q6_k(b, (N, K))
+    n = np.arange(N)
+    for k in range(K):
+        blk, i = divmod(k, 32)
+        lo_b = lo[n // 16, blk, n % 16, i % 16].astype(np.int64)
+        v = (lo_b & 15) if i < 16 else (lo_b >> 4)
+        hb = hi[n // 16, blk, n % 16, i % 8].astype(np.int64)
+        v = v | (((hb >> (2 * (i // 8))) & 3) << 4)
+        s = sc[n // 16, blk, n % 16, i // 16].astype(np.float64)
+        dd = d[n // 16, k // 256, n % 16].astype(np.float64)
+        assert np.array_equal(dd * s * (v - 32), ref[:, k])
+
+
+def test_weights_from_gguf_roundtrip(tmp_path):
+    """A Qwen2 GGUF written from random weights (Q6_K head) is read back into the same weight dict."""
+    cfg = QM.Config(L=2, V=512, FFN=256, H=256, NH=2, NKV=1, HD=128)
+    w = QM.random_weights(cfg, seed=3)
+    w["head_q6k"] = random_q6_k(cfg.V * cfg.H // 256, np.random.default_rng(4))
+    p = tmp_path / "qwen.gguf"
+    write_qwen_gguf(p, cfg, w)
+    cfg2, w2 = QM.weights_from_gguf(p)
+    assert (cfg2.H, cfg2.NH, cfg2.NKV, cfg2.HD, cfg2.FFN, cfg2.L, cfg2.V) == (256, 2, 1, 128, 256, 2, 512)
+    assert abs(cfg2.eps - 1e-6) < 1e-12 and cfg2.theta == 1e6
+    assert np.array_equal(w2["embed"], w["embed"]) and np.array_equal(w2["head_q6k"], w["head_q6k"])
+    for a, b in zip(w["layers"], w2["layers"]):
+        for k in a:
+            assert np.array_equal(np.asarray(a[k]).reshape(-1), np.asarray(b[k]).reshape(-1)), k

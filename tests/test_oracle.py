@@ -239,3 +239,23 @@ def test_model_prefill_equals_decode():
     assert np.allclose(h1, np.stack(hs), rtol=1e-4, atol=1e-4)
     assert np.allclose(c1["K"][:, :, :5].astype(np.float32), c2["K"][:, :, :5].astype(np.float32), atol=2e-3)
     assert np.allclose(c1["V"][:, :, :5].astype(np.float32), c2["V"][:, :, :5].astype(np.float32), atol=2e-3)
+
+
+def test_q6_k_decode_matches_encoded_values():
+    """Q6_K: chosen 6-bit values and scales, scattered into ql/qh bytes by an encoder written from the block
+    definition, decode back exactly (and the three independent decoders agree)."""
+    rng = np.random.default_rng(12)
+    v = rng.integers(0, 64, (3, 256))
+    sc = rng.integers(-128, 128, (3, 16))
+    blk = np.zeros((3, 210), np.uint8)
+    for b in range(3):
+        for n in range(256):
+            half, r = divmod(n, 128)
+            quarter, l = divmod(r, 32)
+            qi = 64 * half + l + (32 if quarter % 2 else 0)
+            blk[b, qi] |= (v[b, n] & 15) << (4 if quarter >= 2 else 0)
+            blk[b, 128 + 32 * half + l] |= (v[b, n] >> 4) << (2 * quarter)
+        blk[b, 192:208] = sc[b].astype(np.int8).view(np.uint8)
+        blk[b, 208:210] = np.array([0.125], np.float16).view(np.uint8)
+    y = OQ.dequant_q6_k(blk, (3, 256))
+    assert np.array_equal(y, 0.125 * np.repeat(sc, 16, axis=1) * (v - 32))
