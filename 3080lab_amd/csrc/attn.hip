@@ -39,39 +39,55 @@ __device__ __forceinline__ float wsum(float v) {
   return (rd_lane(v, 0) + rd_lane(v, 16)) + (rd_lane(v, 32) + rd_lane(v, 48));
 }
 __device__ __forceinline__ double exp_t(double v) { return exp(v); }
+__device__ __forceinline__ double max_t(double a, double b) { return fmax(a, b); }
+__device__ __forceinline__ float max_t(float a, float b) { return fmaxf(a, b); }
+template <int CTRL> __device__ __forceinline__ double dpp_t(double v) { return dpp_d<CTRL>(v); }
+template <int CTRL> __device__ __forceinline__ float dpp_t(float v) { return dpp<CTRL>(v); }
 __device__ __forceinline__ float exp_t(float v) { return expf(v); }
 
 // F = double: every step in f64 (the batch-1 decode path, exact against the f64 oracle to ~1e-12);
 // F = float: fp32 scores, softmax and P.V (the batched path, which also accumulates its GEMMs in fp32).
-template <int G, typename F>
-__global__ void __launch_bounds__(G * 64) k_attn_decode(const AttnArgs a) {
+// W waves per query head (1 or 2): wave W h + w takes positions (64 / W) w .. of the page; its lane
+// (position (64 / W) w + lane / W, dim part lane % W) scores 128 / W dims and the W lanes of a position sum;
+// with W = 2 the two waves of a head exchange their maximum and sum through LDS, so their P.V halves
+// (lane l: dims 2l, 2l+1) share the page maximum and add into one partial (o[128], m, l) per (head, page).
+// W = 2 halves the serial f64 work of each wave (the batch-1 latency); W = 1 keeps more workgroups
+// resident (the batched throughput).
+template <int G, typename F, int W>
+__global__ void __launch_bounds__(G * W * 64) k_attn_decode(const AttnArgs a) {
+  constexpr int PPW = PAGE / W, DPL = HD / W;
   __shared__ __align__(16) __half ks[PAGE][KROW];
   __shared__ __align__(16) __half vs[PAGE][HD];
   __shared__ __align__(16) F qf[G][HD];
+  __shared__ F xm[G][W], xl[G][W];
+  __shared__ __align__(16) F xo[W == 2 ? G : 1][HD];
 
   const int j = blockIdx.y;
   const int kvh = blockIdx.x / a.max_chunks, c = blockIdx.x % a.max_chunks;
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int hh = wv / W, part = wv % W;
   const int pos = a.pos[j];
   const int pg = a.block_table[(size_t)j * a.bt_stride + c];
-  const int hq = kvh * G + wv;
-  const half2 qv = ((const half2*)(a.q + ((size_t)j * a.nh + hq) * HD))[lane];
+  const int hq = kvh * G + hh;
   if (c * PAGE > pos) return;                       // chunk beyond the context: nothing to do
   const int nvalid = min(PAGE, pos + 1 - c * PAGE);
 
   const uint4* kp = (const uint4*)(a.kcache + ((size_t)pg * a.nkv + kvh) * PAGE * HD);
   const uint4* vp = (const uint4*)(a.vcache + ((size_t)pg * a.nkv + kvh) * PAGE * HD);
-  constexpr int NT = G * 64, PER = (PAGE * HD / 8 + NT - 1) / NT;
+  constexpr int NT = G * W * 64, PER = (PAGE * HD / 8 + NT - 1) / NT;
   uint4 kr[PER], vr[PER];
 #pragma unroll
   for (int i = 0; i < PER; ++i) {
-    const int e = min(threadIdx.x + NT * i, PAGE * HD / 8 - 1);   // clamped: loads stay unconditional
+    const int e = min((int)threadIdx.x + NT * i, PAGE * HD / 8 - 1);   // clamped: loads stay unconditional
     kr[i] = kp[e];
     vr[i] = vp[e];
   }
-  const float2 qq = __half22float2(qv);
-  qf[wv][2 * lane] = (F)qq.x;
-  qf[wv][2 * lane + 1] = (F)qq.y;
+  if (part == 0) {
+    const half2 qv = ((const half2*)(a.q + ((size_t)j * a.nh + hq) * HD))[lane];
+    const float2 qq = __half22float2(qv);
+    qf[hh][2 * lane] = (F)qq.x;
+    qf[hh][2 * lane + 1] = (F)qq.y;
+  }
 #pragma unroll
   for (int i = 0; i < PER; ++i) {
     const int e = threadIdx.x + NT * i;
@@ -83,14 +99,15 @@ __global__ void __launch_bounds__(G * 64) k_attn_decode(const AttnArgs a) {
   }
   __syncthreads();
 
-  // scores: lane p, this wave's head (4 independent partial sums)
-  F s = 0;
+  // scores: position p, dims DPL * dh .. + DPL - 1, then the W lanes of the position sum
+  const int p = PPW * part + lane / W, dh = lane % W;
+  F s;
   {
-    const F* qh = qf[wv];
+    const F* qh = qf[hh] + DPL * dh;
     F sp[4] = {0, 0, 0, 0};
 #pragma unroll
-    for (int i = 0; i < HD / 8; ++i) {
-      const uint4 kk = *(const uint4*)&ks[lane][8 * i];
+    for (int i = 0; i < DPL / 8; ++i) {
+      const uint4 kk = *(const uint4*)&ks[p][DPL * dh + 8 * i];
       const __half2* k2 = (const __half2*)&kk;
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
@@ -100,23 +117,42 @@ __global__ void __launch_bounds__(G * 64) k_attn_decode(const AttnArgs a) {
       }
     }
     s = (sp[0] + sp[1]) + (sp[2] + sp[3]);
+    if (W == 2) s += dpp_t<DPP_XOR1>(s);
   }
-  s = lane < nvalid ? s * (F)a.scale : (F)-INFINITY;
-  const F m = wmax(s);
-  const F e = lane < nvalid ? exp_t(s - m) : (F)0;
-  const F l = wsum(e);
+  s = p < nvalid ? s * (F)a.scale : (F)-INFINITY;
+  F m = wmax(s);                                    // with W = 2 each position twice: harmless
+  if (W == 2) {
+    if (lane == 0) xm[hh][part] = m;
+    __syncthreads();
+    m = max_t(xm[hh][0], xm[hh][1]);
+  }
+  const F e = p < nvalid ? exp_t(s - m) : (F)0;
+  const F lw = wsum(dh == 0 ? e : (F)0);
+  if (W == 2 && lane == 0) xl[hh][part] = lw;
 
-  // P.V: lane owns dims 2*lane, 2*lane+1; the weight of position p is broadcast from lane p (readlane)
+  // P.V over this wave's positions: lane owns dims 2*lane, 2*lane+1; position q's weight from lane W q
   F o[4][2] = {{0, 0}, {0, 0}, {0, 0}, {0, 0}};
 #pragma unroll
-  for (int p = 0; p < PAGE; ++p) {
-    const F ep = rd_lane(e, p);
-    const float2 v = __half22float2(((const __half2*)vs[p])[lane]);
-    o[p & 3][0] = fma(ep, (F)v.x, o[p & 3][0]);
-    o[p & 3][1] = fma(ep, (F)v.y, o[p & 3][1]);
+  for (int q = 0; q < PPW; ++q) {
+    const F ep = rd_lane(e, W * q);
+    const float2 v = __half22float2(((const __half2*)vs[PPW * part + q])[lane]);
+    o[q & 3][0] = fma(ep, (F)v.x, o[q & 3][0]);
+    o[q & 3][1] = fma(ep, (F)v.y, o[q & 3][1]);
   }
-  const F o0 = (o[0][0] + o[1][0]) + (o[2][0] + o[3][0]);
-  const F o1 = (o[0][1] + o[1][1]) + (o[2][1] + o[3][1]);
+  F o0 = (o[0][0] + o[1][0]) + (o[2][0] + o[3][0]);
+  F o1 = (o[0][1] + o[1][1]) + (o[2][1] + o[3][1]);
+  F l = lw;
+  if (W == 2) {
+    if (part == 1) {
+      xo[hh][2 * lane] = o0;
+      xo[hh][2 * lane + 1] = o1;
+    }
+    __syncthreads();
+    if (part == 1) return;
+    o0 += xo[hh][2 * lane];
+    o1 += xo[hh][2 * lane + 1];
+    l = xl[hh][0] + xl[hh][1];
+  }
   double* P = a.part + (((size_t)j * a.nh + hq) * a.max_chunks + c) * (HD + 2);
   ((double2*)P)[lane] = make_double2((double)o0, (double)o1);
   if (lane == 0) { P[HD] = (double)m; P[HD + 1] = (double)l; }

@@ -259,15 +259,15 @@ extern "C" int q355_attn_decode(const void* q, const void* kcache, const void* v
   const dim3 grid(nkv * max_chunks, T);
   if (fp32) {
     switch (nh / nkv) {
-      case 4: hipLaunchKernelGGL((k_attn_decode<4, float>), grid, dim3(256), 0, s, a); break;
-      case 6: hipLaunchKernelGGL((k_attn_decode<6, float>), grid, dim3(384), 0, s, a); break;
-      default: hipLaunchKernelGGL((k_attn_decode<8, float>), grid, dim3(512), 0, s, a); break;
+      case 4: hipLaunchKernelGGL((k_attn_decode<4, float, 1>), grid, dim3(256), 0, s, a); break;
+      case 6: hipLaunchKernelGGL((k_attn_decode<6, float, 1>), grid, dim3(384), 0, s, a); break;
+      default: hipLaunchKernelGGL((k_attn_decode<8, float, 1>), grid, dim3(512), 0, s, a); break;
     }
   } else {
     switch (nh / nkv) {
-      case 4: hipLaunchKernelGGL((k_attn_decode<4, double>), grid, dim3(256), 0, s, a); break;
-      case 6: hipLaunchKernelGGL((k_attn_decode<6, double>), grid, dim3(384), 0, s, a); break;
-      default: hipLaunchKernelGGL((k_attn_decode<8, double>), grid, dim3(512), 0, s, a); break;
+      case 4: hipLaunchKernelGGL((k_attn_decode<4, double, 2>), grid, dim3(512), 0, s, a); break;
+      case 6: hipLaunchKernelGGL((k_attn_decode<6, double, 2>), grid, dim3(768), 0, s, a); break;
+      default: hipLaunchKernelGGL((k_attn_decode<8, double, 2>), grid, dim3(1024), 0, s, a); break;
     }
   }
   if (int e = launched("attn_decode")) return e;

@@ -154,9 +154,9 @@ def weights_from_gguf(path) -> tuple:
         b, t = g.raw(name)
         if t.type != 2:
             raise ValueError(f"{name} is ggml type {t.type}; this path needs Q4_0")
-        return np.asarray(b, np.uint8).reshape(-1, 18)
+        return np.array(b, np.uint8).reshape(-1, 18)
 
-    f32 = lambda name: np.ascontiguousarray(g.f32(name), np.float32).reshape(-1)  # noqa: E731
+    f32 = lambda name: np.array(g.f32(name), np.float32).reshape(-1)  # noqa: E731  (a writable copy)
     w = {"embed": q4("token_embd.weight"), "norm": f32("output_norm.weight"), "layers": []}
     for i in range(cfg.L):
         p = f"blk.{i}."
@@ -169,7 +169,7 @@ def weights_from_gguf(path) -> tuple:
         b, t = g.raw("output.weight")
         if t.type != 14:
             raise ValueError(f"output.weight is ggml type {t.type}; Q6_K or a tied head is supported")
-        w["head_q6k"] = np.asarray(b, np.uint8).reshape(-1, 210)
+        w["head_q6k"] = np.array(b, np.uint8).reshape(-1, 210)
     return cfg, w
 
 
