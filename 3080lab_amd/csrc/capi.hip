@@ -118,6 +118,46 @@ extern "C" int q355_gemv_q4_0_q8_1(const uint8_t* qs, const void* d, int N, int 
   }
 }
 
+template <int T, int EPI>
+static void launch_gemv_bf16(const uint8_t* qs, const void* d, int N, int K, const void* x, float* y,
+                             const float* bias, hipStream_t s) {
+  const size_t lds = (size_t)T * K * 2;
+  if (K <= 16 * 3 * 32)
+    hipLaunchKernelGGL((k_gemv_bf16<T, 3, EPI>), dim3(N / 16), dim3(256), lds, s, qs, (const __half*)d, N, K,
+                       (const unsigned short*)x, y, bias);
+  else
+    hipLaunchKernelGGL((k_gemv_bf16<T, 18, EPI>), dim3(N / 16), dim3(256), lds, s, qs, (const __half*)d, N, K,
+                       (const unsigned short*)x, y, bias);
+}
+
+template <int EPI>
+static int gemv_bf16_t(const uint8_t* qs, const void* d, int N, int K, const void* x, int T, float* y,
+                       const float* bias, hipStream_t s) {
+  switch (T) {
+    case 1: launch_gemv_bf16<1, EPI>(qs, d, N, K, x, y, bias, s); break;
+    case 2: launch_gemv_bf16<2, EPI>(qs, d, N, K, x, y, bias, s); break;
+    case 3: launch_gemv_bf16<3, EPI>(qs, d, N, K, x, y, bias, s); break;
+    default: launch_gemv_bf16<4, EPI>(qs, d, N, K, x, y, bias, s); break;
+  }
+  return launched("gemv_q4_0_bf16");
+}
+
+extern "C" int q355_gemv_q4_0_bf16(const uint8_t* qs, const void* d, int N, int K, const void* x, int T, float* y,
+                                   const float* bias, int epi, void* stream) {
+  if (int e = check_mat("gemv_q4_0_bf16", qs, d, N, K)) return e;
+  REQUIRE(x && y, "gemv_q4_0_bf16: null pointer");
+  REQUIRE(T >= 1 && T <= 4, "gemv_q4_0_bf16: T=%d outside 1..4", T);
+  REQUIRE(K <= 9216, "gemv_q4_0_bf16: K=%d > 9216", K);
+  REQUIRE(epi >= 0 && epi <= 2, "gemv_q4_0_bf16: epi=%d (0 store, 1 resid, 2 bias)", epi);
+  REQUIRE(epi != 2 || bias, "gemv_q4_0_bf16: bias epilogue needs bias");
+  hipStream_t s = (hipStream_t)stream;
+  switch (epi) {
+    case 0: return gemv_bf16_t<EPI_STORE>(qs, d, N, K, x, T, y, bias, s);
+    case 1: return gemv_bf16_t<EPI_RESID>(qs, d, N, K, x, T, y, bias, s);
+    default: return gemv_bf16_t<EPI_BIAS>(qs, d, N, K, x, T, y, bias, s);
+  }
+}
+
 extern "C" int q355_gemv_blockdots(const uint8_t* qs, int N, int K, const int8_t* xq, int T, int32_t* out,
                                    void* stream) {
   REQUIRE(qs && xq && out, "gemv_blockdots: null pointer");

@@ -3,4 +3,5 @@
 #include "mmq.hip"
 #include "flash.hip"
 #include "mega.hip"
+#include "gemv_bf16.hip"
 #include "capi.hip"

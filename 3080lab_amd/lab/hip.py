@@ -21,6 +21,7 @@ _SIGS = {
     "q355_quant_q8_1": [_P, _P, _P, c_int, c_int, _P],
     "q355_rmsnorm_q8_1": [_P, _P, _P, _P, c_int, c_int, c_float, _P],
     "q355_gemv_q4_0_q8_1": [_P, _P, c_int, c_int, _P, _P, c_int, _P, _P, c_int, _P],
+    "q355_gemv_q4_0_bf16": [_P, _P, c_int, c_int, _P, c_int, _P, _P, c_int, _P],
     "q355_gemv_blockdots": [_P, c_int, c_int, _P, c_int, _P, _P],
     "q355_qkv_rope_kv": [_P, _P, c_int, _P, _P, c_double, _P, _P, _P, _P, _P, c_int, c_int, _P, _P, _P,
                          c_int, c_int, c_int, _P],

@@ -26,8 +26,12 @@ def gemv_source(S_: int = 1, epi: str = "store", quant: str = "q8_1", G: int = 1
     epi swiglu -> q355_ffn_gate_up (fused RMSNorm prologue + SwiGLU + Q8_1 epilogue);
     epi biasf_kv -> q355_qkv_rope_kv. S_ (the reference's split-K warp count) has no counterpart: the
     library picks the K split (16 or 32 k-lanes per workgroup) from K."""
+    if quant == "bf16":        # reference-parity mode: the reference's bf16-activation fp32 arithmetic
+        if epi not in _EPI_CODE:
+            raise ValueError(f"epilogue {epi!r} not in {EPILOGUES}")
+        return KernelSpec("q355_gemv_q4_0_bf16", {"epi": _EPI_CODE[epi]})
     if quant != "q8_1":
-        raise ValueError(f"quant={quant!r}: this build's GEMV consumes Q8_1 activations")
+        raise ValueError(f"quant={quant!r}: this build's GEMV consumes Q8_1 (or bf16) activations")
     if epi == "swiglu":
         return KernelSpec("q355_ffn_gate_up")
     if epi in ("biasf_kv", "qkv"):

@@ -53,6 +53,12 @@ int q355_rmsnorm_q8_1(const float* h, const float* w, int8_t* xq, void* xds, int
 int q355_gemv_q4_0_q8_1(const uint8_t* qs, const void* d, int N, int K, const int8_t* xq, const void* xds,
                         int T, float* y, const float* bias, int epi, void* stream);
 
+/* Reference-parity mode: Q4_0 x bf16 activations x [T][K] (bf16 bits), fp32 arithmetic as the reference's
+ * gemv_source (lab/qwen_kernels.py:14-113): per 32-block y += d * sum_i fmaf(q_i - 8, x_i); epi 0 store,
+ * 1 += (resid), 2 + bias. N % 16 == 0, K % 32 == 0, K <= 9216, T = 1..4. */
+int q355_gemv_q4_0_bf16(const uint8_t* qs, const void* d, int N, int K, const void* x, int T, float* y,
+                        const float* bias, int epi, void* stream);
+
 /* Debug: every per-block int32 dot out[T][N][K/32] = sum_i q_w,i (0..15) * q_x,i (bit-exact check).
  * Replaces the per-block timing/debug arguments of gemv_source (lab/qwen_kernels.py:46-53). */
 int q355_gemv_blockdots(const uint8_t* qs, int N, int K, const int8_t* xq, int T, int32_t* out, void* stream);

@@ -151,6 +151,26 @@ def gemv_q6_k_q8_1(wbytes: np.ndarray, N: int, K: int, qx: np.ndarray, dx: np.nd
     return x @ w.T
 
 
+def bf16_to_f32(bits: np.ndarray) -> np.ndarray:
+    """bf16 bit patterns (uint16) -> float32: the 16 bits are the top half of the float32 (bfloat16 definition).
+    pinned by: hand values (0x3F80 = 1.0, 0xC040 = -3.0, 0x0000 = 0)."""
+    return (np.asarray(bits, np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def f32_to_bf16(x: np.ndarray) -> np.ndarray:
+    """float32 -> bf16 bits, round to nearest even (finite inputs)."""
+    u = np.asarray(x, np.float32).view(np.uint32).astype(np.uint64)
+    u = u + 0x7FFF + ((u >> 16) & 1)
+    return (u >> 16).astype(np.uint16)
+
+
+def gemv_q4_0_bf16(wbytes: np.ndarray, N: int, K: int, xbits: np.ndarray) -> np.ndarray:
+    """Reference-parity GEMV (lab/qwen_kernels.py:14-113 semantics): Y[T, N] = dequant(W) @ x^T with x in bf16,
+    evaluated in float64 (the GPU's fp32 accumulation agrees to ~1e-6 relative)."""
+    w = dequant_q4_0(wbytes, (N, K)).astype(np.float64)
+    return bf16_to_f32(xbits).astype(np.float64) @ w.T
+
+
 def gemv_dequant_f64(wbytes: np.ndarray, N: int, K: int, qx: np.ndarray, dx: np.ndarray) -> np.ndarray:
     """Independent form of gemv_q4_0_q8_1 (dequantize both operands, float64 matmul); pins it."""
     w = dequant_q4_0(wbytes, (N, K)).astype(np.float64)

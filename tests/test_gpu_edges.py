@@ -161,3 +161,25 @@ def test_decode_at_last_cache_position(small):
     om.forward(prompt, 0, cache)
     h = om.forward([5], 127, cache)
     assert relerr(dec.logits[0].cpu().numpy(), om.logits(h)[0]) < 5e-2
+
+
+@pytest.mark.parametrize("N,K,T,epi", [(8960, 1536, 1, 0), (1536, 8960, 2, 1), (2048, 1536, 4, 2)])
+def test_gemv_bf16_reference_parity_mode(cuda, N, K, T, epi):
+    """Q4_0 x bf16 activations in fp32 (the reference's decode arithmetic) against the f64 dequantized product."""
+    import torch
+    rng = np.random.default_rng(N + K + T)
+    wb = gguf.quantize_q4_0(rng.standard_normal((N, K), dtype=np.float32) * np.float32(0.02))
+    W = QM.Q4Mat(wb, N, K, "cuda")
+    xb = OQ.f32_to_bf16(rng.standard_normal((T, K), dtype=np.float32))
+    bias = rng.standard_normal(N, dtype=np.float32)
+    y0 = rng.standard_normal((T, N), dtype=np.float32) if epi == 1 else np.zeros((T, N), np.float32)
+    y = dev(y0.copy())
+    call("q355_gemv_q4_0_bf16", ptr(W.qs), ptr(W.d), N, K, ptr(dev(xb.view(np.int16))), T, ptr(y),
+         ptr(dev(bias)), epi)
+    torch.cuda.synchronize()
+    ref = OQ.gemv_q4_0_bf16(wb, N, K, xb)
+    if epi == 1:
+        ref = ref + y0
+    elif epi == 2:
+        ref = ref + bias
+    assert relerr(y.cpu().numpy(), ref) < 1e-5

@@ -126,6 +126,7 @@ def test_kernel_specs_name_exported_symbols():
         assert sp.symbol in names
     with pytest.raises(ValueError):
         qwen_kernels.gemv_source(1, "store", quant="g128f32")
+    assert qwen_kernels.gemv_source(1, "resid", quant="bf16").symbol == "q355_gemv_q4_0_bf16"
 
 
 def test_missing_library_fails_loudly(monkeypatch, tmp_path):

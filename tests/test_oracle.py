@@ -259,3 +259,10 @@ def test_q6_k_decode_matches_encoded_values():
         blk[b, 208:210] = np.array([0.125], np.float16).view(np.uint8)
     y = OQ.dequant_q6_k(blk, (3, 256))
     assert np.array_equal(y, 0.125 * np.repeat(sc, 16, axis=1) * (v - 32))
+
+
+def test_bf16_decode_and_rounding():
+    assert OQ.bf16_to_f32(np.array([0x3F80, 0xC040, 0x0000], np.uint16)).tolist() == [1.0, -3.0, 0.0]
+    # 1 + 2^-8 is a bf16 midpoint between 1 and 1 + 2^-7: ties to even (1.0); 1 + 3 * 2^-8 rounds up
+    x = np.array([1.0, 1 + 2 ** -8, 1 + 3 * 2 ** -8, -2.5], np.float32)
+    assert OQ.bf16_to_f32(OQ.f32_to_bf16(x)).tolist() == [1.0, 1.0, 1 + 2 ** -6, -2.5]
