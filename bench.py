@@ -202,6 +202,26 @@ def cpu_baseline(w, cfg, prompt, n_steps: int = 6) -> dict:
                       f"single-threaded numpy, {dt:.1f} s; host os.cpu_count()={os.cpu_count()}"}
 
 
+def paired(args):
+    """Paired A/B rounds (scripts/decode_paired.py protocol) over the config-2 model: arms graph, graph_dup
+    (A/A control), mega and batched (B = 8), `args.steps` tokens each per round."""
+    from lab import paired as PA
+    from lab import qwen_model as QM
+    cfg = QM.QWEN15
+    w = QM.random_weights(cfg, seed=0)
+    dm = QM.DeviceModel(w, cfg, maxlen=2048 + 64)
+    prompt = np.random.default_rng(1).integers(0, cfg.V, 128)
+    arms = PA.decode_arms(dm, prompt, steps=args.steps)
+    if args.llama_bench:
+        arms["llama"] = PA.llama_bench_arm(*args.llama_bench)
+    for a in arms.values():                 # warm-up pass (caches, clocks), not recorded
+        a()
+    raw = PA.collect(arms, args.paired, log=log)
+    res, table = PA.summarize(raw, PA.DECODE_PAIRS)
+    log(table)
+    print(json.dumps({"paired": res, "steps_per_arm": args.steps, "raw": raw}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -211,6 +231,11 @@ def main():
     ap.add_argument("--quick", action="store_true", help="decode only (no roofline / GEMV / CPU legs)")
     ap.add_argument("--copy-probe", action="store_true",
                     help="only run a 64 MiB device-to-device copy 4 times (HBM counter calibration for rocprofv3 --pmc)")
+    ap.add_argument("--paired", type=int, default=0, metavar="ROUNDS",
+                    help="instead of the contract line: paired A/B rounds (graph vs persistent step, A/A control, "
+                         "batched B=8), one JSON line of ratio statistics")
+    ap.add_argument("--llama-bench", nargs=2, metavar=("BINARY", "GGUF"),
+                    help="with --paired: add an external llama.cpp llama-bench arm")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: --gpus {args.gpus} is not supported: this build measures one MI355X "
@@ -227,6 +252,9 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         print(json.dumps({"copy_probe_bytes": src.numel() * 4}))
+        return
+    if args.paired:
+        paired(args)
         return
     cfg = QM.QWEN15
     t0 = time.time()
