@@ -16,6 +16,8 @@ HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = ["-O3", "--offload-arch=gfx950", "-fPIC", "-shared", "-std=c++17",
          # no packed-fp32 VALU ops (v_pk_*_f32) in device code
          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+         # MFMA results in VGPRs: no v_accvgpr_read per result before the fp32 scaling
+         "-mllvm", "-amdgpu-mfma-vgpr-form",
          "-Wno-unused-result"]
 
 

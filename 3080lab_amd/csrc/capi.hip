@@ -378,11 +378,29 @@ static int launch_mmq(GemvArgs a, int KS, hipStream_t s) {
   return launched("mmq");
 }
 
+// Prefill sizes (STORE, RESID_FIX, SWIGLU_Q8 with at least one 128 x 64 tile per CU): the LDS-tiled kernel,
+// 2 x 2 waves of 64 rows x 64 tokens (32 tokens when 64-token tiles leave fewer than 2 workgroups per CU).
+// One K slice: each output has exactly one writer, so RESID_FIX is a plain read-add-write.
+template <int EPI>
+static int launch_mmq_big(GemvArgs a, hipStream_t s) {
+  const bool tg4 = (a.N / 128) * ((a.T + 127) / 128) >= 512;
+  constexpr size_t lds4 = 2 * LdsTile<2, 2, 4, TILE_CB>::BUF, lds2 = 2 * LdsTile<2, 2, 2, TILE_CB>::BUF;
+  if (tg4) {
+    hipLaunchKernelGGL((k_mmq_tile<2, 2, 4, EPI>), dim3(a.N / 128, 1, (a.T + 127) / 128), dim3(256), lds4, s, a);
+  } else {
+    hipLaunchKernelGGL((k_mmq_tile<2, 2, 2, EPI>), dim3(a.N / 128, 1, (a.T + 63) / 64), dim3(256), lds2, s, a);
+  }
+  return launched("mmq");
+}
+
 template <int EPI>
 static int launch_mmq_tg(const GemvArgs& a, int KS, hipStream_t s) {
+  if constexpr (EPI == EPI_STORE || EPI == EPI_RESID_FIX || EPI == EPI_SWIGLU_Q8)
+    if (a.N % 128 == 0 && (a.N / 128) * ((a.T + 63) / 64) >= 256) return launch_mmq_big<EPI>(a, s);
   // up to 64 tokens (decode batches): 16-token workgroups, several per CU, hide each other's latencies;
-  // prefill sizes: 32-token workgroups reuse every staged weight block twice
-  return a.T <= 64 ? launch_mmq<1, EPI>(a, KS, s) : launch_mmq<2, EPI>(a, KS, s);
+  // prefill sizes: 32- or 64-token workgroups reuse every staged weight block 2 or 4 times
+  if (a.T <= 64) return launch_mmq<1, EPI>(a, KS, s);
+  return a.T < 256 ? launch_mmq<2, EPI>(a, KS, s) : launch_mmq<4, EPI>(a, KS, s);
 }
 
 extern "C" int q355_mmq_q4_0_q8_1(const uint8_t* qs, const void* d, int N, int K, const int8_t* xq, const void* xds,

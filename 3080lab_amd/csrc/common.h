@@ -16,6 +16,7 @@
 #include <hip/hip_runtime.h>
 #include <hip/hip_fp16.h>
 #include <stdint.h>
+#include <type_traits>
 
 #define Q355_QK 32
 #define Q355_WAVE 64

@@ -278,6 +278,19 @@ __device__ __forceinline__ double row_value(A (&part)[NW][NT][T][16], int t, int
 
 __device__ __forceinline__ double silu_mul(double g, double u) { return g / (1.0 + exp(-g)) * u; }
 
+// fp32 form for fp32 partials (the MFMA paths, whose block sums are already fp32): partial sum over
+// waves in wave order, SiLU with the hardware exp2 and reciprocal
+template <int NW, int T, int NT>
+__device__ __forceinline__ float row_value_f(float (&part)[NW][NT][T][16], int t, int j, int r) {
+  float v = part[0][t][j][r];
+#pragma unroll
+  for (int w = 1; w < NW; ++w) v += part[w][t][j][r];
+  return v;
+}
+__device__ __forceinline__ float silu_mul_f(float g, float u) {
+  return g * __builtin_amdgcn_rcpf(1.f + __expf(-g)) * u;   // v_rcp_f32: 1 ulp
+}
+
 template <int NW, int T, int NT, int EPI, typename A>
 __device__ __forceinline__ void epilogue(const GemvArgs& a, A (&part)[NW][NT][T][16], int tile0) {
   const int N = a.N;
@@ -313,10 +326,16 @@ __device__ __forceinline__ void epilogue(const GemvArgs& a, A (&part)[NW][NT][T]
       const int j = e >> 5, k = e & 31;
       if (j >= a.T) break;                                      // uniform per 32-lane group
       const int rg = 2 * k, ru = 2 * k + 1;
-      const double g = row_value<NW, T, NT>(part, rg >> 4, j, rg & 15);
-      const double u = row_value<NW, T, NT>(part, ru >> 4, j, ru & 15);
+      float o;
+      if constexpr (std::is_same<A, float>::value) {
+        o = silu_mul_f(row_value_f<NW, T, NT>(part, rg >> 4, j, rg & 15),
+                       row_value_f<NW, T, NT>(part, ru >> 4, j, ru & 15));
+      } else {
+        o = (float)silu_mul(row_value<NW, T, NT>(part, rg >> 4, j, rg & 15),
+                            row_value<NW, T, NT>(part, ru >> 4, j, ru & 15));
+      }
       const int Nout = N / 2;
-      const int q = q8_1_lane32((float)silu_mul(g, u), a.ods + (size_t)j * (Nout / 32) + blockIdx.x, k == 0);
+      const int q = q8_1_lane32(o, a.ods + (size_t)j * (Nout / 32) + blockIdx.x, k == 0);
       a.oq[(size_t)j * Nout + blockIdx.x * 32 + k] = (int8_t)q;
     }
     return;

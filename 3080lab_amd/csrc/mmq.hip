@@ -3,7 +3,8 @@
 //
 // One Q4_0 block (k = 32) of one 16-row tile against 16 tokens is exactly one MFMA: A = the tile's
 // nibbles (unsigned 0..15 as int8), B = the tokens' int8 activations, C = the exact int32 block dots.
-// Then acc[row][tok] += d_w[row] * d_x[tok] * (dot - 8 * sum q_x[tok]) in fp32 -- the reference's MMQ
+// Then acc[row][tok] += d_w[row] * d_x[tok] * (dot - 8 * sum q_x[tok]) in fp32 (the -8 sum term enters as
+// the MFMA's accumulator input) -- the reference's MMQ
 // formula (lab/qwen_batched.py:1099-1101, 1237-1243), per block so each block keeps its own scales.
 // Operand layouts (checked on the GPU): lane l holds A[row l % 16][k = 8 (l / 16) .. +8],
 // B[k = 8 (l / 16) .. +8][col l % 16], and C[row 4 (l / 16) + v][col l % 16], v = 0..3.
@@ -36,20 +37,20 @@ template <int NT, int TG>
 __device__ __forceinline__ void mmq_block(const uint2 (&w)[NT], const uint2 (&dv)[NT], const int8_t* __restrict__ xq, int xstride,
                                           const float* xd, const int* xs, int ld, int bb, int li, int lg,
                                           float (&acc)[NT][TG][4]) {
+  // xs holds -8 * sum(q_x) per (token, block): it is the MFMA's C input, so the matrix core returns
+  // dot - 8 sum(q_x) directly
   v4i c[NT][TG];
   float dx[TG];
-  int s8[TG];
 #pragma unroll
   for (int g = 0; g < TG; ++g) {
     const int j = 16 * g + li;
     const long bx = *(const long*)(xq + (size_t)j * xstride + bb * 32 + 8 * lg);
     dx[g] = xd[j * ld + bb];
-    s8[g] = 8 * xs[j * ld + bb];
+    const int ns = xs[j * ld + bb];
+    const v4i ci = {ns, ns, ns, ns};
 #pragma unroll
-    for (int t = 0; t < NT; ++t) {
-      const v4i zero = {0, 0, 0, 0};
-      c[t][g] = __builtin_amdgcn_mfma_i32_16x16x32_i8(nib8(w[t], lg), bx, zero, 0, 0, 0);
-    }
+    for (int t = 0; t < NT; ++t)
+      c[t][g] = __builtin_amdgcn_mfma_i32_16x16x32_i8(nib8(w[t], lg), bx, ci, 0, 0, 0);
   }
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
@@ -58,7 +59,35 @@ __device__ __forceinline__ void mmq_block(const uint2 (&w)[NT], const uint2 (&dv
 #pragma unroll
     for (int g = 0; g < TG; ++g)
 #pragma unroll
-      for (int v = 0; v < 4; ++v) acc[t][g][v] = fmaf(dw[v] * dx[g], (float)(c[t][g][v] - s8[g]), acc[t][g][v]);
+      for (int v = 0; v < 4; ++v) acc[t][g][v] = fmaf(dw[v] * dx[g], (float)c[t][g][v], acc[t][g][v]);
+  }
+}
+
+// Stage the activations of blocks c0 .. c0 + nbc - 1 for tokens tok0 .. tok0 + TT - 1 into LDS: int8 rows
+// (xstride bytes per token), the fp16 scale as fp32 (xd) and -8 * the block's int sum (xs), both [TT][ld].
+// Two lanes per (token, block), 16 bytes each; tokens past ntok are staged as zero.
+template <int TT, int NW>
+__device__ __forceinline__ void stage_x(const GemvArgs& a, int8_t* xq, float* xd, int* xs, int xstride, int ld,
+                                        int tok0, int ntok, int c0, int nbc) {
+  const int K = a.K, nb = K / 32;
+  const int m = 2 * nbc;                               // pieces per token
+  const float inv = 1.f / (float)m;
+  for (int p = threadIdx.x; p < TT * m; p += NW * 64) {  // TT * m is even: lanes 2i, 2i+1 share a block
+    const int j = (int)(((float)p + 0.5f) * inv);      // exact: p / m lies >= 0.5 / m from an integer
+    const int r = p - j * m, bb = r >> 1, h = r & 1;
+    int4 q = make_int4(0, 0, 0, 0);
+    float dx = 0.f;
+    if (j < ntok) {
+      q = *(const int4*)(a.xq + (size_t)(tok0 + j) * K + (size_t)(c0 + bb) * 32 + 16 * h);
+      dx = __low2float(a.xds[(size_t)(tok0 + j) * nb + c0 + bb]);
+    }
+    *(int4*)(xq + (size_t)j * xstride + bb * 32 + 16 * h) = q;
+    int sum = dot4(q.x, 0x01010101, dot4(q.y, 0x01010101, dot4(q.z, 0x01010101, dot4(q.w, 0x01010101, 0))));
+    sum += __shfl_xor(sum, 1);
+    if (!h) {
+      xs[j * ld + bb] = -8 * sum;
+      xd[j * ld + bb] = dx;
+    }
   }
 }
 
@@ -82,6 +111,13 @@ __global__ void __launch_bounds__(NW * 64) k_mmq(const GemvArgs a) {
 
   const uint2* __restrict__ qs = (const uint2*)a.qs;
   const uint2* __restrict__ dd = (const uint2*)a.d;   // 4 fp16 scales = rows 4*lg .. 4*lg+3
+  const uint2* wq[NT];                              // this lane's nibbles / scales of block 0, per tile
+  const uint2* wd[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    wq[t] = qs + ((size_t)(tile0 + t) * nb * 16 + li) * 2 + (lg & 1);
+    wd[t] = dd + (size_t)(tile0 + t) * nb * 4 + lg;
+  }
   uint2 wA[NT], dA[NT], wB[NT], dB[NT];
   float acc[NT][TG][4];
 #pragma unroll
@@ -97,31 +133,13 @@ __global__ void __launch_bounds__(NW * 64) k_mmq(const GemvArgs a) {
       const int b = c0 + min(bb, nbc - 1);
 #pragma unroll
       for (int t = 0; t < NT; ++t) {
-        const size_t base = ((size_t)(tile0 + t) * nb + b) * 16;
-        w[t] = qs[(base + li) * 2 + (lg & 1)];
-        dv[t] = dd[(base >> 2) + lg];
+        w[t] = wq[t][b * 32];
+        dv[t] = wd[t][b * 4];
       }
     };
     load_blk(wv, wA, dA);                           // first weights of the chunk before the staging
     if (c0 != ks.b0) __syncthreads();               // previous chunk's LDS reads are done
-    // stage the activation chunk: task = (token, block): 32 B + d + sum(q); tokens past T are zero
-    for (int task = threadIdx.x; task < TT * nbc; task += NW * 64) {
-      const int j = task / nbc, bb = task % nbc;
-      int4 q0 = make_int4(0, 0, 0, 0), q1 = q0;
-      float dx = 0.f;
-      if (j < ntok) {
-        const int4* src = (const int4*)(a.xq + (size_t)(tok0 + j) * K + (size_t)(c0 + bb) * 32);
-        q0 = src[0];
-        q1 = src[1];
-        dx = __low2float(a.xds[(size_t)(tok0 + j) * nb + c0 + bb]);
-      }
-      int4* dst = (int4*)(xq + (size_t)j * xstride + bb * 32);
-      dst[0] = q0;
-      dst[1] = q1;
-      const int xv[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
-      xs[j * ch + bb] = sum_i8x32(xv);
-      xd[j * ch + bb] = dx;
-    }
+    stage_x<TT, NW>(a, xq, xd, xs, xstride, ch, tok0, ntok, c0, nbc);
     __syncthreads();
     Q355_TRACE_POINT(1);
 
@@ -205,24 +223,8 @@ __global__ void __launch_bounds__(NW * 64) k_mmq_reg(const GemvArgs a) {
     const int t = e / (nbs * 4), bb = (e / 4) % nbs, q = e & 3;
     wsc[e] = dd[(((size_t)(tile0 + t) * nb + ks.b0 + bb) * 16 >> 2) + q];
   }
-  // activations of the slice -> LDS: task = (token, block): 32 B + d + sum(q); tokens past T are zero
-  for (int task = threadIdx.x; task < TT * nbs; task += NW * 64) {
-    const int j = task / nbs, bb = task % nbs;
-    int4 q0 = make_int4(0, 0, 0, 0), q1 = q0;
-    float dx = 0.f;
-    if (j < ntok) {
-      const int4* src = (const int4*)(a.xq + (size_t)(tok0 + j) * K + (size_t)(ks.b0 + bb) * 32);
-      q0 = src[0];
-      q1 = src[1];
-      dx = __low2float(a.xds[(size_t)(tok0 + j) * nb + ks.b0 + bb]);
-    }
-    int4* dst = (int4*)(xq + (size_t)j * xstride + bb * 32);
-    dst[0] = q0;
-    dst[1] = q1;
-    const int xv[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
-    xs[j * nbs + bb] = sum_i8x32(xv);
-    xd[j * nbs + bb] = dx;
-  }
+  // activations of the slice -> LDS
+  stage_x<TT, NW>(a, xq, xd, xs, xstride, nbs, tok0, ntok, ks.b0, nbs);
   __syncthreads();
   Q355_TRACE_POINT(1);
   float acc[NT][TG][4];
@@ -268,6 +270,232 @@ __global__ void __launch_bounds__(NW * 64) k_mmq_reg(const GemvArgs a) {
   }
   epilogue<NW, TT, NT, EPI>(b, part, tile0);
   Q355_TRACE_POINT(5);
+}
+
+// Prefill-size GEMM tile: a workgroup computes (RW * 64 rows) x (CW * 16 TG tokens) with RW x CW = 4 waves,
+// each wave a 64 x 16 TG sub-tile (4 row tiles x TG token groups, 4 TG MFMAs per K block) over the full K slice.
+// K advances in chunks of CB blocks staged in LDS, double-buffered: the global loads of chunk c + 1 are
+// issued (16 B per lane, contiguous) before chunk c is computed, and written to the other buffer after.
+// The weights enter the MFMA as signed int8 16 (q - 8): nibble moved to the high half of the byte with its
+// top bit flipped, so no -8 sum(q_x) correction is needed; the 16 is folded into the activation scale,
+// stored as d_x / 16 (exact), so d_w (d_x / 16) (16 dot) is bit-identical to d_w d_x dot.
+// LDS per buffer (block-major inside each tile / token group, so every MFMA operand read is one
+// contiguous, conflict-free 512 B wave read):
+//   A  [RW*4 tiles][CB][16 rows][16 B]     nibbles as stored in HBM
+//   W  [RW*4 tiles][CB][16]                row scales (fp32)
+//   B  [CW*TG groups][CB][16 tokens][32 B] int8 activations; tokens 8..15 of a group swap their 16 B
+//                                          halves, so the two half-wave reads of a B operand use all banks
+//   X  [CB][CW*16*TG]                      activation scale / 16 (fp32)
+// Epilogues from registers: STORE, RESID_FIX (plain read-add-write: each output has one writer),
+// SWIGLU_Q8 (rows interleaved g0, u0, ...: each 64-row tile group is one Q8_1 block per token).
+template <int RW, int CW, int TG, int CB>
+struct LdsTile {
+  static constexpr int TW = CW * 16 * TG;            // tokens per workgroup
+  static constexpr int A = RW * 4 * CB * 256, W = RW * 4 * CB * 64, B = CW * TG * CB * 512;
+  static constexpr int X = CB * TW * 4;
+  static constexpr int BUF = A + W + B + X;
+};
+
+// nibbles of one Q4_0 row half (8 bytes) -> the 8 int8 values 16 (q - 8) of k-group g
+__device__ __forceinline__ long snib8(uint2 w, int g) {
+  const int sh = g < 2 ? 4 : 0;
+  const unsigned lo = ((w.x << sh) & 0xF0F0F0F0u) ^ 0x80808080u, hi = ((w.y << sh) & 0xF0F0F0F0u) ^ 0x80808080u;
+  return (long)(((unsigned long)hi << 32) | lo);
+}
+
+constexpr int TILE_CB = 4;                           // K blocks per LDS chunk
+
+template <int RW, int CW, int TG, int EPI>
+__global__ void __launch_bounds__(256) k_mmq_tile(const GemvArgs a) {
+  constexpr int CB = TILE_CB;
+  using L = LdsTile<RW, CW, TG, CB>;
+  constexpr int TW = L::TW;
+  constexpr int NA = RW * 4 * CB * 16;               // 16-byte pieces of A per chunk
+  constexpr int NWp = RW * 4 * CB * 2;               // of W (fp16 in HBM)
+  constexpr int NBp = TW * CB * 2;                   // of B (two per token and block)
+  static_assert(NA % 256 == 0 && NBp % 256 == 0 && NWp <= 256, "staging shape");
+  extern __shared__ __align__(16) char lds[];
+  const int K = a.K, nb = K / 32, N = a.N;
+  const KSlice ks(nb);
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int li = lane & 15, lg = lane >> 4;
+  const int wr = wv / CW, wc = wv % CW;              // this wave's row block and token block
+  const int tile0 = blockIdx.x * RW * 4;             // first 16-row tile of the workgroup
+  const int tok0 = blockIdx.z * TW;                  // first token of the workgroup
+  const int tid = threadIdx.x;
+
+  // staging registers for one chunk
+  uint4 rA[NA / 256], rB[NBp / 256], rW;
+  half2 rX[NBp / 256];
+  const uint4* __restrict__ gA = (const uint4*)a.qs;
+  const uint4* __restrict__ gW = (const uint4*)a.d;
+
+#define Q355_TILE_LOAD(c0)                                                                        \
+  {                                                                                               \
+    const int cb_ = (c0);                                                                         \
+    _Pragma("unroll") for (int i = 0; i < NA / 256; ++i) {                                        \
+      const int p = tid + 256 * i, t = p / (CB * 16), r = p % (CB * 16), blk = r >> 4;            \
+      rA[i] = cb_ + blk < ks.b1 ? gA[((size_t)(tile0 + t) * nb + cb_) * 16 + r] : make_uint4(0, 0, 0, 0); \
+    }                                                                                             \
+    if (tid < NWp) {                                                                              \
+      const int t = tid / (CB * 2), r = tid % (CB * 2), blk = r >> 1;                             \
+      rW = cb_ + blk < ks.b1 ? gW[((size_t)(tile0 + t) * nb + cb_) * 2 + r] : make_uint4(0, 0, 0, 0); \
+    }                                                                                             \
+    _Pragma("unroll") for (int i = 0; i < NBp / 256; ++i) {                                       \
+      const int p = tid + 256 * i, h = p & 1, j = (p >> 1) % TW, blk = p / (2 * TW);              \
+      const bool ok = tok0 + j < a.T && cb_ + blk < ks.b1;                                        \
+      rB[i] = ok ? *(const uint4*)(a.xq + (size_t)(tok0 + j) * K + (size_t)(cb_ + blk) * 32 + 16 * h) \
+                 : make_uint4(0, 0, 0, 0);                                                        \
+      rX[i] = ok && !h ? a.xds[(size_t)(tok0 + j) * nb + cb_ + blk] : half2{};                    \
+    }                                                                                             \
+  }
+
+#define Q355_TILE_STORE(buf)                                                                      \
+  {                                                                                               \
+    char* base_ = lds + (buf) * L::BUF;                                                           \
+    _Pragma("unroll") for (int i = 0; i < NA / 256; ++i)                                          \
+      *(uint4*)(base_ + (size_t)(tid + 256 * i) * 16) = rA[i];                                    \
+    if (tid < NWp) {                                                                              \
+      const __half2* h_ = (const __half2*)&rW;                                                    \
+      float4* dst_ = (float4*)(base_ + L::A + tid * 32);                                          \
+      dst_[0] = make_float4(__low2float(h_[0]), __high2float(h_[0]), __low2float(h_[1]), __high2float(h_[1])); \
+      dst_[1] = make_float4(__low2float(h_[2]), __high2float(h_[2]), __low2float(h_[3]), __high2float(h_[3])); \
+    }                                                                                             \
+    _Pragma("unroll") for (int i = 0; i < NBp / 256; ++i) {                                       \
+      const int p = tid + 256 * i, h = p & 1, j = (p >> 1) % TW, blk = p / (2 * TW);              \
+      *(uint4*)(base_ + L::A + L::W + (((j >> 4) * CB + blk) * 16 + (j & 15)) * 32 +              \
+                16 * (h ^ ((j >> 3) & 1))) = rB[i];                                               \
+      if (!h) ((float*)(base_ + L::A + L::W + L::B))[blk * TW + j] = __low2float(rX[i]) * 0.0625f; \
+    }                                                                                             \
+  }
+
+  float acc[4][TG][4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t)
+#pragma unroll
+    for (int g = 0; g < TG; ++g)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) acc[t][g][v] = 0.f;
+
+  int buf = 0;
+  if (ks.b0 < ks.b1) {
+    Q355_TILE_LOAD(ks.b0);
+    Q355_TILE_STORE(0);
+  }
+  __syncthreads();
+  for (int c0 = ks.b0; c0 < ks.b1; c0 += CB) {
+    const bool more = c0 + CB < ks.b1;               // uniform
+    if (more) Q355_TILE_LOAD(c0 + CB);
+    const char* base = lds + buf * L::BUF;
+    const char* sA = base + (size_t)(wr * 4) * CB * 256;
+    const char* sW = base + L::A + (size_t)(wr * 4) * CB * 64;
+    const char* sB = base + L::A + L::W + (size_t)(wc * TG) * CB * 512;
+    const float* sX = (const float*)(base + L::A + L::W + L::B) + wc * 16 * TG;
+#pragma unroll 1
+    for (int blk = 0; blk < CB; ++blk) {
+      long w[4];
+      float4 dw[4];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        w[t] = snib8(*(const uint2*)(sA + (t * CB + blk) * 256 + li * 16 + (lg & 1) * 8), lg);
+        dw[t] = *(const float4*)(sW + (t * CB + blk) * 64 + lg * 16);
+      }
+#pragma unroll
+      for (int g = 0; g < TG; ++g) {
+        const long bx = *(const long*)(sB + ((g * CB + blk) * 16 + li) * 32 + (lg ^ ((li >> 3) << 1)) * 8);
+        const float dx = sX[blk * TW + g * 16 + li];
+        const v4i zero = {0, 0, 0, 0};
+        v4i c[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) c[t] = __builtin_amdgcn_mfma_i32_16x16x32_i8(w[t], bx, zero, 0, 0, 0);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          acc[t][g][0] = fmaf(dw[t].x * dx, (float)c[t][0], acc[t][g][0]);
+          acc[t][g][1] = fmaf(dw[t].y * dx, (float)c[t][1], acc[t][g][1]);
+          acc[t][g][2] = fmaf(dw[t].z * dx, (float)c[t][2], acc[t][g][2]);
+          acc[t][g][3] = fmaf(dw[t].w * dx, (float)c[t][3], acc[t][g][3]);
+        }
+      }
+    }
+    if (more) {
+      Q355_TILE_STORE(buf ^ 1);
+      __syncthreads();
+      buf ^= 1;
+    }
+  }
+#undef Q355_TILE_LOAD
+#undef Q355_TILE_STORE
+
+  const int rt0 = tile0 + wr * 4;                    // this wave's first row tile
+#pragma unroll
+  for (int g = 0; g < TG; ++g) {
+    const int tok = tok0 + wc * 16 * TG + g * 16 + li;
+    const bool ok = tok < a.T;
+    if (EPI == EPI_STORE) {
+      if (ok)
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+          *(float4*)(a.y + (size_t)tok * N + (rt0 + t) * 16 + 4 * lg) =
+              make_float4(acc[t][g][0], acc[t][g][1], acc[t][g][2], acc[t][g][3]);
+    } else if (EPI == EPI_RESID_FIX) {
+      if (ok) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          long long* y = a.yfix + (size_t)tok * N + (rt0 + t) * 16 + 4 * lg;
+          if (gridDim.y == 1) {                      // this lane owns these 4 sums: plain read-add-write
+            longlong2* y2 = (longlong2*)y;
+            longlong2 p0 = y2[0], p1 = y2[1];
+            p0.x += to_fix((double)acc[t][g][0]); p0.y += to_fix((double)acc[t][g][1]);
+            p1.x += to_fix((double)acc[t][g][2]); p1.y += to_fix((double)acc[t][g][3]);
+            y2[0] = p0;
+            y2[1] = p1;
+          } else {
+#pragma unroll
+            for (int v = 0; v < 4; ++v)
+              atomicAdd((unsigned long long*)(y + v), (unsigned long long)to_fix((double)acc[t][g][v]));
+          }
+        }
+      }
+    } else if (EPI == EPI_SWIGLU_Q8) {
+      // this lane holds outputs 8t + 2lg, 8t + 2lg + 1 of its wave's 32; the 4 lanes of token li hold all 32
+      float o[4][2];
+      float amax = 0.f;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        o[t][0] = silu_mul_f(acc[t][g][0], acc[t][g][1]);
+        o[t][1] = silu_mul_f(acc[t][g][2], acc[t][g][3]);
+        amax = fmaxf(amax, fmaxf(fabsf(o[t][0]), fabsf(o[t][1])));
+      }
+      amax = fmaxf(amax, __shfl_xor(amax, 16));
+      amax = fmaxf(amax, __shfl_xor(amax, 32));
+      const __half d16 = __float2half_rn(amax / 127.0f);
+      const float df = __half2float(d16);
+      const float inv = df != 0.0f ? 1.0f / df : 0.0f;   // one division per token; x * (1 / d) per value
+      int sq = 0;
+      unsigned short pk[4];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        int q0 = 0, q1 = 0;
+        if (df != 0.0f) {
+          q0 = (int)roundf(o[t][0] * inv);
+          q1 = (int)roundf(o[t][1] * inv);
+          q0 = q0 > 127 ? 127 : (q0 < -127 ? -127 : q0);
+          q1 = q1 > 127 ? 127 : (q1 < -127 ? -127 : q1);
+        }
+        sq += q0 + q1;
+        pk[t] = (unsigned short)((q0 & 255) | ((q1 & 255) << 8));
+      }
+      sq += __shfl_xor(sq, 16);
+      sq += __shfl_xor(sq, 32);
+      if (ok) {
+        const int Nout = N / 2, ob = rt0 / 4;        // output Q8_1 block of this wave's 64 rows
+        int8_t* dst = a.oq + (size_t)tok * Nout + ob * 32 + 2 * lg;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) *(unsigned short*)(dst + 8 * t) = pk[t];
+        if (lg == 0) a.ods[(size_t)tok * (Nout / 32) + ob] = __halves2half2(d16, __float2half_rn(df * (float)sq));
+      }
+    }
+  }
 }
 
 }  // namespace q355

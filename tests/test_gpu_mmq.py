@@ -209,3 +209,65 @@ def test_batched_equals_single_sequence(small):
     ref = one.generate(16)[0]
     _, margins = om.greedy(prompt, 16)
     check_greedy(got[0], ref, margins, "batched vs batch-1")
+
+
+# Prefill-size products (the LDS-tiled kernel: N % 128 == 0 and at least 256 tiles of 128 x 64): the full
+# product is too large for the oracle, so a random subset of rows is checked against it.
+def rows_of(b, N, K, rows):
+    return b.reshape(N, K // 32, 18)[rows].reshape(-1, 18)
+
+
+@pytest.mark.parametrize("N,K,T", [(17920, 1536, 300), (4096, 1536, 2100), (4096, 1568, 700)])
+def test_mmq_tile_store(cuda, N, K, T):
+    import torch
+    W, b = mat(N, K, 3 * N + T)
+    x = np.random.default_rng(T).standard_normal((T, K), dtype=np.float32)
+    xq, xds, q, d = q8(x)
+    y = torch.zeros(T, N, device=cuda)
+    call("q355_mmq_q4_0_q8_1", ptr(W.qs), ptr(W.d), N, K, ptr(xq), ptr(xds), T, 0, ptr(y), None, None, None, None, None)
+    sync()
+    rows = np.sort(np.random.default_rng(N).choice(N, 48, replace=False))
+    ref = OQ.gemv_q4_0_q8_1(rows_of(b, N, K, rows), len(rows), K, q, d)
+    assert relerr(y.cpu().numpy()[:, rows], ref) < REL
+
+
+@pytest.mark.parametrize("N,K,T", [(2048, 2304, 1000), (4096, 1568, 700)])
+def test_mmq_tile_resid_fix(cuda, N, K, T):
+    W, b = mat(N, K, 5 * N + T)
+    rng = np.random.default_rng(N + T)
+    x = rng.standard_normal((T, K), dtype=np.float32)
+    xq, xds, q, d = q8(x)
+    h0 = rng.standard_normal((T, N), dtype=np.float32)
+    h = dev(np.round(h0.astype(np.float64) * QM.FIX_SCALE).astype(np.int64))
+    call("q355_mmq_q4_0_q8_1", ptr(W.qs), ptr(W.d), N, K, ptr(xq), ptr(xds), T, 6, None, ptr(h), None, None, None, None)
+    sync()
+    rows = np.sort(np.random.default_rng(K).choice(N, 48, replace=False))
+    got = h.cpu().numpy()[:, rows] / QM.FIX_SCALE - h0[:, rows]
+    ref = OQ.gemv_q4_0_q8_1(rows_of(b, N, K, rows), len(rows), K, q, d)
+    assert relerr(got, ref) < REL
+
+
+def test_mmq_tile_swiglu_q8(cuda):
+    import torch
+    F, K, T = 8960, 1536, 400
+    g = np.random.default_rng(11).standard_normal((F, K), dtype=np.float32) * np.float32(0.02)
+    u = np.random.default_rng(12).standard_normal((F, K), dtype=np.float32) * np.float32(0.02)
+    gb, ub = gguf.quantize_q4_0(g), gguf.quantize_q4_0(u)
+    gu = gguf.take_rows_q4_0(np.concatenate([gb, ub]), K, gguf.gate_up_row_order(F))
+    W = QM.Q4Mat(gu, 2 * F, K, "cuda")
+    x = np.random.default_rng(13).standard_normal((T, K), dtype=np.float32)
+    xq, xds, q, d = q8(x)
+    mq = torch.zeros(T, F, dtype=torch.int8, device=cuda)
+    mds = torch.zeros(T, F // 32, 2, dtype=torch.float16, device=cuda)
+    call("q355_mmq_q4_0_q8_1", ptr(W.qs), ptr(W.d), 2 * F, K, ptr(xq), ptr(xds), T, 7, None, None, ptr(mq), ptr(mds),
+         None, None)
+    sync()
+    for blk in (0, 101, F // 32 - 1):                      # whole Q8_1 output blocks of 32 outputs
+        cols = np.arange(32 * blk, 32 * blk + 32)
+        m = OM.silu_mul(OQ.gemv_q4_0_q8_1(rows_of(gb, F, K, cols), 32, K, q, d),
+                        OQ.gemv_q4_0_q8_1(rows_of(ub, F, K, cols), 32, K, q, d)).astype(np.float32)
+        qo, do, _ = OQ.quantize_q8_1(m)
+        got = OQ.dequant_q8_1(mq.cpu().numpy()[:, cols], mds.cpu().numpy()[:, blk:blk + 1, 0])
+        assert relerr(got, OQ.dequant_q8_1(qo, do)) < 2e-2
+        assert relerr(mds.cpu().numpy()[:, blk, 0], do[:, 0]) < 5e-3
+        assert (np.abs(mq.cpu().numpy()[:, cols].astype(int) - qo.astype(int)) > 1).mean() < 1e-3
