@@ -457,15 +457,34 @@ extern "C" int q355_qkv_finish(int64_t* acc, const float* bias, const float* rop
   return launched("qkv_finish");
 }
 
+static int pf_max_splits(int max_ctx) { return ((max_ctx - 1) / PAGE) / PF_SPLIT_PAGES + 1; }
+
+extern "C" int64_t q355_attn_prefill_ws_bytes(int P, int max_ctx, int nh, int nkv) {
+  if (P < 1 || max_ctx < P || nh < 1 || nkv < 1 || nh % nkv) return -1;
+  return (int64_t)(pf_ws_floats((P + PF_QB - 1) / PF_QB, nkv, nh / nkv, pf_max_splits(max_ctx)) * sizeof(float));
+}
+
 extern "C" int q355_attn_prefill(const void* q, const void* kcache, const void* vcache, const int32_t* block_table,
-                                 int pos0, int P, int nh, int nkv, float scale, float* out, void* stream) {
+                                 int pos0, int P, int nh, int nkv, float scale, float* out, void* ws,
+                                 int64_t ws_bytes, void* stream) {
   REQUIRE(q && kcache && vcache && block_table && out, "attn_prefill: null pointer");
   REQUIRE(P >= 1 && pos0 >= 0, "attn_prefill: P=%d pos0=%d", P, pos0);
-  REQUIRE(nh > 0 && nkv > 0 && nh % nkv == 0 && nh <= 65535, "attn_prefill: nh=%d nkv=%d", nh, nkv);
+  REQUIRE(nh > 0 && nkv > 0 && nh % nkv == 0 && nh / nkv >= 4 && nh / nkv <= 8 && nkv <= 65535,
+          "attn_prefill: nh=%d nkv=%d (4 to 8 query heads per KV head)", nh, nkv);
   PrefillAttnArgs a = {};
   a.q = (const __half*)q; a.kcache = (const __half*)kcache; a.vcache = (const __half*)vcache;
   a.block_table = block_table; a.pos0 = pos0; a.P = P; a.nh = nh; a.nkv = nkv; a.scale = scale; a.out = out;
-  hipLaunchKernelGGL(k_attn_prefill, dim3((P + 63) / 64, nh), dim3(256), 0, (hipStream_t)stream, a);
+  const int nqb = (P + PF_QB - 1) / PF_QB;
+  int splits = 1;
+  if (ws) {
+    splits = pf_max_splits(pos0 + P);
+    const int64_t need = (int64_t)(pf_ws_floats(nqb, nkv, nh / nkv, splits) * sizeof(float));
+    REQUIRE(ws_bytes >= need, "attn_prefill: workspace of %lld bytes, %lld needed for pos0 + P = %d",
+            (long long)ws_bytes, (long long)need, pos0 + P);
+    a.ws = (float*)ws;
+    a.max_splits = splits;
+  }
+  hipLaunchKernelGGL(k_attn_prefill, dim3(nqb, splits, nkv), dim3(64 * (nh / nkv)), 0, (hipStream_t)stream, a);
   return launched("attn_prefill");
 }
 

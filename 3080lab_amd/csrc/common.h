@@ -233,4 +233,11 @@ __device__ __forceinline__ int q8_1_lane32(float x, half2* ds, bool leader) {
   return q;
 }
 
+// Device-coherent relaxed accesses (agent scope): stores reach the memory every XCD reads and loads bypass
+// the non-coherent caches, so workgroups on different XCDs can exchange data without cache maintenance.
+template <typename T>
+__device__ __forceinline__ T ldc(const T* p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+template <typename T>
+__device__ __forceinline__ void stc(T* p, T v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+
 }  // namespace q355

@@ -5,9 +5,8 @@
 // its sequence; scores q.k * scale, softmax with running max (exp2 of scores pre-scaled by log2 e),
 // fp16 P, fp32 accumulation; output o = sum p v / sum p in fp32.
 //
-// Workgroup = 64 queries of one query head (grid (ceil(P/64), nh)); wave w owns queries 16w..16w+15.
-// Per 64-key block (one KV page): K (row-padded) and V transposed (Vt[dim][key]) are staged in LDS,
-// the next page is loaded into registers while the current one is used.
+// Per 64-key block (one KV page): K (row-padded) and V transposed (Vt[dim][key]) are staged in LDS once for
+// all query heads of the KV head; the next page is loaded into registers while the current one is used.
 // The wave computes S^T = K Q^T (A = K rows from LDS, B = the wave's Q rows held in registers), so lane l
 // holds scores of ONE query (l % 16) for keys 16t + 4(l/16) + v: the softmax statistics of a query live
 // in the 4 lanes l % 16 + 16g and need only two cross-lane steps. The same registers, converted to fp16,
@@ -26,141 +25,242 @@ typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef float f4 __attribute__((ext_vector_type(4)));
 
 constexpr int FK_ROW = HD + 8;     // K row in LDS (halves), padded
-constexpr int FV_ROW = PAGE + 8;   // Vt row (one dim, 64 keys) in LDS (halves), padded
+constexpr int FV_ROW = PAGE + 4;   // Vt row (one dim, 64 keys) in LDS (halves): 136 B, so the transposing
+                                   // 16 B writes of dims 2l and 2l + 1 spread over all banks
 
 __device__ __forceinline__ h8 as_h8(uint4 v) { return *reinterpret_cast<h8*>(&v); }
 
-__global__ void __launch_bounds__(256) k_attn_prefill(const PrefillAttnArgs a) {
+constexpr int CBN = PF_QB / 16;      // 16-query MFMA column blocks per wave
+
+// Workgroup = one KV head x 16 queries x one key split of up to 32 pages, G = nh / nkv waves (wave w: query
+// head kvh * G + w), so each staged K/V page serves all G heads of the group. Wave tile: 16 queries (one
+// MFMA column block; 147 VGPRs, so two workgroups share a CU). grid (ceil(P / 16), max splits, nkv), the
+// longest query blocks first;
+// 64 G threads. With several splits, each writes its unnormalized O, m and l to the workspace; the last
+// to arrive (counter per query block and KV head, reset by it) merges them and writes the output. Partials
+// and counters use device-coherent accesses: the splits may run on different XCDs.
+__global__ void __launch_bounds__(512) k_attn_prefill(const PrefillAttnArgs a) {
   __shared__ __align__(16) _Float16 ks[PAGE][FK_ROW];
   __shared__ __align__(16) _Float16 vt[HD][FV_ROW];
-  const int qb = blockIdx.x, hq = blockIdx.y;
-  const int kvh = hq / (a.nh / a.nkv);
+  const int G = a.nh / a.nkv;
+  const int qb = gridDim.x - 1 - blockIdx.x, split = blockIdx.y, kvh = blockIdx.z;
+  const int nsplit = a.ws ? pf_splits(a.pos0, qb, a.P) : 1;
+  if (split >= nsplit) return;                           // uniform per workgroup
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int li = lane & 15, lg = lane >> 4;
-  const int qi = qb * 64 + wv * 16 + li;                 // this lane's query (chunk index)
-  const int qc = min(qi, a.P - 1);
-  const int qpos = a.pos0 + qi;                          // its position
+  const int hq = kvh * G + wv;
   const int nq = a.nh * HD;
+  const int nthr = 64 * G;
 
-  // the wave's Q rows as B operands: dims 32c + 8g .. +8 of query qc
-  h8 qf[4];
+  int qi[CBN], qpos[CBN];
+  h8 qf[CBN][4];
 #pragma unroll
-  for (int c = 0; c < 4; ++c)
-    qf[c] = as_h8(*(const uint4*)(a.q + (size_t)qc * nq + hq * HD + 32 * c + 8 * lg));
-
-  const int last_key = min(a.pos0 + qb * 64 + 63, a.pos0 + a.P - 1);   // largest key any query here needs
-  const int nkb = last_key / PAGE + 1;
-  const float sl2 = a.scale * 1.4426950408889634f;       // scores in log2 units
-
-  // staging: 1024 uint4 per page for K and for V; 4 per thread (key e / 16, dims 8 (e % 16) .. +8)
-  u32x4 kr[4], vr[4];
-#define Q355_LOAD_PAGE(kb)                                                                     \
-  {                                                                                            \
-    const int pg_ = a.block_table[kb];                                                         \
-    const u32x4* kp_ = (const u32x4*)(a.kcache + ((size_t)pg_ * a.nkv + kvh) * PAGE * HD);     \
-    const u32x4* vp_ = (const u32x4*)(a.vcache + ((size_t)pg_ * a.nkv + kvh) * PAGE * HD);     \
-    kr[0] = kp_[threadIdx.x];                                                                  \
-    kr[1] = kp_[threadIdx.x + 256];                                                            \
-    kr[2] = kp_[threadIdx.x + 512];                                                            \
-    kr[3] = kp_[threadIdx.x + 768];                                                            \
-    vr[0] = vp_[threadIdx.x];                                                                  \
-    vr[1] = vp_[threadIdx.x + 256];                                                            \
-    vr[2] = vp_[threadIdx.x + 512];                                                            \
-    vr[3] = vp_[threadIdx.x + 768];                                                            \
+  for (int cb = 0; cb < CBN; ++cb) {
+    qi[cb] = qb * PF_QB + 16 * cb + li;
+    qpos[cb] = a.pos0 + qi[cb];
+    const int qc = min(qi[cb], a.P - 1);
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+      qf[cb][c] = as_h8(*(const uint4*)(a.q + (size_t)qc * nq + hq * HD + 32 * c + 8 * lg));
   }
 
-  float m = -INFINITY, l = 0.f;
-  f4 acc[8];
-#pragma unroll
-  for (int t = 0; t < 8; ++t) acc[t] = f4{0.f, 0.f, 0.f, 0.f};
+  const int last_key = min(a.pos0 + qb * PF_QB + PF_QB - 1, a.pos0 + a.P - 1);
+  const int kb0 = a.ws ? split * PF_SPLIT_PAGES : 0;
+  const int nkb = a.ws ? min(last_key / PAGE + 1, kb0 + PF_SPLIT_PAGES) : last_key / PAGE + 1;
+  const float sl2 = a.scale * 1.4426950408889634f;       // scores in log2 units
 
-  Q355_LOAD_PAGE(0);
-  for (int kb = 0; kb < nkb; ++kb) {
+  // staging: K as 1024 16 B pieces (key e / 16, dims 8 (e % 16) ..); V transposed: lane l of wave w takes
+  // dims 2l, 2l + 1 of the 8-key groups w, w + G, ...: 8 dword loads per group, packed into two 16 B rows
+  constexpr int VMAX = 2;                                // V key groups per thread (G >= 4)
+  u32x4 kr[4];
+  unsigned vr[VMAX][8];
+  const int kper = (1024 + nthr - 1) / nthr, vper = (8 + G - 1) / G;
+  // the page ids of this workgroup's key range, read once (each page's loads then wait on one latency)
+  __shared__ int pages[64];
+  for (int i = threadIdx.x; i < nkb - kb0 && i < 64; i += nthr) pages[i] = a.block_table[kb0 + i];
+  __syncthreads();
+#define Q355_LOAD_PAGE(kb)                                                                     \
+  {                                                                                            \
+    const int pg_ = (kb) - kb0 < 64 ? pages[(kb) - kb0] : a.block_table[kb];                   \
+    const u32x4* kp_ = (const u32x4*)(a.kcache + ((size_t)pg_ * a.nkv + kvh) * PAGE * HD);     \
+    const unsigned* vp_ = (const unsigned*)(a.vcache + ((size_t)pg_ * a.nkv + kvh) * PAGE * HD); \
+    _Pragma("unroll") for (int i = 0; i < 4; ++i) {                                            \
+      const int e = threadIdx.x + nthr * i;                                                    \
+      if (i < kper && e < 1024) kr[i] = kp_[e];                                                \
+    }                                                                                          \
+    _Pragma("unroll") for (int i = 0; i < VMAX; ++i) {                                         \
+      const int kg = wv + G * i;                                                               \
+      if (i < vper && kg < 8)                                                                  \
+        _Pragma("unroll") for (int u = 0; u < 8; ++u) vr[i][u] = vp_[(kg * 8 + u) * (HD / 2) + lane]; \
+    }                                                                                          \
+  }
+
+  float m[CBN], l[CBN];
+  f4 acc[CBN][8];
+#pragma unroll
+  for (int cb = 0; cb < CBN; ++cb) {
+    m[cb] = -INFINITY;
+    l[cb] = 0.f;
+#pragma unroll
+    for (int t = 0; t < 8; ++t) acc[cb][t] = f4{0.f, 0.f, 0.f, 0.f};
+  }
+
+  Q355_LOAD_PAGE(kb0);
+  for (int kb = kb0; kb < nkb; ++kb) {
     __syncthreads();                                       // previous page's LDS reads are done
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int e = threadIdx.x + 256 * i;
-      const int key = e >> 4, d0 = (e & 15) * 8;
-      *(u32x4*)&ks[key][d0] = kr[i];
-      const u32x4 w = vr[i];
+      const int e = threadIdx.x + nthr * i;
+      if (i < kper && e < 1024) *(u32x4*)&ks[e >> 4][(e & 15) * 8] = kr[i];
+    }
 #pragma unroll
-      for (int u = 0; u < 8; ++u)
-        *reinterpret_cast<unsigned short*>(&vt[d0 + u][key]) = (unsigned short)(w[u >> 1] >> (16 * (u & 1)));
+    for (int i = 0; i < VMAX; ++i) {
+      const int kg = wv + G * i;
+      if (i < vper && kg < 8) {
+        u32x4 lo, hi;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          lo[j] = __builtin_amdgcn_perm(vr[i][2 * j + 1], vr[i][2 * j], 0x05040100u);
+          hi[j] = __builtin_amdgcn_perm(vr[i][2 * j + 1], vr[i][2 * j], 0x07060302u);
+        }
+        *(u32x4*)&vt[2 * lane][kg * 8] = lo;
+        *(u32x4*)&vt[2 * lane + 1][kg * 8] = hi;
+      }
     }
     __syncthreads();
     Q355_LOAD_PAGE(min(kb + 1, nkb - 1));                  // next page (clamped: unconditional), in flight now
 
-    // S^T tiles: keys 16t + (4g + v), query li
-    f4 s[4];
+    // S^T tiles: keys 16t + (4g + v), query li of column block cb; each K operand feeds both blocks
+    f4 s[CBN][4];
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
-      s[t] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int cb = 0; cb < CBN; ++cb) s[cb][t] = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
         const h8 kA = as_h8(*(const uint4*)&ks[16 * t + li][32 * c + 8 * lg]);
-        s[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kA, qf[c], s[t], 0, 0, 0);
+#pragma unroll
+        for (int cb = 0; cb < CBN; ++cb) s[cb][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kA, qf[cb][c], s[cb][t], 0, 0, 0);
       }
     }
-    // causal mask + running max (keys beyond the query's position, and queries past P, get -inf)
-    float bm = -INFINITY;
+    h8 pB[CBN][2];
+    // causal mask only where the page reaches past the block's first query (uniform); queries past P need
+    // none: each query column of S, P and O is independent and is never stored
+    const bool diag = (kb + 1) * PAGE - 1 > a.pos0 + qb * PF_QB;
 #pragma unroll
-    for (int t = 0; t < 4; ++t)
+    for (int cb = 0; cb < CBN; ++cb) {
+      if (diag) {
 #pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const int key = kb * PAGE + 16 * t + 4 * lg + v;
-        const float x = (key <= qpos && qi < a.P) ? s[t][v] * sl2 : -INFINITY;
-        s[t][v] = x;
-        bm = fmaxf(bm, x);
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+          for (int v = 0; v < 4; ++v)
+            if (kb * PAGE + 16 * t + 4 * lg + v > qpos[cb]) s[cb][t][v] = -INFINITY;
       }
-    bm = fmaxf(bm, __shfl_xor(bm, 16));
-    bm = fmaxf(bm, __shfl_xor(bm, 32));
-    const float mn = fmaxf(m, bm);
-    const float ms = mn == -INFINITY ? 0.f : mn;           // fully masked so far: keep exp2 finite
-    const float alpha = exp2f(m - ms);
-    float rs = 0.f;
-    _Float16 ph[4][4];
+      float bm = -INFINITY;                                // raw-score max; scaled once below
 #pragma unroll
-    for (int t = 0; t < 4; ++t)
+      for (int t = 0; t < 4; ++t) bm = fmaxf(bm, fmaxf(fmaxf(s[cb][t][0], s[cb][t][1]), fmaxf(s[cb][t][2], s[cb][t][3])));
+      bm = fmaxf(bm, __shfl_xor(bm, 16));
+      bm = fmaxf(bm, __shfl_xor(bm, 32));
+      const float mn = fmaxf(m[cb], bm * sl2);
+      const float ms = mn == -INFINITY ? 0.f : mn;         // fully masked so far: keep exp2 finite
+      const float alpha = __builtin_amdgcn_exp2f(m[cb] - ms);
+      float rs = 0.f;
 #pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const float p = exp2f(s[t][v] - ms);
-        rs += p;
-        ph[t][v] = (_Float16)p;
+      for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const float p = __builtin_amdgcn_exp2f(fmaf(s[cb][t][v], sl2, -ms));
+          rs += p;
+          pB[cb][t >> 1][4 * (t & 1) + v] = (_Float16)p;
+        }
+      rs += __shfl_xor(rs, 16);
+      rs += __shfl_xor(rs, 32);
+      l[cb] = l[cb] * alpha + rs;
+      m[cb] = mn;
+      if (__any(alpha != 1.f)) {                           // the running max moved for some query of the wave
+#pragma unroll
+        for (int t = 0; t < 8; ++t) acc[cb][t] *= alpha;
       }
-    rs += __shfl_xor(rs, 16);
-    rs += __shfl_xor(rs, 32);
-    l = l * alpha + rs;
-    m = mn;
+    }
+    // O^T += Vt P^T over two 32-key chunks; each Vt operand feeds both blocks
 #pragma unroll
-    for (int t = 0; t < 8; ++t) acc[t] *= alpha;
-    // O^T += Vt P^T over two 32-key chunks
-#pragma unroll
-    for (int c = 0; c < 2; ++c) {
-      h8 pB;
-#pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        pB[v] = ph[2 * c][v];
-        pB[4 + v] = ph[2 * c + 1][v];
-      }
+    for (int c = 0; c < 2; ++c)
 #pragma unroll
       for (int dt = 0; dt < 8; ++dt) {
         const _Float16* row = &vt[16 * dt + li][0];
         const uint2 lo = *(const uint2*)(row + 32 * c + 4 * lg);
         const uint2 hi = *(const uint2*)(row + 32 * c + 16 + 4 * lg);
-        const uint4 vv = make_uint4(lo.x, lo.y, hi.x, hi.y);
-        acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(vv), pB, acc[dt], 0, 0, 0);
+        const h8 vA = as_h8(make_uint4(lo.x, lo.y, hi.x, hi.y));
+#pragma unroll
+        for (int cb = 0; cb < CBN; ++cb)
+          acc[cb][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vA, pB[cb][c], acc[cb][dt], 0, 0, 0);
+      }
+  }
+#undef Q355_LOAD_PAGE
+  if (nsplit > 1) {
+    // partial -> workspace (same lane order on both sides), then arrival count
+    const size_t slot = (((size_t)qb * a.nkv + kvh) * a.max_splits + split) * G + wv;
+    float4* po = (float4*)a.ws + slot * (CBN * 8 * 64);
+    float* pml = a.ws + (size_t)gridDim.x * a.nkv * a.max_splits * G * (CBN * 8 * 64 * 4) + slot * (CBN * 16 * 2);
+#pragma unroll
+    for (int cb = 0; cb < CBN; ++cb) {
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) stc((float*)&po[(cb * 8 + dt) * 64 + lane] + v, acc[cb][dt][v]);
+      if (lg == 0) {
+        stc(pml + (cb * 16 + li) * 2, m[cb]);
+        stc(pml + (cb * 16 + li) * 2 + 1, l[cb]);
+      }
+    }
+    __builtin_amdgcn_s_waitcnt(0);                         // this wave's coherent stores have completed
+    __syncthreads();
+    __shared__ int last;
+    int* cnt = (int*)(a.ws + pf_ws_floats(gridDim.x, a.nkv, G, a.max_splits) - (size_t)gridDim.x * a.nkv) +
+               qb * a.nkv + kvh;
+    if (threadIdx.x == 0) {
+      last = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == nsplit - 1;
+      if (last) stc(cnt, 0);                             // every split has arrived: ready for the next call
+    }
+    __syncthreads();
+    if (!last) return;
+    // merge: rescale every split to the common max
+    const size_t slot0 = (((size_t)qb * a.nkv + kvh) * a.max_splits) * G + wv;
+    const float4* pa = (const float4*)a.ws + slot0 * (CBN * 8 * 64);   // read with coherent loads
+    const float* pmla = a.ws + (size_t)gridDim.x * a.nkv * a.max_splits * G * (CBN * 8 * 64 * 4) + slot0 * (CBN * 16 * 2);
+#pragma unroll
+    for (int cb = 0; cb < CBN; ++cb) {
+      float mt = m[cb];
+      for (int s2 = 0; s2 < nsplit; ++s2)
+        if (s2 != split) mt = fmaxf(mt, ldc(pmla + (size_t)s2 * G * (CBN * 32) + (cb * 16 + li) * 2));
+      const float f0 = __builtin_amdgcn_exp2f(m[cb] - mt);
+      l[cb] *= f0;
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) acc[cb][dt] *= f0;
+      for (int s2 = 0; s2 < nsplit; ++s2) {
+        if (s2 == split) continue;
+        const float* ml = pmla + (size_t)s2 * G * (CBN * 32) + (cb * 16 + li) * 2;
+        const float f = __builtin_amdgcn_exp2f(ldc(ml) - mt);
+        l[cb] += f * ldc(ml + 1);
+        const float4* src = pa + (size_t)s2 * G * (CBN * 8 * 64) + cb * 8 * 64 + lane;
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt) {
+#pragma unroll
+          for (int v = 0; v < 4; ++v) acc[cb][dt][v] += f * ldc((const float*)&src[dt * 64] + v);
+        }
       }
     }
   }
-#undef Q355_LOAD_PAGE
-  if (qi < a.P) {
-    const float inv = 1.f / l;
-    float* o = a.out + (size_t)qi * nq + hq * HD;
 #pragma unroll
-    for (int dt = 0; dt < 8; ++dt)
-      *(float4*)(o + 16 * dt + 4 * lg) = make_float4(acc[dt][0] * inv, acc[dt][1] * inv, acc[dt][2] * inv,
-                                                     acc[dt][3] * inv);
-  }
+  for (int cb = 0; cb < CBN; ++cb)
+    if (qi[cb] < a.P) {
+      const float inv = 1.f / l[cb];
+      float* o = a.out + (size_t)qi[cb] * nq + hq * HD;
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt)
+        *(float4*)(o + 16 * dt + 4 * lg) = make_float4(acc[cb][dt][0] * inv, acc[cb][dt][1] * inv,
+                                                       acc[cb][dt][2] * inv, acc[cb][dt][3] * inv);
+    }
 }
 
 }  // namespace q355

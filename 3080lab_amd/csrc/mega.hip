@@ -104,10 +104,6 @@ __device__ __forceinline__ MegaWs mega_ws(char* p, int max_chunks, int L) {
 }
 
 // device-scope (cross-workgroup coherent) loads and stores
-template <typename T>
-__device__ __forceinline__ T ldc(const T* p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
-template <typename T>
-__device__ __forceinline__ void stc(T* p, T v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
 
 __device__ __forceinline__ bool seq_reached(unsigned v, unsigned seq) { return (int)(v - seq) >= 0; }
 

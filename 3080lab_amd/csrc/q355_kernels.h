@@ -88,7 +88,23 @@ struct PrefillAttnArgs {
   int pos0, P, nh, nkv;
   float scale;
   float* out;                  // [P][nh*HD] fp32
+  // split over keys (null: one workgroup per query block takes all its keys): partials
+  // [n_qblocks][nkv][max_splits][G][CBN][8][64] float4 (O^T in MFMA accumulator order), m / l
+  // [n_qblocks][nkv][max_splits][G][CBN][16][2], arrival counters [n_qblocks][nkv]
+  float* ws;
+  int max_splits;
 };
+
+constexpr int PF_QB = 16;              // queries per prefill-attention workgroup (16 per MFMA column block)
+constexpr int PF_SPLIT_PAGES = 32;     // KV pages per key split (2048 keys)
+
+__host__ __device__ inline int pf_splits(int pos0, int qb, int P) {   // key splits of query block qb
+  const int last = (pos0 + (qb + 1) * PF_QB - 1 < pos0 + P - 1) ? pos0 + (qb + 1) * PF_QB - 1 : pos0 + P - 1;
+  return (last / PAGE) / PF_SPLIT_PAGES + 1;
+}
+__host__ __device__ inline size_t pf_ws_floats(int nqb, int nkv, int G, int max_splits) {
+  return (size_t)nqb * nkv * max_splits * G * ((PF_QB / 16) * (8 * 64 * 4 + 16 * 2)) + (size_t)nqb * nkv;
+}
 
 struct AttnArgs {
   const __half* q;             // [T][nh*HD] RoPE'd fp16 queries

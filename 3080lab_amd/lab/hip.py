@@ -38,7 +38,8 @@ _SIGS = {
     "q355_rmsnorm_fix_q8_1": [_P, _P, _P, _P, c_int, c_int, c_double, _P],
     "q355_mmq_q4_0_q8_1": [_P, _P, c_int, c_int, _P, _P, c_int, c_int, _P, _P, _P, _P, _P, _P, _P],
     "q355_mmq_nparts": [c_int],
-    "q355_attn_prefill": [_P, _P, _P, _P, c_int, c_int, c_int, c_int, c_float, _P, _P],
+    "q355_attn_prefill": [_P, _P, _P, _P, c_int, c_int, c_int, c_int, c_float, _P, _P, ctypes.c_int64, _P],
+    "q355_attn_prefill_ws_bytes": [c_int, c_int, c_int, c_int],
     "q355_mega_ws_bytes": [c_int, c_int],
     "q355_mega_layer_bytes": [],
     "q355_mega_decode": [_P, c_int, _P, _P, _P, c_int, _P, _P, _P, c_int, c_double, _P, _P, _P, _P, _P,
@@ -46,7 +47,8 @@ _SIGS = {
     "q355_qkv_finish": [_P, _P, _P, _P, _P, _P, c_int, c_int, _P, _P, _P, c_int, c_int, c_int, _P],
 }
 # entry points returning something other than an int status
-_VALUE_FUNCS = {"q355_head_nparts", "q355_mmq_nparts", "q355_mega_ws_bytes", "q355_mega_layer_bytes"}
+_VALUE_FUNCS = {"q355_head_nparts", "q355_mmq_nparts", "q355_mega_ws_bytes", "q355_mega_layer_bytes",
+                "q355_attn_prefill_ws_bytes"}
 
 _lib = None
 
@@ -69,7 +71,7 @@ def lib():
         for name, args in _SIGS.items():
             f = getattr(L, name)
             f.argtypes = args
-            f.restype = ctypes.c_int64 if name == "q355_mega_ws_bytes" else c_int
+            f.restype = ctypes.c_int64 if name.endswith("_ws_bytes") else c_int
         _lib = L
     return _lib
 

@@ -225,6 +225,9 @@ class Prefill:
         self.ids = torch.zeros(P, dtype=torch.int32, device=dev)
         self.pos = torch.zeros(P, dtype=torch.int32, device=dev)
         self.fin_pos = torch.zeros(1, dtype=torch.int32, device=dev)
+        # key-split workspace of the attention (zeroed once; its arrival counters reset themselves)
+        nbytes = call("q355_attn_prefill_ws_bytes", P, dec.max_chunks * 64, c.NH, c.NKV)
+        self.attn_ws = torch.zeros((nbytes + 3) // 4, dtype=torch.float32, device=dev)
         self.scale = 1.0 / math.sqrt(c.HD)
 
     def layer(self, i: int, P: int, pos0: int):
@@ -237,7 +240,7 @@ class Prefill:
         call("q355_qkv_finish", ptr(self.qkv_acc), ptr(L["qkv_b"]), ptr(m.cos), ptr(m.sin), ptr(self.pos),
              ptr(d.block_table), d.max_chunks, 0, ptr(d.kc[i]), ptr(d.vc[i]), ptr(self.q), c.NH, c.NKV, P)
         call("q355_attn_prefill", ptr(self.q), ptr(d.kc[i]), ptr(d.vc[i]), ptr(d.block_table), pos0, P, c.NH, c.NKV,
-             self.scale, ptr(self.att))
+             self.scale, ptr(self.att), ptr(self.attn_ws), self.attn_ws.numel() * 4)
         call("q355_quant_q8_1", ptr(self.att), ptr(self.xq), ptr(self.xds), P, c.NH * c.HD)
         W = L["o"]
         call("q355_mmq_q4_0_q8_1", ptr(W.qs), ptr(W.d), W.N, W.K, ptr(self.xq), ptr(self.xds), P, 6,

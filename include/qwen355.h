@@ -161,10 +161,16 @@ int q355_qkv_finish(int64_t* acc, const float* bias, const float* rope_cos, cons
 /* Causal GQA prefill attention (fp16 MFMA, fp32 accumulation) for one sequence: queries q fp16
  * [P][nh*128] at positions pos0 .. pos0 + P - 1 attend to keys 0 .. their own position in the paged cache
  * (block_table = the sequence's page ids, >= (pos0 + P - 1) / 64 + 1 of them; K/V of every attended
- * position already written); out fp32 [P][nh*128] = softmax(q k^T * scale) v.
+ * position already written); out fp32 [P][nh*128] = softmax(q k^T * scale) v. 4 to 8 query heads per KV
+ * head. ws (optional, ws_bytes >= q355_attn_prefill_ws_bytes(P, pos0 + P, nh, nkv), zeroed once by the
+ * caller and reused across calls) lets long query rows split their keys over several workgroups; with
+ * ws = NULL each 32-query block takes all its keys in one workgroup. Calls sharing a workspace must not
+ * overlap.
  * Replaces flash_prefill_v3_source (lab/qwen_batched.py:1795-2037). */
 int q355_attn_prefill(const void* q, const void* kcache, const void* vcache, const int32_t* block_table, int pos0,
-                      int P, int nh, int nkv, float scale, float* out, void* stream);
+                      int P, int nh, int nkv, float scale, float* out, void* ws, int64_t ws_bytes, void* stream);
+/* Workspace bytes of q355_attn_prefill for chunks of up to P queries with pos0 + P <= max_ctx (-1: bad sizes). */
+int64_t q355_attn_prefill_ws_bytes(int P, int max_ctx, int nh, int nkv);
 
 /* ---- persistent whole-step decode (batch 1) ---- */
 

@@ -20,9 +20,13 @@ def relerr(a, b):
     return float(np.abs(a - b).max() / max(np.abs(b).max(), 1e-30))
 
 
+@pytest.mark.parametrize("split", [False, True])
 @pytest.mark.parametrize("P,pos0,nh,nkv", [(1, 0, 12, 2), (64, 0, 12, 2), (100, 0, 12, 2), (200, 37, 12, 2),
-                                           (130, 64, 8, 2), (17, 250, 12, 2)])
-def test_attn_prefill_matches_oracle(cuda, P, pos0, nh, nkv):
+                                           (130, 64, 8, 2), (17, 250, 12, 2), (700, 0, 12, 2), (300, 555, 16, 2),
+                                           (77, 1500, 12, 2), (64, 4100, 12, 2), (130, 2000, 8, 2)])
+def test_attn_prefill_matches_oracle(cuda, P, pos0, nh, nkv, split):
+    """Without and with the key-split workspace (splits of 2048 keys: pos0 = 4100 merges 3 splits; pos0 = 2000
+    makes a query block straddle a split boundary, so some of its queries see no key of the last split)."""
     import torch
     rng = np.random.default_rng(P * 1000 + pos0)
     n = pos0 + P
@@ -43,17 +47,28 @@ def test_attn_prefill_matches_oracle(cuda, P, pos0, nh, nkv):
     out = torch.zeros(P, nh * 128, device=cuda)
     q_t = torch.from_numpy(q.reshape(P, -1)).cuda()
     table_t = torch.from_numpy(table).cuda()
-    call("q355_attn_prefill", ptr(q_t), ptr(kc_t), ptr(vc_t), ptr(table_t), pos0, P, nh, nkv, 1.0 / math.sqrt(128),
-         ptr(out))
-    torch.cuda.synchronize()
-    ref = OM.attn_prefill(q, K, V, pos0, nh, nkv)
-    assert relerr(out.cpu().numpy(), ref) < ATT_TOL
+    ws, nb = None, 0
+    if split:
+        nb = call("q355_attn_prefill_ws_bytes", P, n, nh, nkv)
+        ws = torch.zeros(nb // 4, dtype=torch.float32, device=cuda)
+    for rep in range(2 if split else 1):                  # the second call reuses the self-resetting counters
+        out.zero_()
+        call("q355_attn_prefill", ptr(q_t), ptr(kc_t), ptr(vc_t), ptr(table_t), pos0, P, nh, nkv,
+             1.0 / math.sqrt(128), ptr(out), ptr(ws) if split else None, nb)
+        torch.cuda.synchronize()
+        ref = OM.attn_prefill(q, K, V, pos0, nh, nkv)
+        assert relerr(out.cpu().numpy(), ref) < ATT_TOL
+    if split:
+        cnt = ws[-((P + 15) // 16) * nkv:].view(torch.int32)
+        assert int(cnt.abs().sum()) == 0
 
 
 def test_attn_prefill_bad_args(cuda):
     from lab.hip import HipError
     with pytest.raises(HipError, match="attn_prefill"):
-        call("q355_attn_prefill", 1, 1, 1, 1, 0, 0, 12, 2, 0.1, 1)
+        call("q355_attn_prefill", 1, 1, 1, 1, 0, 0, 12, 2, 0.1, 1, None, 0)
+    with pytest.raises(HipError, match="workspace"):
+        call("q355_attn_prefill", 1, 1, 1, 1, 0, 2048, 12, 2, 0.1, 1, 1, 100)
 
 
 CFG_S = QM.Config(L=2, V=4096)
