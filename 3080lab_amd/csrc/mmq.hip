@@ -2,10 +2,10 @@
 // (T = 5..32 tokens per launch) and prefill (T up to 64 per launch, grid.z over token groups).
 //
 // One Q4_0 block (k = 32) of one 16-row tile against 16 tokens is exactly one MFMA: A = the tile's
-// nibbles (unsigned 0..15 as int8), B = the tokens' int8 activations, C = the exact int32 block dots.
-// Then acc[row][tok] += d_w[row] * d_x[tok] * (dot - 8 * sum q_x[tok]) in fp32 (the -8 sum term enters as
-// the MFMA's accumulator input) -- the reference's MMQ
-// formula (lab/qwen_batched.py:1099-1101, 1237-1243), per block so each block keeps its own scales.
+// weights as int8 16 (q - 8), B = the tokens' int8 activations, C = 16 x the exact int32 block dots
+// dot(q - 8, q_x) = dot - 8 sum q_x. Then acc[row][tok] += d_w[row] * (d_x[tok] / 16) * C in fp32, which
+// equals d_w d_x (dot - 8 sum q_x) bit for bit -- the reference's MMQ formula
+// (lab/qwen_batched.py:1099-1101, 1237-1243), per block so each block keeps its own scales.
 // Operand layouts (checked on the GPU): lane l holds A[row l % 16][k = 8 (l / 16) .. +8],
 // B[k = 8 (l / 16) .. +8][col l % 16], and C[row 4 (l / 16) + v][col l % 16], v = 0..3.
 // Workgroup = NT tiles x one K slice (grid.y) x 16*TG tokens (grid.z token groups); its NW waves take
@@ -20,12 +20,14 @@ namespace q355 {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 
-// nibbles of one Q4_0 row half (8 bytes) -> the 8 int8 A values of k-group g (g < 2: low, else high)
-__device__ __forceinline__ long nib8(uint2 w, int g) {
-  const int sh = (g >> 1) * 4;
-  const unsigned lo = (w.x >> sh) & 0x0F0F0F0Fu, hi = (w.y >> sh) & 0x0F0F0F0Fu;
+// nibbles of one Q4_0 row half (8 bytes) -> the 8 int8 values 16 (q - 8) of k-group g
+__device__ __forceinline__ long snib8(uint2 w, int g) {
+  const int sh = g < 2 ? 4 : 0;
+  const unsigned lo = ((w.x << sh) & 0xF0F0F0F0u) ^ 0x80808080u, hi = ((w.y << sh) & 0xF0F0F0F0u) ^ 0x80808080u;
   return (long)(((unsigned long)hi << 32) | lo);
 }
+
+constexpr int TILE_CB = 4;                           // K blocks per LDS chunk
 
 #ifndef Q355_TRACE_POINT
 #define Q355_TRACE_POINT(k)
@@ -33,24 +35,22 @@ __device__ __forceinline__ long nib8(uint2 w, int g) {
 
 // One K block (LDS column bb) against NT tiles x TG token groups: all NT * TG MFMAs are issued before
 // any of their results is scaled, so the matrix-core latency overlaps instead of stalling each product.
+// Weights enter as 16 (q - 8) (snib8) and xd holds d_x / 16, so d_w xd (16 dot') = d_w d_x (dot - 8 sum q_x)
+// exactly, with no activation sums.
 template <int NT, int TG>
 __device__ __forceinline__ void mmq_block(const uint2 (&w)[NT], const uint2 (&dv)[NT], const int8_t* __restrict__ xq, int xstride,
-                                          const float* xd, const int* xs, int ld, int bb, int li, int lg,
-                                          float (&acc)[NT][TG][4]) {
-  // xs holds -8 * sum(q_x) per (token, block): it is the MFMA's C input, so the matrix core returns
-  // dot - 8 sum(q_x) directly
+                                          const float* xd, int ld, int bb, int li, int lg, float (&acc)[NT][TG][4]) {
   v4i c[NT][TG];
   float dx[TG];
+  const v4i zero = {0, 0, 0, 0};
 #pragma unroll
   for (int g = 0; g < TG; ++g) {
     const int j = 16 * g + li;
     const long bx = *(const long*)(xq + (size_t)j * xstride + bb * 32 + 8 * lg);
     dx[g] = xd[j * ld + bb];
-    const int ns = xs[j * ld + bb];
-    const v4i ci = {ns, ns, ns, ns};
 #pragma unroll
     for (int t = 0; t < NT; ++t)
-      c[t][g] = __builtin_amdgcn_mfma_i32_16x16x32_i8(nib8(w[t], lg), bx, ci, 0, 0, 0);
+      c[t][g] = __builtin_amdgcn_mfma_i32_16x16x32_i8(snib8(w[t], lg), bx, zero, 0, 0, 0);
   }
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
@@ -64,30 +64,25 @@ __device__ __forceinline__ void mmq_block(const uint2 (&w)[NT], const uint2 (&dv
 }
 
 // Stage the activations of blocks c0 .. c0 + nbc - 1 for tokens tok0 .. tok0 + TT - 1 into LDS: int8 rows
-// (xstride bytes per token), the fp16 scale as fp32 (xd) and -8 * the block's int sum (xs), both [TT][ld].
-// Two lanes per (token, block), 16 bytes each; tokens past ntok are staged as zero.
+// (xstride bytes per token) and the fp16 scale / 16 as fp32 (xd, [TT][ld]). One lane per (token, block
+// half), 16 bytes each; tokens past ntok are staged as zero.
 template <int TT, int NW>
-__device__ __forceinline__ void stage_x(const GemvArgs& a, int8_t* xq, float* xd, int* xs, int xstride, int ld,
+__device__ __forceinline__ void stage_x(const GemvArgs& a, int8_t* xq, float* xd, int xstride, int ld,
                                         int tok0, int ntok, int c0, int nbc) {
   const int K = a.K, nb = K / 32;
   const int m = 2 * nbc;                               // pieces per token
   const float inv = 1.f / (float)m;
-  for (int p = threadIdx.x; p < TT * m; p += NW * 64) {  // TT * m is even: lanes 2i, 2i+1 share a block
+  for (int p = threadIdx.x; p < TT * m; p += NW * 64) {
     const int j = (int)(((float)p + 0.5f) * inv);      // exact: p / m lies >= 0.5 / m from an integer
     const int r = p - j * m, bb = r >> 1, h = r & 1;
     int4 q = make_int4(0, 0, 0, 0);
     float dx = 0.f;
     if (j < ntok) {
       q = *(const int4*)(a.xq + (size_t)(tok0 + j) * K + (size_t)(c0 + bb) * 32 + 16 * h);
-      dx = __low2float(a.xds[(size_t)(tok0 + j) * nb + c0 + bb]);
+      if (!h) dx = __low2float(a.xds[(size_t)(tok0 + j) * nb + c0 + bb]) * 0.0625f;
     }
     *(int4*)(xq + (size_t)j * xstride + bb * 32 + 16 * h) = q;
-    int sum = dot4(q.x, 0x01010101, dot4(q.y, 0x01010101, dot4(q.z, 0x01010101, dot4(q.w, 0x01010101, 0))));
-    sum += __shfl_xor(sum, 1);
-    if (!h) {
-      xs[j * ld + bb] = -8 * sum;
-      xd[j * ld + bb] = dx;
-    }
+    if (!h) xd[j * ld + bb] = dx;
   }
 }
 
@@ -104,7 +99,6 @@ __global__ void __launch_bounds__(NW * 64) k_mmq(const GemvArgs a) {
   const int xstride = ch * 32 + 16;                 // padded LDS row (bytes) per token
   int8_t* xq = (int8_t*)lds;
   float* xd = (float*)(lds + (size_t)TT * xstride);
-  int* xs = (int*)(xd + TT * ch);
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int li = lane & 15, lg = lane >> 4;
   const int tile0 = blockIdx.x * NT;
@@ -139,12 +133,12 @@ __global__ void __launch_bounds__(NW * 64) k_mmq(const GemvArgs a) {
     };
     load_blk(wv, wA, dA);                           // first weights of the chunk before the staging
     if (c0 != ks.b0) __syncthreads();               // previous chunk's LDS reads are done
-    stage_x<TT, NW>(a, xq, xd, xs, xstride, ch, tok0, ntok, c0, nbc);
+    stage_x<TT, NW>(a, xq, xd, xstride, ch, tok0, ntok, c0, nbc);
     __syncthreads();
     Q355_TRACE_POINT(1);
 
     auto compute_blk = [&](int bb, const uint2 (&w)[NT], const uint2 (&dv)[NT]) {
-      mmq_block<NT, TG>(w, dv, xq, xstride, xd, xs, ch, bb, li, lg, acc);
+      mmq_block<NT, TG>(w, dv, xq, xstride, xd, ch, bb, li, lg, acc);
     };
     // 2-deep pipeline over this wave's blocks wv, wv + NW, ... of the chunk
     int bb = wv;
@@ -203,8 +197,7 @@ __global__ void __launch_bounds__(NW * 64) k_mmq_reg(const GemvArgs a) {
   const int xstride = nbs * 32 + 16;
   int8_t* xq = (int8_t*)lds;
   float* xd = (float*)(lds + (size_t)TT * xstride);
-  int* xs = (int*)(xd + TT * nbs);
-  uint2* wsc = (uint2*)(xs + TT * nbs);                 // [NT][nbs][4] groups of 4 fp16 row scales
+  uint2* wsc = (uint2*)(xd + 2 * TT * nbs);             // [NT][nbs][4] groups of 4 fp16 row scales
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int li = lane & 15, lg = lane >> 4;
   const int tile0 = blockIdx.x * NT;
@@ -224,7 +217,7 @@ __global__ void __launch_bounds__(NW * 64) k_mmq_reg(const GemvArgs a) {
     wsc[e] = dd[(((size_t)(tile0 + t) * nb + ks.b0 + bb) * 16 >> 2) + q];
   }
   // activations of the slice -> LDS
-  stage_x<TT, NW>(a, xq, xd, xs, xstride, nbs, tok0, ntok, ks.b0, nbs);
+  stage_x<TT, NW>(a, xq, xd, xstride, nbs, tok0, ntok, ks.b0, nbs);
   __syncthreads();
   Q355_TRACE_POINT(1);
   float acc[NT][TG][4];
@@ -241,7 +234,7 @@ __global__ void __launch_bounds__(NW * 64) k_mmq_reg(const GemvArgs a) {
       uint2 dv[NT];
 #pragma unroll
       for (int t = 0; t < NT; ++t) dv[t] = wsc[(t * nbs + bb) * 4 + lg];
-      mmq_block<NT, TG>(w[i], dv, xq, xstride, xd, xs, nbs, bb, li, lg, acc);
+      mmq_block<NT, TG>(w[i], dv, xq, xstride, xd, nbs, bb, li, lg, acc);
     }
   }
   Q355_TRACE_POINT(2);
@@ -295,15 +288,6 @@ struct LdsTile {
   static constexpr int X = CB * TW * 4;
   static constexpr int BUF = A + W + B + X;
 };
-
-// nibbles of one Q4_0 row half (8 bytes) -> the 8 int8 values 16 (q - 8) of k-group g
-__device__ __forceinline__ long snib8(uint2 w, int g) {
-  const int sh = g < 2 ? 4 : 0;
-  const unsigned lo = ((w.x << sh) & 0xF0F0F0F0u) ^ 0x80808080u, hi = ((w.y << sh) & 0xF0F0F0F0u) ^ 0x80808080u;
-  return (long)(((unsigned long)hi << 32) | lo);
-}
-
-constexpr int TILE_CB = 4;                           // K blocks per LDS chunk
 
 template <int RW, int CW, int TG, int EPI>
 __global__ void __launch_bounds__(256) k_mmq_tile(const GemvArgs a) {
