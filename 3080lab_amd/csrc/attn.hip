@@ -46,7 +46,7 @@ template <int CTRL> __device__ __forceinline__ float dpp_t(float v) { return dpp
 __device__ __forceinline__ float exp_t(float v) { return expf(v); }
 
 // F = double: every step in f64 (the batch-1 decode path, exact against the f64 oracle to ~1e-12);
-// F = float: fp32 scores, softmax and P.V (the batched path, which also accumulates its GEMMs in fp32).
+// F = float: fp32 scores, softmax and P.V (not launched: the batched path runs k_attn_decode_mfma below).
 // W waves per query head (1 or 2): wave W h + w takes positions (64 / W) w .. of the page; its lane
 // (position (64 / W) w + lane / W, dim part lane % W) scores 128 / W dims and the W lanes of a position sum;
 // with W = 2 the two waves of a head exchange their maximum and sum through LDS, so their P.V halves
@@ -156,6 +156,128 @@ __global__ void __launch_bounds__(G * W * 64) k_attn_decode(const AttnArgs a) {
   double* P = a.part + (((size_t)j * a.nh + hq) * a.max_chunks + c) * (HD + 2);
   ((double2*)P)[lane] = make_double2((double)o0, (double)o1);
   if (lane == 0) { P[HD] = (double)m; P[HD + 1] = (double)l; }
+}
+
+// ---------------------------------------------------------------------------------------------
+// fp32 path on the matrix cores (the batched decode): one wave per (token j, KV head, page c), the G query
+// heads of the group are the MFMA columns (16 columns, G used). S^T = K Q^T takes K rows straight from
+// global memory as A operands; V is transposed into the wave's own LDS slice through dword gathers
+// (lane l: dims 2l, 2l + 1 of 8 keys, packed in pairs), so O^T = Vt P^T reads 8-key runs. P is rounded to
+// fp16 for the MFMA (fp32 accumulation). Output: the same partial (o, m, l) as k_attn_decode, m in
+// natural-log units. No barriers: each wave only touches its own LDS slice.
+typedef _Float16 ah8 __attribute__((ext_vector_type(8)));
+typedef float af4 __attribute__((ext_vector_type(4)));
+constexpr int AV_ROW = PAGE + 4;   // Vt row (one dim, 64 keys) in halves: 136 B, so the dim 2l / 2l + 1
+                                   // 16 B writes spread over all banks
+
+__global__ void __launch_bounds__(256) k_attn_decode_mfma(const AttnArgs a) {
+  __shared__ __align__(16) _Float16 vt[4][HD][AV_ROW];
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int li = lane & 15, lg = lane >> 4;
+  const int G = a.nh / a.nkv;
+  const int nc4 = (a.max_chunks + 3) / 4;
+  const int j = blockIdx.y, kvh = blockIdx.x / nc4, c = (blockIdx.x % nc4) * 4 + wv;
+  const int pos = a.pos[j];
+  if (c >= a.max_chunks || c * PAGE > pos) return;   // uniform per wave
+  const int nvalid = min(PAGE, pos + 1 - c * PAGE);
+  const int pg = a.block_table[(size_t)j * a.bt_stride + c];
+  const _Float16* kp = (const _Float16*)a.kcache + ((size_t)pg * a.nkv + kvh) * PAGE * HD;
+  const unsigned* vp = (const unsigned*)(a.vcache + ((size_t)pg * a.nkv + kvh) * PAGE * HD);
+
+  // every load of the page first: K operands (16 B per lane per tile), V dwords, q
+  uint4 kA[4][4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t)
+#pragma unroll
+    for (int cc = 0; cc < 4; ++cc) kA[t][cc] = *(const uint4*)(kp + (16 * t + li) * HD + 32 * cc + 8 * lg);
+  unsigned vr[8][8];
+#pragma unroll
+  for (int kg = 0; kg < 8; ++kg)
+#pragma unroll
+    for (int u = 0; u < 8; ++u) vr[kg][u] = vp[(kg * 8 + u) * (HD / 2) + lane];
+  ah8 qB[4];
+  const int hq = kvh * G + li;
+#pragma unroll
+  for (int cc = 0; cc < 4; ++cc) {
+    uint4 q = make_uint4(0, 0, 0, 0);
+    if (li < G) q = *(const uint4*)(a.q + ((size_t)j * a.nh + hq) * HD + 32 * cc + 8 * lg);
+    qB[cc] = *reinterpret_cast<ah8*>(&q);
+  }
+
+  // S^T: keys 16t + 4lg + v (rows), head li (column)
+  af4 sc[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    sc[t] = af4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int cc = 0; cc < 4; ++cc)
+      sc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(*reinterpret_cast<ah8*>(&kA[t][cc]), qB[cc], sc[t], 0, 0, 0);
+  }
+  const float scale = (float)a.scale, sl2 = scale * 1.4426950408889634f;
+  float bm = -INFINITY;
+#pragma unroll
+  for (int t = 0; t < 4; ++t)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      if (16 * t + 4 * lg + v >= nvalid) sc[t][v] = -INFINITY;
+      bm = fmaxf(bm, sc[t][v]);
+    }
+  bm = fmaxf(bm, __shfl_xor(bm, 16));
+  bm = fmaxf(bm, __shfl_xor(bm, 32));                  // key 0 of the page is always valid: finite
+  const float mnat = bm * scale, ml2 = bm * sl2;
+  float rs = 0.f;
+  ah8 pB[2];
+#pragma unroll
+  for (int t = 0; t < 4; ++t)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const float p = __builtin_amdgcn_exp2f(fmaf(sc[t][v], sl2, -ml2));
+      rs += p;
+      pB[t >> 1][4 * (t & 1) + v] = (_Float16)p;
+    }
+  rs += __shfl_xor(rs, 16);
+  rs += __shfl_xor(rs, 32);
+
+  // V -> Vt in this wave's LDS slice (keys past the context zeroed: p = 0 there, V may hold anything)
+#pragma unroll
+  for (int kg = 0; kg < 8; ++kg) {
+    u32x4 lo, hi;
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) {
+      const unsigned v0 = kg * 8 + 2 * jj < nvalid ? vr[kg][2 * jj] : 0u;
+      const unsigned v1 = kg * 8 + 2 * jj + 1 < nvalid ? vr[kg][2 * jj + 1] : 0u;
+      lo[jj] = __builtin_amdgcn_perm(v1, v0, 0x05040100u);
+      hi[jj] = __builtin_amdgcn_perm(v1, v0, 0x07060302u);
+    }
+    *(u32x4*)&vt[wv][2 * lane][kg * 8] = lo;
+    *(u32x4*)&vt[wv][2 * lane + 1][kg * 8] = hi;
+  }
+  __builtin_amdgcn_s_waitcnt(0xc07f);                   // lgkmcnt(0): this wave's LDS writes landed
+  __builtin_amdgcn_wave_barrier();
+
+  // O^T = Vt P^T; 32-key chunk cc2 in k-slot order 8g + i -> key 32 cc2 + 4g + i (i < 4), + 16 + 4g + i - 4
+  af4 acc[8];
+#pragma unroll
+  for (int dt = 0; dt < 8; ++dt) acc[dt] = af4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int cc2 = 0; cc2 < 2; ++cc2)
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) {
+      const _Float16* row = &vt[wv][16 * dt + li][0];
+      const uint2 lo = *(const uint2*)(row + 32 * cc2 + 4 * lg);
+      const uint2 hi = *(const uint2*)(row + 32 * cc2 + 16 + 4 * lg);
+      uint4 vv = make_uint4(lo.x, lo.y, hi.x, hi.y);
+      acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(*reinterpret_cast<ah8*>(&vv), pB[cc2], acc[dt], 0, 0, 0);
+    }
+  if (li < G) {
+    double* P = a.part + (((size_t)j * a.nh + hq) * a.max_chunks + c) * (HD + 2);
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) {
+      ((double2*)(P + 16 * dt + 4 * lg))[0] = make_double2((double)acc[dt][0], (double)acc[dt][1]);
+      ((double2*)(P + 16 * dt + 4 * lg))[1] = make_double2((double)acc[dt][2], (double)acc[dt][3]);
+    }
+    if (lg == 0) { P[HD] = (double)mnat; P[HD + 1] = (double)rs; }
+  }
 }
 
 // ---------------------------------------------------------------------------------------------

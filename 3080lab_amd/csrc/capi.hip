@@ -298,11 +298,7 @@ extern "C" int q355_attn_decode(const void* q, const void* kcache, const void* v
   hipStream_t s = (hipStream_t)stream;
   const dim3 grid(nkv * max_chunks, T);
   if (fp32) {
-    switch (nh / nkv) {
-      case 4: hipLaunchKernelGGL((k_attn_decode<4, float, 1>), grid, dim3(256), 0, s, a); break;
-      case 6: hipLaunchKernelGGL((k_attn_decode<6, float, 1>), grid, dim3(384), 0, s, a); break;
-      default: hipLaunchKernelGGL((k_attn_decode<8, float, 1>), grid, dim3(512), 0, s, a); break;
-    }
+    hipLaunchKernelGGL(k_attn_decode_mfma, dim3(nkv * ((max_chunks + 3) / 4), T), dim3(256), 0, s, a);
   } else {
     switch (nh / nkv) {
       case 4: hipLaunchKernelGGL((k_attn_decode<4, double, 2>), grid, dim3(512), 0, s, a); break;
