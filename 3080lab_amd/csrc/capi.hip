@@ -389,8 +389,27 @@ static int launch_mmq_big(GemvArgs a, hipStream_t s) {
   return launched("mmq");
 }
 
+// LOGITS over a large vocabulary (N % 128 == 0) for up to 64 tokens: the LDS-tiled kernel with all tokens
+// in one workgroup, so each weight is read once (128 rows x 16 / 32 / 64 tokens per workgroup).
+static int launch_mmq_logits_tile(const GemvArgs& a, hipStream_t s) {
+  const dim3 grid(a.N / 128, 1, 1);
+  if (a.T <= 16) {
+    constexpr size_t lds = 2 * LdsTile<2, 1, 1, TILE_CB>::BUF;
+    hipLaunchKernelGGL((k_mmq_tile<2, 1, 1, EPI_LOGITS>), grid, dim3(128), lds, s, a);
+  } else if (a.T <= 32) {
+    constexpr size_t lds = 2 * LdsTile<2, 2, 1, TILE_CB>::BUF;
+    hipLaunchKernelGGL((k_mmq_tile<2, 2, 1, EPI_LOGITS>), grid, dim3(256), lds, s, a);
+  } else {
+    constexpr size_t lds = 2 * LdsTile<2, 2, 2, TILE_CB>::BUF;
+    hipLaunchKernelGGL((k_mmq_tile<2, 2, 2, EPI_LOGITS>), grid, dim3(256), lds, s, a);
+  }
+  return launched("mmq");
+}
+
 template <int EPI>
 static int launch_mmq_tg(const GemvArgs& a, int KS, hipStream_t s) {
+  if constexpr (EPI == EPI_LOGITS)
+    if (a.N % 128 == 0 && a.N >= 128 * 256 && a.T <= 64) return launch_mmq_logits_tile(a, s);
   if constexpr (EPI == EPI_STORE || EPI == EPI_RESID_FIX || EPI == EPI_SWIGLU_Q8)
     if (a.N % 128 == 0 && (a.N / 128) * ((a.T + 63) / 64) >= 256) return launch_mmq_big<EPI>(a, s);
   // up to 64 tokens (decode batches): 16-token workgroups, several per CU, hide each other's latencies;

@@ -280,7 +280,8 @@ __global__ void __launch_bounds__(NW * 64) k_mmq_reg(const GemvArgs a) {
 //                                          halves, so the two half-wave reads of a B operand use all banks
 //   X  [CB][CW*16*TG]                      activation scale / 16 (fp32)
 // Epilogues from registers: STORE, RESID_FIX (plain read-add-write: each output has one writer),
-// SWIGLU_Q8 (rows interleaved g0, u0, ...: each 64-row tile group is one Q8_1 block per token).
+// SWIGLU_Q8 (rows interleaved g0, u0, ...: each 64-row tile group is one Q8_1 block per token), LOGITS
+// (fp32 logits + one (max, row) partial per 64 rows and token, the layout of the other LOGITS kernels).
 template <int RW, int CW, int TG, int CB>
 struct LdsTile {
   static constexpr int TW = CW * 16 * TG;            // tokens per workgroup
@@ -294,10 +295,11 @@ __global__ void __launch_bounds__(256) k_mmq_tile(const GemvArgs a) {
   constexpr int CB = TILE_CB;
   using L = LdsTile<RW, CW, TG, CB>;
   constexpr int TW = L::TW;
+  constexpr int NTH = RW * CW * 64;                  // threads
   constexpr int NA = RW * 4 * CB * 16;               // 16-byte pieces of A per chunk
   constexpr int NWp = RW * 4 * CB * 2;               // of W (fp16 in HBM)
   constexpr int NBp = TW * CB * 2;                   // of B (two per token and block)
-  static_assert(NA % 256 == 0 && NBp % 256 == 0 && NWp <= 256, "staging shape");
+  static_assert(NA % NTH == 0 && NBp % NTH == 0 && NWp <= NTH, "staging shape");
   extern __shared__ __align__(16) char lds[];
   const int K = a.K, nb = K / 32, N = a.N;
   const KSlice ks(nb);
@@ -309,24 +311,24 @@ __global__ void __launch_bounds__(256) k_mmq_tile(const GemvArgs a) {
   const int tid = threadIdx.x;
 
   // staging registers for one chunk
-  uint4 rA[NA / 256], rB[NBp / 256], rW;
-  half2 rX[NBp / 256];
+  uint4 rA[NA / NTH], rB[NBp / NTH], rW;
+  half2 rX[NBp / NTH];
   const uint4* __restrict__ gA = (const uint4*)a.qs;
   const uint4* __restrict__ gW = (const uint4*)a.d;
 
 #define Q355_TILE_LOAD(c0)                                                                        \
   {                                                                                               \
     const int cb_ = (c0);                                                                         \
-    _Pragma("unroll") for (int i = 0; i < NA / 256; ++i) {                                        \
-      const int p = tid + 256 * i, t = p / (CB * 16), r = p % (CB * 16), blk = r >> 4;            \
+    _Pragma("unroll") for (int i = 0; i < NA / NTH; ++i) {                                        \
+      const int p = tid + NTH * i, t = p / (CB * 16), r = p % (CB * 16), blk = r >> 4;            \
       rA[i] = cb_ + blk < ks.b1 ? gA[((size_t)(tile0 + t) * nb + cb_) * 16 + r] : make_uint4(0, 0, 0, 0); \
     }                                                                                             \
     if (tid < NWp) {                                                                              \
       const int t = tid / (CB * 2), r = tid % (CB * 2), blk = r >> 1;                             \
       rW = cb_ + blk < ks.b1 ? gW[((size_t)(tile0 + t) * nb + cb_) * 2 + r] : make_uint4(0, 0, 0, 0); \
     }                                                                                             \
-    _Pragma("unroll") for (int i = 0; i < NBp / 256; ++i) {                                       \
-      const int p = tid + 256 * i, h = p & 1, j = (p >> 1) % TW, blk = p / (2 * TW);              \
+    _Pragma("unroll") for (int i = 0; i < NBp / NTH; ++i) {                                       \
+      const int p = tid + NTH * i, h = p & 1, j = (p >> 1) % TW, blk = p / (2 * TW);              \
       const bool ok = tok0 + j < a.T && cb_ + blk < ks.b1;                                        \
       rB[i] = ok ? *(const uint4*)(a.xq + (size_t)(tok0 + j) * K + (size_t)(cb_ + blk) * 32 + 16 * h) \
                  : make_uint4(0, 0, 0, 0);                                                        \
@@ -337,16 +339,16 @@ __global__ void __launch_bounds__(256) k_mmq_tile(const GemvArgs a) {
 #define Q355_TILE_STORE(buf)                                                                      \
   {                                                                                               \
     char* base_ = lds + (buf) * L::BUF;                                                           \
-    _Pragma("unroll") for (int i = 0; i < NA / 256; ++i)                                          \
-      *(uint4*)(base_ + (size_t)(tid + 256 * i) * 16) = rA[i];                                    \
+    _Pragma("unroll") for (int i = 0; i < NA / NTH; ++i)                                          \
+      *(uint4*)(base_ + (size_t)(tid + NTH * i) * 16) = rA[i];                                    \
     if (tid < NWp) {                                                                              \
       const __half2* h_ = (const __half2*)&rW;                                                    \
       float4* dst_ = (float4*)(base_ + L::A + tid * 32);                                          \
       dst_[0] = make_float4(__low2float(h_[0]), __high2float(h_[0]), __low2float(h_[1]), __high2float(h_[1])); \
       dst_[1] = make_float4(__low2float(h_[2]), __high2float(h_[2]), __low2float(h_[3]), __high2float(h_[3])); \
     }                                                                                             \
-    _Pragma("unroll") for (int i = 0; i < NBp / 256; ++i) {                                       \
-      const int p = tid + 256 * i, h = p & 1, j = (p >> 1) % TW, blk = p / (2 * TW);              \
+    _Pragma("unroll") for (int i = 0; i < NBp / NTH; ++i) {                                       \
+      const int p = tid + NTH * i, h = p & 1, j = (p >> 1) % TW, blk = p / (2 * TW);              \
       *(uint4*)(base_ + L::A + L::W + (((j >> 4) * CB + blk) * 16 + (j & 15)) * 32 +              \
                 16 * (h ^ ((j >> 3) & 1))) = rB[i];                                               \
       if (!h) ((float*)(base_ + L::A + L::W + L::B))[blk * TW + j] = __low2float(rX[i]) * 0.0625f; \
@@ -439,6 +441,30 @@ __global__ void __launch_bounds__(256) k_mmq_tile(const GemvArgs a) {
               atomicAdd((unsigned long long*)(y + v), (unsigned long long)to_fix((double)acc[t][g][v]));
           }
         }
+      }
+    } else if (EPI == EPI_LOGITS) {
+      // fp32 logits, and this wave's (max, lowest row) over its 64 rows: partial rt0 / 4 of N / 64
+      float bv = -INFINITY;
+      int bi = 0x7fffffff;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        if (ok)
+          *(float4*)(a.y + (size_t)tok * N + (rt0 + t) * 16 + 4 * lg) =
+              make_float4(acc[t][g][0], acc[t][g][1], acc[t][g][2], acc[t][g][3]);
+#pragma unroll
+        for (int v = 0; v < 4; ++v)                      // rows increase with (t, v): strict '>' keeps the lowest
+          if (acc[t][g][v] > bv) { bv = acc[t][g][v]; bi = (rt0 + t) * 16 + 4 * lg + v; }
+      }
+#pragma unroll
+      for (int o = 16; o <= 32; o <<= 1) {
+        const float ov = __shfl_xor(bv, o);
+        const int oi = __shfl_xor(bi, o);
+        if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+      }
+      if (ok && lg == 0) {
+        const int np = N / 64;
+        a.pmax[(size_t)tok * np + rt0 / 4] = bv;
+        a.pidx[(size_t)tok * np + rt0 / 4] = bi;
       }
     } else if (EPI == EPI_SWIGLU_Q8) {
       // this lane holds outputs 8t + 2lg, 8t + 2lg + 1 of its wave's 32; the 4 lanes of token li hold all 32

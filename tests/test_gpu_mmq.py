@@ -45,6 +45,10 @@ def mat(N, K, seed):
     return QM.Q4Mat(b, N, K, "cuda"), b
 
 
+def rows_of(b, N, K, rows):
+    return b.reshape(N, K // 32, 18)[rows].reshape(-1, 18)
+
+
 def q8(x):
     q, d, s = OQ.quantize_q8_1(x)
     return dev(q), dev(np.stack([d, s], -1).view(np.int16)), q, d
@@ -100,9 +104,13 @@ def test_mmq_swiglu_q8(cuda):
     assert (np.abs(mq.cpu().numpy().astype(int) - qo.astype(int)) > 1).mean() < 1e-3
 
 
-def test_mmq_logits_argmax(cuda):
+@pytest.mark.parametrize("V,T", [(8192, 20), (32768, 10), (32768, 33)])
+def test_mmq_logits_argmax(cuda, V, T):
+    """The staged kernel (V = 8192) and the LDS-tiled large-vocabulary kernel (V >= 32768; 16-, 64-token
+    tiles): logits against the oracle (all rows, or 256 random rows for the large vocabulary) and the
+    argmax over the partials equal to the argmax of the logits."""
     import torch
-    V, K, T = 8192, 1536, 20
+    K = 1536
     W, b = mat(V, K, 99)
     x = np.random.default_rng(4).standard_normal((T, K), dtype=np.float32)
     xq, xds, q, d = q8(x)
@@ -117,7 +125,8 @@ def test_mmq_logits_argmax(cuda):
     call("q355_finish", ptr(pm), ptr(pi), n, ptr(tok), ptr(pos), T)
     sync()
     yy = y.cpu().numpy()
-    assert relerr(yy, OQ.gemv_q4_0_q8_1(b, V, K, q, d)) < REL
+    rows = np.arange(V) if V <= 8192 else np.sort(np.random.default_rng(V + T).choice(V, 256, replace=False))
+    assert relerr(yy[:, rows], OQ.gemv_q4_0_q8_1(rows_of(b, V, K, rows), len(rows), K, q, d)) < REL
     assert tok.cpu().numpy().tolist() == [int(np.argmax(r)) for r in yy]
     assert pos.cpu().numpy().tolist() == [1] * T
 
@@ -213,10 +222,6 @@ def test_batched_equals_single_sequence(small):
 
 # Prefill-size products (the LDS-tiled kernel: N % 128 == 0 and at least 256 tiles of 128 x 64): the full
 # product is too large for the oracle, so a random subset of rows is checked against it.
-def rows_of(b, N, K, rows):
-    return b.reshape(N, K // 32, 18)[rows].reshape(-1, 18)
-
-
 @pytest.mark.parametrize("N,K,T", [(17920, 1536, 300), (4096, 1536, 2100), (4096, 1568, 700)])
 def test_mmq_tile_store(cuda, N, K, T):
     import torch
