@@ -317,7 +317,7 @@ __device__ __forceinline__ void attn_merge_head(const double* __restrict__ P, in
 }
 
 // Standalone merge: one wave per (token, query head) -> fp32 o32 (optional) and Q8_1 oq/ods of the head's
-// 128 values (4 blocks).
+// 128 values (4 blocks), or fp16 oh.
 __global__ void __launch_bounds__(64) k_attn_merge(const AttnArgs a) {
   __shared__ double sm[HD];
   const int j = blockIdx.x, h = blockIdx.y;
@@ -325,6 +325,15 @@ __global__ void __launch_bounds__(64) k_attn_merge(const AttnArgs a) {
   attn_merge_head(a.part + ((size_t)j * a.nh + h) * a.max_chunks * (HD + 2), nch, sm);
   __syncthreads();
   const int n = a.nh * HD;
+  if (a.oh) {                                           // fp16 output (the fp16 batched path)
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int e = h * HD + 64 * u + threadIdx.x;
+      a.oh[(size_t)j * n + e] = half_rn(sm[64 * u + threadIdx.x]);
+      if (a.o32) a.o32[(size_t)j * n + e] = (float)sm[64 * u + threadIdx.x];
+    }
+    return;
+  }
 #pragma unroll
   for (int u = 0; u < 2; ++u) {                         // 64 lanes = two 32-value blocks per pass
     const int e = h * HD + 64 * u + threadIdx.x;

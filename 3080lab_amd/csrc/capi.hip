@@ -312,6 +312,25 @@ extern "C" int q355_attn_decode(const void* q, const void* kcache, const void* v
   return launched("attn_merge");
 }
 
+extern "C" int q355_attn_decode_f16(const void* q, const void* kcache, const void* vcache, const int32_t* pos,
+                                    const int32_t* block_table, int bt_stride, int nh, int nkv, int max_chunks,
+                                    double scale, double* part, void* oh, int T, void* stream) {
+  REQUIRE(q && kcache && vcache && pos && block_table && part && oh, "attn_decode_f16: null pointer");
+  REQUIRE(nh > 0 && nkv > 0 && nh % nkv == 0 && nh / nkv <= 16, "attn_decode_f16: nh=%d nkv=%d", nh, nkv);
+  REQUIRE(max_chunks > 0 && max_chunks <= bt_stride && max_chunks <= 64, "attn_decode_f16: max_chunks=%d bt_stride=%d",
+          max_chunks, bt_stride);
+  REQUIRE(T > 0 && T <= 65535, "attn_decode_f16: T=%d", T);
+  AttnArgs a = {};
+  a.q = (const __half*)q; a.kcache = (const __half*)kcache; a.vcache = (const __half*)vcache;
+  a.pos = pos; a.block_table = block_table; a.bt_stride = bt_stride; a.nh = nh; a.nkv = nkv;
+  a.max_chunks = max_chunks; a.scale = scale; a.part = part; a.oh = (__half*)oh;
+  hipStream_t s = (hipStream_t)stream;
+  hipLaunchKernelGGL(k_attn_decode_mfma, dim3(nkv * ((max_chunks + 3) / 4), T), dim3(256), 0, s, a);
+  if (int e = launched("attn_decode_f16")) return e;
+  hipLaunchKernelGGL(k_attn_merge, dim3(T, nh), dim3(64), 0, s, a);
+  return launched("attn_merge");
+}
+
 extern "C" int q355_attn_o_resid(const uint8_t* qs, const void* d, int N, const double* part, int max_chunks,
                                  const int32_t* pos, int nh, int64_t* h, int T, void* stream) {
   const int K = nh * HD;
@@ -456,6 +475,112 @@ extern "C" int q355_mmq_q4_0_q8_1(const uint8_t* qs, const void* d, int N, int K
 }
 
 extern "C" int q355_mmq_nparts(int N) { return N / 64; }
+
+// ------------------------------------------------------------------------------------------------
+// fp16-activation batched decode path.
+template <int TG, int EPI>
+static int launch_gemm_f16(GemvArgs a, int KS, hipStream_t s) {
+  constexpr int NT = 4, NW = 4, TT = 16 * TG;
+  constexpr size_t LDS_MAX = 65536;
+  const int nb = a.K / 32, per = (nb + KS - 1) / KS;
+  const size_t pb = (size_t)NW * NT * TT * 16 * 4;
+  const int ch_max = (int)(LDS_MAX / ((size_t)TT * 2) - 8) / 32;
+  const int nchunks = (per + ch_max - 1) / ch_max;
+  a.mmq_chunk = (per + nchunks - 1) / nchunks;
+  const size_t xb = (size_t)TT * (a.mmq_chunk * 32 + 8) * 2;
+  const size_t lds = xb > pb ? xb : pb;
+  const dim3 grid(a.N / (16 * NT), KS, (a.T + TT - 1) / TT);
+  hipLaunchKernelGGL((k_gemm_f16<TG, NT, NW, EPI>), grid, dim3(NW * 64), lds, s, a);
+  return launched("gemm_f16");
+}
+
+// Register-resident variant for T <= 32: one launch per shape class. SWIGLU_F16 and the other single-slice
+// epilogues: 80-row workgroups (N % 80 == 0; 224 for gate_up, one per CU) or 64-row ones, 8 waves x 6
+// blocks over K <= 1536. RESID_FIX: 64-row workgroups of 4 waves, K split until ~256 workgroups.
+// Returns -1 when the shape falls outside these classes.
+template <int TG, int EPI>
+static int launch_gemm_f16r_tg(const GemvArgs& a, hipStream_t s) {
+  const int nb = a.K / 32;
+  if (EPI == EPI_RESID_FIX) {
+    if (a.N % 64) return -1;
+    if (nb >= 64) {                                  // long K (down): 8 waves x 4 blocks per slice
+      const int KS = (nb + 31) / 32;
+      hipLaunchKernelGGL((k_gemm_f16r<TG, 4, 8, 4, EPI>), dim3(a.N / 64, KS), dim3(512), 0, s, a);
+      return launched("gemm_f16");
+    }
+    int KS = 1;
+    while ((a.N / 64) * KS < 256 && nb / (KS + 1) >= 4) ++KS;
+    while ((nb + KS - 1) / KS > 4 * 8) ++KS;
+    const int per = (nb + KS - 1) / KS;
+    const dim3 grid(a.N / 64, KS);
+    if (per <= 4 * 2) hipLaunchKernelGGL((k_gemm_f16r<TG, 4, 4, 2, EPI>), grid, dim3(256), 0, s, a);
+    else if (per <= 4 * 4) hipLaunchKernelGGL((k_gemm_f16r<TG, 4, 4, 4, EPI>), grid, dim3(256), 0, s, a);
+    else hipLaunchKernelGGL((k_gemm_f16r<TG, 4, 4, 8, EPI>), grid, dim3(256), 0, s, a);
+    return launched("gemm_f16");
+  }
+  if (nb > 8 * 6) return -1;
+  if (a.N % 80 == 0 && a.N / 80 <= 256) {
+    hipLaunchKernelGGL((k_gemm_f16r<TG, 5, 8, 6, EPI>), dim3(a.N / 80), dim3(512), 0, s, a);
+  } else {
+    if (a.N % 64) return -1;
+    hipLaunchKernelGGL((k_gemm_f16r<TG, 4, 8, 6, EPI>), dim3(a.N / 64), dim3(512), 0, s, a);
+  }
+  return launched("gemm_f16");
+}
+
+template <int EPI>
+static int launch_gemm_f16_tg(const GemvArgs& a, int KS, hipStream_t s) {
+  if (a.T <= 32) {
+    const int r = a.T <= 16 ? launch_gemm_f16r_tg<1, EPI>(a, s) : launch_gemm_f16r_tg<2, EPI>(a, s);
+    if (r >= 0) return r;
+  }
+  return a.T <= 16 ? launch_gemm_f16<1, EPI>(a, KS, s) : launch_gemm_f16<2, EPI>(a, KS, s);
+}
+
+extern "C" int q355_gemm_q4_0_f16(const uint8_t* qs, const void* d, int N, int K, const void* xh, int T, int epi,
+                                  float* y, int64_t* yfix, void* yh, float* pmax, int32_t* pidx, void* stream) {
+  if (int e = check_mat("gemm_q4_0_f16", qs, d, N, K)) return e;
+  REQUIRE(xh, "gemm_q4_0_f16: null activation pointer");
+  REQUIRE(T >= 1 && T <= 65535 * 32, "gemm_q4_0_f16: T=%d", T);
+  REQUIRE(N % 64 == 0, "gemm_q4_0_f16: N=%d must be a multiple of 64", N);
+  GemvArgs a = {};
+  a.qs = qs; a.d = (const __half*)d; a.N = N; a.K = K; a.T = T; a.xh = (const __half*)xh;
+  hipStream_t s = (hipStream_t)stream;
+  const int nb = K / 32, groups = N / 64;
+  switch (epi) {
+    case 0:
+      REQUIRE(y, "gemm_q4_0_f16: store needs y");
+      a.y = y;
+      return launch_gemm_f16_tg<EPI_STORE>(a, 1, s);
+    case 5:
+      REQUIRE(y && pmax && pidx, "gemm_q4_0_f16: logits needs y, pmax, pidx");
+      a.y = y; a.pmax = pmax; a.pidx = pidx;
+      return launch_gemm_f16_tg<EPI_LOGITS>(a, 1, s);
+    case 6: {
+      REQUIRE(yfix, "gemm_q4_0_f16: resid_fix needs yfix");
+      a.yfix = (long long*)yfix;
+      int KS = 384 / groups;
+      KS = KS < 1 ? 1 : (KS > nb / 4 ? nb / 4 : KS);
+      if (KS < 1) KS = 1;
+      return launch_gemm_f16_tg<EPI_RESID_FIX>(a, KS, s);
+    }
+    case 8:
+      REQUIRE(yh, "gemm_q4_0_f16: swiglu_f16 needs yh");
+      a.yh = (__half*)yh;
+      return launch_gemm_f16_tg<EPI_SWIGLU_F16>(a, 1, s);
+    default:
+      return fail(Q355_EINVAL, "gemm_q4_0_f16: epi=%d (0 store, 5 logits, 6 resid_fix, 8 swiglu_f16)", epi);
+  }
+}
+
+extern "C" int q355_rmsnorm_fix_f16(const int64_t* h, const float* w, void* xh, int T, int H, double eps,
+                                    void* stream) {
+  REQUIRE(h && w && xh, "rmsnorm_fix_f16: null pointer");
+  REQUIRE(T >= 1 && H % 8 == 0 && H / 8 <= 256, "rmsnorm_fix_f16: T=%d H=%d", T, H);
+  hipLaunchKernelGGL(k_rmsnorm_fix_f16, dim3(T), dim3(256), 0, (hipStream_t)stream, (const long long*)h, w,
+                     (__half*)xh, H, eps);
+  return launched("rmsnorm_fix_f16");
+}
 
 extern "C" int q355_qkv_finish(int64_t* acc, const float* bias, const float* rope_cos, const float* rope_sin,
                                const int32_t* pos, const int32_t* block_table, int bt_stride, int seq_stride,

@@ -340,6 +340,23 @@ __device__ __forceinline__ void epilogue(const GemvArgs& a, A (&part)[NW][NT][T]
     }
     return;
   }
+  if (EPI == EPI_SWIGLU_F16) {
+    // rows interleaved (g0, u0, g1, u1, ...): one thread per output pair, fp32 SiLU, fp16 out
+    for (int e = threadIdx.x; e < NT * T * 8; e += blockDim.x) {
+      const int t = e / (T * 8), j = (e >> 3) % T, k = e & 7;
+      if (j >= a.T) continue;
+      float g, u;
+      if constexpr (std::is_same<A, float>::value) {
+        g = row_value_f<NW, T, NT>(part, t, j, 2 * k);
+        u = row_value_f<NW, T, NT>(part, t, j, 2 * k + 1);
+      } else {
+        g = (float)row_value<NW, T, NT>(part, t, j, 2 * k);
+        u = (float)row_value<NW, T, NT>(part, t, j, 2 * k + 1);
+      }
+      a.yh[(size_t)j * (N / 2) + (tile0 + t) * 8 + k] = __float2half_rn(silu_mul_f(g, u));
+    }
+    return;
+  }
   if (EPI == EPI_SWIGLU) {
     // rows interleaved (g0, u0, g1, u1, ...): one thread per output pair
     for (int e = threadIdx.x; e < NT * T * 8; e += blockDim.x) {
@@ -594,6 +611,34 @@ __global__ void __launch_bounds__(256) k_rmsnorm_fix_q8_1(const long long* __res
   if (act) {
     *(uint2*)(xq + (size_t)tok * H + 8 * g) = pk;
     if ((g & 3) == 0) xds[(size_t)tok * (H / 32) + (g >> 2)] = __halves2half2(__float2half_rn(df), __float2half_rn(df * (float)sq));
+  }
+}
+
+// RMSNorm of the fixed-point residual stream -> fp16 (the fp16 batched path), one token per workgroup.
+__global__ void __launch_bounds__(256) k_rmsnorm_fix_f16(const long long* __restrict__ h, const float* __restrict__ w,
+                                                         __half* __restrict__ xh, int H, double eps) {
+  __shared__ double red[4];
+  const int tok = blockIdx.x;
+  const int g = threadIdx.x;                       // 8 consecutive values per thread, H / 8 <= 256
+  const bool act = g < H / 8;
+  double hv[8];
+  double ss = 0.0;
+#pragma unroll
+  for (int u = 0; u < 8; ++u) {
+    hv[u] = act ? from_fix(h[(size_t)tok * H + 8 * g + u]) : 0.0;
+    ss = fma(hv[u], hv[u], ss);
+  }
+  ss = wave_sum_d(ss);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+  __syncthreads();
+  const double r = 1.0 / sqrt((red[0] + red[1] + red[2] + red[3]) / (double)H + eps);
+  if (act) {
+    const float4 w0 = ((const float4*)w)[2 * g], w1 = ((const float4*)w)[2 * g + 1];
+    const float wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+    __half o[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) o[u] = half_rn(hv[u] * r * (double)wv[u]);
+    *(uint4*)(xh + (size_t)tok * H + 8 * g) = *(const uint4*)o;
   }
 }
 

@@ -16,6 +16,7 @@ enum Epilogue {
   EPI_LOGITS = 5,      // y = acc and per-workgroup (max, lowest index) partials
   EPI_RESID_FIX = 6,   // fixed-point residual: yfix += round(acc * 2^48) (int64 atomics; any K split)
   EPI_SWIGLU_Q8 = 7,   // as SWIGLU, quantized to Q8_1 (oq, ods): NT == 4 (64 rows -> one 32-output block)
+  EPI_SWIGLU_F16 = 8,  // as SWIGLU, rounded to fp16 (yh [T][N / 2])
 };
 
 constexpr int HD = 128;        // head dim (Qwen2.5-1.5B)
@@ -77,6 +78,9 @@ struct GemvArgs {
   // LOGITS: per-workgroup (max, index) partials [T][gridDim.x]
   float* pmax;
   int* pidx;
+  // fp16-activation products (batched decode): x fp16 [T][K], SWIGLU_F16 output
+  const __half* xh;
+  __half* yh;
 };
 
 // Causal prefill attention over one sequence's paged KV cache (keys 0 .. pos0 + P - 1 already written).
@@ -119,6 +123,7 @@ struct AttnArgs {
   int8_t* oq;                  // [T][nh*HD] Q8_1 output for the O projection (standalone merge)
   half2* ods;                  // [T][nh*HD/32]
   float* o32;                  // optional fp32 output [T][nh*HD] (tests), may be null
+  __half* oh;                  // fp16 merged output [T][nh*HD] (the fp16 batched path), instead of oq/ods
 };
 
 template <int T, int NT, int NW, int KPL, int PRO, int EPI, int WF>

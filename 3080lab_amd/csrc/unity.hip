@@ -4,4 +4,5 @@
 #include "flash.hip"
 #include "mega.hip"
 #include "gemv_bf16.hip"
+#include "gemm_f16.hip"
 #include "capi.hip"

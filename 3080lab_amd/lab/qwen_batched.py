@@ -1,16 +1,17 @@
-"""Batched decode on int8 MFMA and the reference's lab/qwen_batched.py names.
+"""Batched decode and prefill, with the reference's lab/qwen_batched.py names.
 
 The reference's batched step (scripts/qwen_batched_decode.py:156-187) runs B sequences per step with
 tensor-core GEMVs over bf16 activations (gemv_v2_source) and per-sequence contiguous bf16 KV caches.
-Here B sequences share one step with:
-  rmsnorm_fix_q8_1       RMSNorm of the fixed-point residual stream -> Q8_1 (per token)
-  mmq (resid_fix)        QKV on v_mfma_i32_16x16x32_i8, K-sliced into an int64 accumulator
+Here B sequences share one step (BatchedDecoder, act "f16", the default) with:
+  rmsnorm_fix_f16        RMSNorm of the fixed-point residual stream -> fp16 activations (per token)
+  gemm_f16 (resid_fix)   QKV: fp16-dequantized Q4_0 x fp16 on v_mfma_f32_16x16x32_f16, K-sliced into int64
   qkv_finish             bias + RoPE + fp16 q + paged fp16 K/V write (clears the accumulator)
-  attn_decode + merge    split-K GQA attention (fp32) over 64-position pages of every sequence -> Q8_1
-  mmq (resid_fix)        O projection into the residual stream
-  rmsnorm_fix_q8_1, mmq (swiglu_q8)   gate_up + SwiGLU, output already Q8_1
-  mmq (resid_fix)        down projection into the residual stream
-then rmsnorm + mmq (logits) over the tied Q4_0 head + finish (argmax per sequence, pos += 1).
+  attn_decode_f16        GQA attention on the matrix cores over 64-position pages + merge -> fp16
+  gemm_f16 (resid_fix)   O projection into the residual stream
+  rmsnorm_fix_f16, gemm_f16 (swiglu_f16)   gate_up + SwiGLU -> fp16
+  gemm_f16 (resid_fix)   down projection into the residual stream
+then rmsnorm_fix_q8_1 + mmq (logits) over the tied Q4_0 head + finish (argmax per sequence, pos += 1).
+act "q8" runs the same step on Q8_1 activations and the int8 MMQ kernels (the prefill arithmetic).
 The KV cache is paged: a shared pool of 64-position pages, one block-table row per sequence.
 """
 from __future__ import annotations
@@ -32,10 +33,11 @@ class KernelSpec:
 
 # reference generator names (lab/qwen_batched.py) -> the C-ABI entry points that replace them
 def gemv_v2_source(WM=1, WK=1, MT=1, B=8, epi="store", PF=1, KS=1, ACC16=False) -> KernelSpec:
-    """Batched decode GEMV (lab/qwen_batched.py:467-641) -> q355_mmq_q4_0_q8_1 (int8 MFMA); epi store /
-    resid (fixed-point residual) / swiglu (-> swiglu_q8) / biasf (-> resid_fix + q355_qkv_finish)."""
-    code = {"store": 0, "logits": 5, "resid": 6, "biasf": 6, "swiglu": 7, "swiglu_q8": 7}[epi]
-    return KernelSpec("q355_mmq_q4_0_q8_1", {"epi": code})
+    """Batched decode GEMV (lab/qwen_batched.py:467-641) -> q355_gemm_q4_0_f16 (the same fp16 weight
+    dequantization, fp16 MFMA); epi store / logits / resid (fixed-point residual) / swiglu (fp16 out) /
+    biasf (-> resid_fix + q355_qkv_finish)."""
+    code = {"store": 0, "logits": 5, "resid": 6, "biasf": 6, "swiglu": 8}[epi]
+    return KernelSpec("q355_gemm_q4_0_f16", {"epi": code})
 
 
 def gemm_q4i8_ms_source(WM=4, WN=2, MT=2, NT=4, epi="store", KB=4, NSTG=2, MINB=1, ABL=None) -> KernelSpec:
@@ -71,12 +73,17 @@ class BatchedDecoder:
     sequences in a seeded random order (the block table is a permutation), so the kernels are exercised
     on non-contiguous pages."""
 
-    def __init__(self, m: DeviceModel, B: int, max_ctx: int, page_seed: int = 0):
+    def __init__(self, m: DeviceModel, B: int, max_ctx: int, page_seed: int = 0, act: str = "f16"):
+        """act "f16": fp16 activations and fp16-dequantized weights on the fp16 matrix cores, the reference's
+        batched decode arithmetic (gemv_v2_source, lab/qwen_batched.py:467-680); "q8": Q8_1 activations on
+        the int8 MMQ kernels (the prefill arithmetic)."""
         import torch
         c = m.cfg
         if m.head_q6k is not None:
-            raise ValueError("the batched (MMQ) step implements the tied Q4_0 head only")
-        self.m, self.cfg, self.B = m, c, B
+            raise ValueError("the batched step implements the tied Q4_0 head only")
+        if act not in ("f16", "q8"):
+            raise ValueError(f"act={act!r}: 'f16' or 'q8'")
+        self.m, self.cfg, self.B, self.act = m, c, B, act
         dev = m.device
         self.max_chunks = -(-max_ctx // PAGE)
         n_pages = B * self.max_chunks
@@ -94,6 +101,9 @@ class BatchedDecoder:
         self.q = torch.zeros(B, c.NH * c.HD, dtype=torch.float16, device=dev)
         self.part = torch.zeros(B, c.NH, self.max_chunks, c.HD + 2, dtype=torch.float64, device=dev)
         self.aq = torch.zeros(B, c.NH * c.HD, dtype=torch.int8, device=dev)
+        self.xh = torch.zeros(B, max(H, c.NH * c.HD), dtype=torch.float16, device=dev)
+        self.ah = torch.zeros(B, c.NH * c.HD, dtype=torch.float16, device=dev)
+        self.mh = torch.zeros(B, c.FFN, dtype=torch.float16, device=dev)
         self.ads = torch.zeros(B, c.NH * c.HD // 32, 2, dtype=torch.float16, device=dev)
         self.logits = torch.zeros(B, c.V, dtype=torch.float32, device=dev)
         self.nparts = call("q355_mmq_nparts", c.V)
@@ -115,7 +125,33 @@ class BatchedDecoder:
         call("q355_mmq_q4_0_q8_1", ptr(W.qs), ptr(W.d), W.N, W.K, ptr(xq), ptr(xds), self.B, epi,
              ptr(y), ptr(yfix), ptr(oq), ptr(ods), ptr(pmax), ptr(pidx))
 
+    def _normh(self, w):
+        c = self.cfg
+        call("q355_rmsnorm_fix_f16", ptr(self.h), ptr(w), ptr(self.xh), self.B, c.H, c.eps)
+
+    def _gemm(self, W, xh, epi, y=None, yfix=None, yh=None, pmax=None, pidx=None):
+        call("q355_gemm_q4_0_f16", ptr(W.qs), ptr(W.d), W.N, W.K, ptr(xh), self.B, epi, ptr(y), ptr(yfix), ptr(yh),
+             ptr(pmax), ptr(pidx))
+
+    def layer_f16(self, i: int):
+        m, c, B = self.m, self.cfg, self.B
+        L = m.layers[i]
+        self._normh(L["ln1"])
+        self._gemm(L["qkv"], self.xh, 6, yfix=self.qkv_acc)
+        call("q355_qkv_finish", ptr(self.qkv_acc), ptr(L["qkv_b"]), ptr(m.cos), ptr(m.sin), ptr(self.pos),
+             ptr(self.block_table), self.max_chunks, 1, ptr(self.kc[i]), ptr(self.vc[i]), ptr(self.q),
+             c.NH, c.NKV, B)
+        call("q355_attn_decode_f16", ptr(self.q), ptr(self.kc[i]), ptr(self.vc[i]), ptr(self.pos),
+             ptr(self.block_table), self.max_chunks, c.NH, c.NKV, self.max_chunks, self.scale, ptr(self.part),
+             ptr(self.ah), B)
+        self._gemm(L["o"], self.ah, 6, yfix=self.h)
+        self._normh(L["ln2"])
+        self._gemm(L["gu"], self.xh, 8, yh=self.mh)
+        self._gemm(L["down"], self.mh, 6, yfix=self.h)
+
     def layer(self, i: int):
+        if self.act == "f16":
+            return self.layer_f16(i)
         m, c, B = self.m, self.cfg, self.B
         L = m.layers[i]
         self._norm(L["ln1"])
@@ -137,6 +173,7 @@ class BatchedDecoder:
         call("q355_embed_q4_0", ptr(e.qs), ptr(e.d), e.N, e.K, ptr(self.tok), ptr(self.h), self.B)
         for i in range(c.L):
             self.layer(i)
+        # the LM head runs on Q8_1 activations in both modes (the int8 LDS-tiled kernel reads its 131 MB once)
         self._norm(m.norm)
         self._mmq(e, self.xq, self.xds, 5, y=self.logits, pmax=self.pmax, pidx=self.pidx)
         call("q355_finish", ptr(self.pmax), ptr(self.pidx), self.nparts, ptr(self.tok), ptr(self.pos), self.B)

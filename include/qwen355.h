@@ -144,12 +144,35 @@ int q355_rmsnorm_fix_q8_1(const int64_t* h, const float* w, int8_t* xq, void* xd
  * epi 0: y fp32 [T][N] = W x;  5: logits y [T][N] + argmax partials pmax/pidx [T][q355_mmq_nparts(N)];
  * 6: yfix [T][N] += W x (int64 fixed point, K-sliced, integer atomics);
  * 7: rows interleaved (gate, up): Q8_1 of silu(g) * u into oq [T][N/2], ods [T][N/64].
- * Replaces gemv_v2_source (lab/qwen_batched.py:467-641; batched decode, fp16 tensor cores there) and
- * gemm_q4i8_source / gemm_q4i8_ms_source with epilogues resid / swiglu_q8 (lab/qwen_batched.py:1093-1561). */
+ * Replaces gemm_q4i8_source / gemm_q4i8_ms_source with epilogues resid / swiglu_q8
+ * (lab/qwen_batched.py:1093-1561; prefill), and serves batched decode in its Q8_1 mode. */
 int q355_mmq_q4_0_q8_1(const uint8_t* qs, const void* d, int N, int K, const int8_t* xq, const void* xds, int T,
                        int epi, float* y, int64_t* yfix, int8_t* oq, void* ods, float* pmax, int32_t* pidx,
                        void* stream);
 int q355_mmq_nparts(int N);
+
+/* ---- fp16-activation path: batched decode (config 3) ---- */
+
+/* RMSNorm of the fixed-point residual stream -> fp16 xh [T][H] (one rounding of the f64 value).
+ * Replaces the bf16 RMSNorm of the batched decode (scripts/qwen_batched_decode.py:156-187). */
+int q355_rmsnorm_fix_f16(const int64_t* h, const float* w, void* xh, int T, int H, double eps, void* stream);
+
+/* Q4_0 weights dequantized to fp16 (d (q - 8), one rounding) times fp16 activations xh [T][K] on
+ * v_mfma_f32_16x16x32_f16 with fp32 accumulation, N % 64 == 0.
+ * epi 0: y fp32 [T][N];  5: logits y [T][N] + argmax partials pmax/pidx [T][q355_mmq_nparts(N)];
+ * 6: yfix [T][N] += W x (int64 fixed point, K-sliced, integer atomics);
+ * 8: rows interleaved (gate, up): yh fp16 [T][N/2] = silu(g) * u.
+ * Replaces gemv_v2_source (lab/qwen_batched.py:467-680: the same fp16 dequantization, fp16 tensor cores)
+ * and head_v2_source (:681-833) for the tied Q4_0 head. */
+int q355_gemm_q4_0_f16(const uint8_t* qs, const void* d, int N, int K, const void* xh, int T, int epi, float* y,
+                       int64_t* yfix, void* yh, float* pmax, int32_t* pidx, void* stream);
+
+/* Batched decode attention (fp16 MFMA, fp32 softmax; the GQA group's heads as MFMA columns) + f64 merge of
+ * the page partials -> fp16 oh [T][nh*128]. Arguments as q355_attn_decode; part is its scratch.
+ * Replaces the batched ATTN4 + combine of scripts/qwen_batched_decode.py:156-187. */
+int q355_attn_decode_f16(const void* q, const void* kcache, const void* vcache, const int32_t* pos,
+                         const int32_t* block_table, int bt_stride, int nh, int nkv, int max_chunks, double scale,
+                         double* part, void* oh, int T, void* stream);
 
 /* QKV epilogue of the MFMA path: acc int64 fixed point [T][nqkv] (device row order) -> + bias, RoPE, fp16
  * q out [T][nh*128], fp16 K/V cache rows at pos[j] of sequence j * seq_stride; acc is zeroed.

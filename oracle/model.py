@@ -19,7 +19,9 @@ with this build's operand formats (Q8_1 activations, fp16 KV cache, tied Q4_0 em
   logits = E Q8_1(rmsnorm(h) * norm); tok = argmax (lowest index wins ties); pos += 1
                                                FINISH / FINISH_MB (lab/qwen_kernels.py:222-282)
 
-Rounding points follow the product: every GEMV input is Q8_1 of an fp32 value (x, att, m), q/K/V are
+Rounding points follow the product: every GEMV input is Q8_1 of an fp32 value (x, att, m) -- with
+act "f16" (the batched decode path) the layer GEMV inputs are instead rounded to fp16 and the weights are
+the fp16 values d (q - 8) (gemv_v2_source, lab/qwen_batched.py:467-680); the LM head keeps Q8_1 -- q/K/V are
 rounded f64 -> fp16 once (round to nearest even), logits are fp32; everything else (GEMV outputs, the residual stream h,
 RMSNorm, RoPE, attention, SwiGLU) is float64.
 GEMVs use gemv_q4_0_q8_1 semantics; mode "f64" computes them as a float64 BLAS product of the
@@ -142,19 +144,26 @@ class LinearQ6K:
 
 
 class Linear:
-    """One Q4_0 matrix W [N, K] from GGUF bytes, applied to Q8_1 activations."""
+    """One Q4_0 matrix W [N, K] from GGUF bytes, applied to Q8_1 activations (act "q8"), or, as the batched
+    decode does (gemv_v2_source, lab/qwen_batched.py:467-680), as fp16-dequantized weights to fp16
+    activations (act "f16")."""
 
-    def __init__(self, wbytes: np.ndarray, N: int, K: int, mode: str = "f64"):
-        self.b, self.N, self.K, self.mode = wbytes, N, K, mode
+    def __init__(self, wbytes: np.ndarray, N: int, K: int, mode: str = "f64", act: str = "q8"):
+        self.b, self.N, self.K, self.mode, self.act = wbytes, N, K, mode, act
         self._w = None
 
     def dense(self):
         if self._w is None:
-            self._w = Q.dequant_q4_0(self.b, (self.N, self.K)).astype(np.float64)
+            if self.act == "f16":
+                self._w = Q.dequant_q4_0_f16(self.b, (self.N, self.K)).astype(np.float64)
+            else:
+                self._w = Q.dequant_q4_0(self.b, (self.N, self.K)).astype(np.float64)
         return self._w
 
     def __call__(self, x: np.ndarray) -> np.ndarray:
-        """x fp32 [T, K] -> quantize Q8_1 -> y float64 [T, N]."""
+        """x [T, K] -> Q8_1 (or fp16) activations -> y float64 [T, N]."""
+        if self.act == "f16":
+            return np.asarray(x).astype(np.float16).astype(np.float64) @ self.dense().T
         qx, dx, _ = Q.quantize_q8_1(np.asarray(x, np.float32))
         if self.mode == "int":
             return Q.gemv_q4_0_q8_1(self.b, self.N, self.K, qx, dx, out_dtype=np.float64)
@@ -170,19 +179,22 @@ class Model:
     w: dict
     maxlen: int = 2048
     mode: str = "f64"
+    act: str = "q8"              # "q8": Q8_1 activations (batch 1, prefill); "f16": the batched decode path
     lin: list = field(default_factory=list)
 
     def __post_init__(self):
         c = self.cfg
         self.cos, self.sin = rope_tables(self.maxlen, c.HD, c.theta)
+        md, ac = self.mode, self.act
         for L in self.w["layers"]:
             self.lin.append({
-                "q": Linear(L["wq"], c.NH * c.HD, c.H, self.mode), "k": Linear(L["wk"], c.NKV * c.HD, c.H, self.mode),
-                "v": Linear(L["wv"], c.NKV * c.HD, c.H, self.mode), "o": Linear(L["wo"], c.H, c.NH * c.HD, self.mode),
-                "g": Linear(L["wg"], c.FFN, c.H, self.mode), "u": Linear(L["wu"], c.FFN, c.H, self.mode),
-                "d": Linear(L["wd"], c.H, c.FFN, self.mode)})
+                "q": Linear(L["wq"], c.NH * c.HD, c.H, md, ac), "k": Linear(L["wk"], c.NKV * c.HD, c.H, md, ac),
+                "v": Linear(L["wv"], c.NKV * c.HD, c.H, md, ac), "o": Linear(L["wo"], c.H, c.NH * c.HD, md, ac),
+                "g": Linear(L["wg"], c.FFN, c.H, md, ac), "u": Linear(L["wu"], c.FFN, c.H, md, ac),
+                "d": Linear(L["wd"], c.H, c.FFN, md, ac)})
+        # the LM head takes Q8_1 activations in both modes (the batched decode's head is the int8 kernel)
         self.head = (LinearQ6K(self.w["head_q6k"], c.V, c.H) if "head_q6k" in self.w
-                     else Linear(self.w["embed"], c.V, c.H, self.mode))
+                     else Linear(self.w["embed"], c.V, c.H, md))
 
     def new_cache(self):
         c = self.cfg

@@ -171,6 +171,24 @@ def gemv_q4_0_bf16(wbytes: np.ndarray, N: int, K: int, xbits: np.ndarray) -> np.
     return bf16_to_f32(xbits).astype(np.float64) @ w.T
 
 
+def dequant_q4_0_f16(b: np.ndarray, shape) -> np.ndarray:
+    """GGUF Q4_0 bytes -> fp16 values d (q - 8), rounded once (the batched-decode weight dequantization of
+    gemv_v2_source, lab/qwen_batched.py:486-491: (q | 0x6400) as fp16 = 1024 + q, minus 1032, times d).
+    The float32 product d (q - 8) is exact (11 x 4 significant bits), so one float32 -> float16 rounding
+    gives the single rounding of the fp16 multiply.
+    pinned by: the same value computed in numpy float16 arithmetic step by step (tests/test_oracle.py)."""
+    d, q = q4_0_blocks(b)
+    return (d.astype(np.float32)[:, None] * (q.astype(np.float32) - 8)).astype(np.float16).reshape(shape)
+
+
+def gemv_q4_0_f16(wbytes: np.ndarray, N: int, K: int, x: np.ndarray) -> np.ndarray:
+    """Batched-decode product (gemv_v2_source semantics): fp16-dequantized W [N, K] times fp16 activations
+    x [T, K] (rounded to fp16 here if given wider), evaluated in float64 (the GPU's fp32 MFMA accumulation
+    agrees to ~1e-6 relative)."""
+    w = dequant_q4_0_f16(wbytes, (N, K)).astype(np.float64)
+    return np.asarray(x).astype(np.float16).astype(np.float64) @ w.T
+
+
 def gemv_dequant_f64(wbytes: np.ndarray, N: int, K: int, qx: np.ndarray, dx: np.ndarray) -> np.ndarray:
     """Independent form of gemv_q4_0_q8_1 (dequantize both operands, float64 matmul); pins it."""
     w = dequant_q4_0(wbytes, (N, K)).astype(np.float64)

@@ -176,6 +176,13 @@ def small(cuda):
     return w, QM.DeviceModel(w, CFG_S, maxlen=512), OM.Model(OM.Config(L=2, V=4096), w, maxlen=512)
 
 
+@pytest.fixture(scope="module")
+def small_f16(small):
+    """The oracle with the batched decode's fp16 activation / fp16-dequantized weight arithmetic."""
+    w, dm, _ = small
+    return OM.Model(OM.Config(L=2, V=4096), w, maxlen=512, act="f16")
+
+
 def check_greedy(got, ref, margins, what):
     """Greedy parity rule: tokens equal up to the first step whose oracle top-2 logit margin is a near-tie
     (< NEAR_TIE); there, ulp-level differences of fp32 accumulation order and of Q8_1 re-quantization may
@@ -190,13 +197,17 @@ def check_greedy(got, ref, margins, what):
 NEAR_TIE = 1e-2
 
 
+@pytest.mark.parametrize("act", ["f16", "q8"])
 @pytest.mark.parametrize("B", [8, 32])
-def test_batched_greedy_matches_oracle(small, B):
-    """B independent prompts decoded together (paged KV, scattered pages) match the oracle per sequence."""
+def test_batched_greedy_matches_oracle(small, small_f16, B, act):
+    """B independent prompts decoded together (paged KV, scattered pages) match the oracle per sequence, in
+    both arithmetic modes (the oracle in the matching mode)."""
     w, dm, om = small
+    if act == "f16":
+        om = small_f16
     rng = np.random.default_rng(B)
     prompts = rng.integers(0, CFG_S.V, (B, 6))
-    bd = QB.BatchedDecoder(dm, B=B, max_ctx=256, page_seed=B)
+    bd = QB.BatchedDecoder(dm, B=B, max_ctx=256, page_seed=B, act=act)
     bd.prefill_tokens(prompts)
     got = bd.generate(10)
     for b in ([0, 3, B - 1] if B > 8 else range(B)):
@@ -209,7 +220,11 @@ def test_batched_equals_single_sequence(small):
     (scripts/qwen_batched_decode.py:258-261), up to a near-tie of the two paths' fp32 sums."""
     w, dm, om = small
     prompt = [7, 300, 12, 4000, 5]
-    bd = QB.BatchedDecoder(dm, B=8, max_ctx=256, page_seed=3)
+    fb = QB.BatchedDecoder(dm, B=8, max_ctx=256, page_seed=3)            # fp16 mode: rows identical
+    fb.prefill_tokens(np.array([prompt] * 8))
+    f16rows = fb.generate(16)
+    assert (f16rows == f16rows[0:1]).all()
+    bd = QB.BatchedDecoder(dm, B=8, max_ctx=256, page_seed=3, act="q8")  # Q8_1 mode: also = batch 1
     bd.prefill_tokens(np.array([prompt] * 8))
     got = bd.generate(16)
     assert (got == got[0:1]).all()

@@ -266,3 +266,18 @@ def test_bf16_decode_and_rounding():
     # 1 + 2^-8 is a bf16 midpoint between 1 and 1 + 2^-7: ties to even (1.0); 1 + 3 * 2^-8 rounds up
     x = np.array([1.0, 1 + 2 ** -8, 1 + 3 * 2 ** -8, -2.5], np.float32)
     assert OQ.bf16_to_f32(OQ.f32_to_bf16(x)).tolist() == [1.0, 1.0, 1 + 2 ** -6, -2.5]
+
+
+def test_q4_0_f16_dequant_matches_fp16_arithmetic():
+    """d (q - 8) rounded once to fp16 equals the reference's fp16 steps: (1024 + q) - 1032, times d, each
+    step in float16 arithmetic (lab/qwen_batched.py:486-491)."""
+    rng = np.random.default_rng(5)
+    w = (rng.standard_normal((64, 256)) * rng.choice([1e-3, 0.02, 3.0], (64, 1))).astype(np.float32)
+    b = OQ.quantize_q4_0(w)
+    d, q = OQ.q4_0_blocks(b)
+    step = ((np.float16(1024) + q.astype(np.float16)) - np.float16(1032)) * d.astype(np.float16)[:, None]
+    assert step.dtype == np.float16
+    got = OQ.dequant_q4_0_f16(b, (64, 256))
+    assert np.array_equal(got.reshape(-1, 32).view(np.uint16), step.view(np.uint16))
+    # and it is the fp32 dequantization rounded to fp16
+    assert np.array_equal(got, OQ.dequant_q4_0(b, (64, 256)).astype(np.float16))
