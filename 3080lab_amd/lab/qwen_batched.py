@@ -2,7 +2,7 @@
 
 The reference's batched step (scripts/qwen_batched_decode.py:156-187) runs B sequences per step with
 tensor-core GEMVs over bf16 activations (gemv_v2_source) and per-sequence contiguous bf16 KV caches.
-Here B sequences share one step (BatchedDecoder, act "f16", the default) with:
+Here B sequences share one step (BatchedDecoder). With act "f16" (the reference's gemv_v2 arithmetic):
   rmsnorm_fix_f16        RMSNorm of the fixed-point residual stream -> fp16 activations (per token)
   gemm_f16 (resid_fix)   QKV: fp16-dequantized Q4_0 x fp16 on v_mfma_f32_16x16x32_f16, K-sliced into int64
   qkv_finish             bias + RoPE + fp16 q + paged fp16 K/V write (clears the accumulator)
@@ -11,7 +11,8 @@ Here B sequences share one step (BatchedDecoder, act "f16", the default) with:
   rmsnorm_fix_f16, gemm_f16 (swiglu_f16)   gate_up + SwiGLU -> fp16
   gemm_f16 (resid_fix)   down projection into the residual stream
 then rmsnorm_fix_q8_1 + mmq (logits) over the tied Q4_0 head + finish (argmax per sequence, pos += 1).
-act "q8" runs the same step on Q8_1 activations and the int8 MMQ kernels (the prefill arithmetic).
+act "q8" (the default; BASELINE config 3 specifies int8 MMQ) runs the same step on Q8_1 activations and the
+int8 MMQ kernels, with the matrix-core attention merged to Q8_1.
 The KV cache is paged: a shared pool of 64-position pages, one block-table row per sequence.
 """
 from __future__ import annotations
@@ -73,10 +74,10 @@ class BatchedDecoder:
     sequences in a seeded random order (the block table is a permutation), so the kernels are exercised
     on non-contiguous pages."""
 
-    def __init__(self, m: DeviceModel, B: int, max_ctx: int, page_seed: int = 0, act: str = "f16"):
-        """act "f16": fp16 activations and fp16-dequantized weights on the fp16 matrix cores, the reference's
-        batched decode arithmetic (gemv_v2_source, lab/qwen_batched.py:467-680); "q8": Q8_1 activations on
-        the int8 MMQ kernels (the prefill arithmetic)."""
+    def __init__(self, m: DeviceModel, B: int, max_ctx: int, page_seed: int = 0, act: str = "q8"):
+        """act "q8" (default: Q4_0 x Q8_1 int8 MMQ on MFMA): Q8_1 activations on the int8
+        MMQ kernels; "f16": fp16 activations and fp16-dequantized weights on the fp16 matrix cores, the
+        reference's own batched decode arithmetic (gemv_v2_source, lab/qwen_batched.py:467-680)."""
         import torch
         c = m.cfg
         if m.head_q6k is not None:

@@ -15,6 +15,9 @@ Printed on one JSON line, besides the contract fields:
                 HIP events on the launch stream, cycling the 28 layers' distinct weights (434 MB > MALL)
   gemv          BASELINE config 0: the 8960 x 1536 Q4_0 x Q8_1 GEMV, cold (64 distinct weight copies,
                 495 MB) and hot-MALL, GB/s of algorithmic bytes (7,779,008 B per call)
+  batched       BASELINE config 3 at B = 8 and 32 on the config's int8 MMQ (Q4_0 x Q8_1), tok/s
+  batched_f16   the same batches in the reference's own batched arithmetic (fp16-dequantized Q4_0 x fp16)
+  prefill       BASELINE config 4: one 2048-token prompt, tok/s
   cpu_baseline  the numpy oracle (exact int32 block-dot form, one core) timed on this host for a few
                 decode steps of the same model, tok/s
 """
@@ -118,15 +121,16 @@ def gemv_config0(copies: int = 64) -> dict:
             "weight_copies": copies}
 
 
-def batched_decode(dm, B: int, steps: int = 32, warmup: int = 2) -> dict:
+def batched_decode(dm, B: int, steps: int = 32, warmup: int = 2, act: str = "q8") -> dict:
     """B sequences with contexts uniform in [256, 2048] (seed 3), paged fp16 KV filled
-    with N(0, 1), one hipGraph per step on the fp16-activation MFMA path (fp16-dequantized Q4_0, the
-    reference's batched arithmetic; the LM head on the int8 tiled kernel); tok/s = B * steps / time."""
+    with N(0, 1), one hipGraph per step. act "q8": the config's Q4_0 x Q8_1 int8 MMQ on MFMA; act "f16":
+    the reference's own batched arithmetic (fp16-dequantized Q4_0 x fp16 activations on the fp16 matrix
+    cores, gemv_v2_source). tok/s = B * steps / time."""
     import torch
     from lab import qwen_batched as QB
     rng = np.random.default_rng(3)
     ctx = rng.integers(256, 2049, B)
-    bd = QB.BatchedDecoder(dm, B=B, max_ctx=2048 + warmup + steps + 1, page_seed=B)
+    bd = QB.BatchedDecoder(dm, B=B, max_ctx=2048 + warmup + steps + 1, page_seed=B, act=act)
     bd.fill_random_context(ctx, seed=B)
     bd.tok.copy_(torch.from_numpy(rng.integers(0, dm.cfg.V, B).astype(np.int32)))
     pos0, tok0 = bd.pos.clone(), bd.tok.clone()
@@ -145,7 +149,7 @@ def batched_decode(dm, B: int, steps: int = 32, warmup: int = 2) -> dict:
     ms = s.elapsed_time(e) / steps
     kv = int(28_672 * (ctx.sum() + B * steps / 2))          # mean K+V bytes read per step
     wbytes = dm.weight_bytes_per_token()
-    out = {"B": B, "tok_per_s": round(B * 1e3 / ms, 1), "ms_per_step": round(ms, 4),
+    out = {"B": B, "act": act, "tok_per_s": round(B * 1e3 / ms, 1), "ms_per_step": round(ms, 4),
            "ctx_mean": float(ctx.mean()), "bytes_per_step": wbytes + kv,
            "hbm_GBps": round((wbytes + kv) / (ms * 1e-3) / 1e9, 1)}
     del bd
@@ -302,6 +306,8 @@ def main():
     if not args.quick:
         out["batched"] = [batched_decode(dm, B) for B in (8, 32)]
         log("batched:", out["batched"])
+        out["batched_f16"] = [batched_decode(dm, B, act="f16") for B in (8, 32)]
+        log("batched_f16:", out["batched_f16"])
         out["prefill"] = prefill(dm)
         log("prefill:", out["prefill"])
         out["roofline"] = gate_up_roofline(dm, dec)

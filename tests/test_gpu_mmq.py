@@ -220,7 +220,7 @@ def test_batched_equals_single_sequence(small):
     (scripts/qwen_batched_decode.py:258-261), up to a near-tie of the two paths' fp32 sums."""
     w, dm, om = small
     prompt = [7, 300, 12, 4000, 5]
-    fb = QB.BatchedDecoder(dm, B=8, max_ctx=256, page_seed=3)            # fp16 mode: rows identical
+    fb = QB.BatchedDecoder(dm, B=8, max_ctx=256, page_seed=3, act="f16")  # fp16 mode: rows identical
     fb.prefill_tokens(np.array([prompt] * 8))
     f16rows = fb.generate(16)
     assert (f16rows == f16rows[0:1]).all()
