@@ -425,8 +425,42 @@ static int launch_mmq_logits_tile(const GemvArgs& a, hipStream_t s) {
   return launched("mmq");
 }
 
+// Register-resident decode-batch kernel (T <= 32). SWIGLU (fp32 out) with N % 80 == 0 and K <= 1536:
+// 80-row workgroups of 8 waves x 6 blocks (224 for gate_up, one per CU). RESID_FIX from fp32 activations
+// (XF32): 64-row workgroups, K split 32 blocks per slice (8 waves x 4) or <= 16 (4 waves x 4).
+// Returns -1 outside these classes.
+template <int TG, int EPI, bool XF32>
+static int launch_mmq_r_tg(const GemvArgs& a, hipStream_t s) {
+  const int nb = a.K / 32;
+  if constexpr (EPI == EPI_SWIGLU && !XF32) {
+    if (a.N % 80 || a.N / 80 > 256 || nb > 8 * 6) return -1;
+    hipLaunchKernelGGL((k_mmq_r<TG, 5, 8, 6, EPI, XF32>), dim3(a.N / 80), dim3(512), 0, s, a);
+    return launched("mmq");
+  }
+  if constexpr (EPI == EPI_RESID_FIX && XF32) {
+    if (a.N % 64) return -1;
+    if (nb >= 64) {
+      const int KS = (nb + 31) / 32;
+      hipLaunchKernelGGL((k_mmq_r<TG, 4, 8, 4, EPI, XF32>), dim3(a.N / 64, KS), dim3(512), 0, s, a);
+      return launched("mmq");
+    }
+    int KS = 1;
+    while ((a.N / 64) * KS < 256 && nb / (KS + 1) >= 4) ++KS;
+    if ((nb + KS - 1) / KS > 16) return -1;
+    hipLaunchKernelGGL((k_mmq_r<TG, 4, 4, 4, EPI, XF32>), dim3(a.N / 64, KS), dim3(256), 0, s, a);
+    return launched("mmq");
+  }
+  return -1;
+}
+
 template <int EPI>
 static int launch_mmq_tg(const GemvArgs& a, int KS, hipStream_t s) {
+  if constexpr (EPI == EPI_SWIGLU) {
+    if (a.T <= 32) {
+      const int r = a.T <= 16 ? launch_mmq_r_tg<1, EPI, false>(a, s) : launch_mmq_r_tg<2, EPI, false>(a, s);
+      if (r >= 0) return r;
+    }
+  }
   if constexpr (EPI == EPI_LOGITS)
     if (a.N % 128 == 0 && a.N >= 128 * 256 && a.T <= 64) return launch_mmq_logits_tile(a, s);
   if constexpr (EPI == EPI_STORE || EPI == EPI_RESID_FIX || EPI == EPI_SWIGLU_Q8)
@@ -461,6 +495,10 @@ extern "C" int q355_mmq_q4_0_q8_1(const uint8_t* qs, const void* d, int N, int K
       if (KS < 1) KS = 1;
       return launch_mmq_tg<EPI_RESID_FIX>(a, KS, s);
     }
+    case 4:
+      REQUIRE(y, "mmq_q4_0_q8_1: swiglu needs y");
+      a.y = y;
+      return launch_mmq_tg<EPI_SWIGLU>(a, 1, s);
     case 7:
       REQUIRE(oq && ods, "mmq_q4_0_q8_1: swiglu_q8 needs oq/ods");
       a.oq = oq; a.ods = (half2*)ods;
@@ -470,11 +508,25 @@ extern "C" int q355_mmq_q4_0_q8_1(const uint8_t* qs, const void* d, int N, int K
       a.y = y; a.pmax = pmax; a.pidx = pidx;
       return launch_mmq_tg<EPI_LOGITS>(a, 1, s);
     default:
-      return fail(Q355_EINVAL, "mmq_q4_0_q8_1: epi=%d (0 store, 5 logits, 6 resid_fix, 7 swiglu_q8)", epi);
+      return fail(Q355_EINVAL, "mmq_q4_0_q8_1: epi=%d (0 store, 4 swiglu, 5 logits, 6 resid_fix, 7 swiglu_q8)", epi);
   }
 }
 
 extern "C" int q355_mmq_nparts(int N) { return N / 64; }
+
+extern "C" int q355_mmq_q4_0_f32(const uint8_t* qs, const void* d, int N, int K, const float* xf, int T,
+                                 int64_t* yfix, void* stream) {
+  if (int e = check_mat("mmq_q4_0_f32", qs, d, N, K)) return e;
+  REQUIRE(xf && yfix, "mmq_q4_0_f32: null pointer");
+  REQUIRE(T >= 1 && T <= 32, "mmq_q4_0_f32: T=%d (decode batches, <= 32)", T);
+  REQUIRE(N % 64 == 0, "mmq_q4_0_f32: N=%d must be a multiple of 64", N);
+  GemvArgs a = {};
+  a.qs = qs; a.d = (const __half*)d; a.N = N; a.K = K; a.T = T; a.xf = xf; a.yfix = (long long*)yfix;
+  hipStream_t s = (hipStream_t)stream;
+  const int r = T <= 16 ? launch_mmq_r_tg<1, EPI_RESID_FIX, true>(a, s) : launch_mmq_r_tg<2, EPI_RESID_FIX, true>(a, s);
+  if (r < 0) return fail(Q355_EINVAL, "mmq_q4_0_f32: K=%d outside the supported slices", K);
+  return r;
+}
 
 // ------------------------------------------------------------------------------------------------
 // fp16-activation batched decode path.

@@ -362,8 +362,13 @@ __device__ __forceinline__ void epilogue(const GemvArgs& a, A (&part)[NW][NT][T]
     for (int e = threadIdx.x; e < NT * T * 8; e += blockDim.x) {
       const int t = e / (T * 8), j = (e >> 3) % T, k = e & 7;
       if (j >= a.T) continue;
-      const double g = row_value<NW, T, NT>(part, t, j, 2 * k), u = row_value<NW, T, NT>(part, t, j, 2 * k + 1);
-      a.y[(size_t)j * (N / 2) + (tile0 + t) * 8 + k] = (float)silu_mul(g, u);
+      if constexpr (std::is_same<A, float>::value) {
+        a.y[(size_t)j * (N / 2) + (tile0 + t) * 8 + k] =
+            silu_mul_f(row_value_f<NW, T, NT>(part, t, j, 2 * k), row_value_f<NW, T, NT>(part, t, j, 2 * k + 1));
+      } else {
+        const double g = row_value<NW, T, NT>(part, t, j, 2 * k), u = row_value<NW, T, NT>(part, t, j, 2 * k + 1);
+        a.y[(size_t)j * (N / 2) + (tile0 + t) * 8 + k] = (float)silu_mul(g, u);
+      }
     }
     return;
   }

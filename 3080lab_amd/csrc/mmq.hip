@@ -86,6 +86,118 @@ __device__ __forceinline__ void stage_x(const GemvArgs& a, int8_t* xq, float* xd
   }
 }
 
+// Q8_1 of the 8 fp32 values this lane holds of one 32-block whose 4 quarters sit in lanes l, l ^ 16, l ^ 32,
+// l ^ 48 (the MFMA B-operand layout): d = fp16(amax / 127), q = round(x / d) (as a product with 1 / d).
+__device__ __forceinline__ long q8_1_mfma8(const float (&x)[8], float& df) {
+  float amax = 0.f;
+#pragma unroll
+  for (int u = 0; u < 8; ++u) amax = fmaxf(amax, fabsf(x[u]));
+  amax = fmaxf(amax, __shfl_xor(amax, 16));
+  amax = fmaxf(amax, __shfl_xor(amax, 32));
+  df = __half2float(__float2half_rn(amax / 127.0f));
+  const float inv = df != 0.0f ? 1.0f / df : 0.0f;
+  unsigned lo = 0, hi = 0;
+#pragma unroll
+  for (int u = 0; u < 8; ++u) {
+    int v = (int)roundf(x[u] * inv);
+    v = v > 127 ? 127 : (v < -127 ? -127 : v);
+    if (u < 4) lo |= (unsigned)(v & 255) << (8 * u);
+    else hi |= (unsigned)(v & 255) << (8 * (u - 4));
+  }
+  return (long)(((unsigned long)hi << 32) | lo);
+}
+
+// Decode-batch variant (T <= 16 TG tokens, all in one workgroup): every operand of the workgroup -- weights,
+// row scales, activations and their scales -- is loaded before the first product, so a workgroup pays one
+// memory latency. Wave wv takes blocks b0 + wv + NW i of the K slice (i < KPW); activations come straight
+// from global memory (each element is used by one wave only): Q8_1 (xq / xds), or with XF32 fp32 values
+// (xf, the SwiGLU output) quantized to Q8_1 in registers. Partials reduce over waves through LDS.
+template <int TG, int NT, int NW, int KPW, int EPI, bool XF32>
+__global__ void __launch_bounds__(NW * 64) k_mmq_r(const GemvArgs a) {
+  __shared__ float part[NW][NT][16 * TG][16];
+  constexpr int TT = 16 * TG;
+  const int K = a.K, nb = K / 32;
+  const KSlice ks(nb);
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int li = lane & 15, lg = lane >> 4;
+  const int tile0 = blockIdx.x * NT;
+  uint2 w[KPW][NT], dv[KPW][NT];
+  long xb[KPW][TG];
+  float dx[KPW][TG];
+  float4 xr[XF32 ? KPW : 1][XF32 ? TG : 1][2];
+#pragma unroll
+  for (int i = 0; i < KPW; ++i) {
+    const int b = min(ks.b0 + wv + NW * i, ks.b1 - 1);   // clamped: blocks past the slice are skipped below
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      const size_t base = ((size_t)(tile0 + t) * nb + b) * 16;
+      w[i][t] = ((const uint2*)a.qs)[(base + li) * 2 + (lg & 1)];
+      dv[i][t] = ((const uint2*)a.d)[(base >> 2) + lg];
+    }
+#pragma unroll
+    for (int g = 0; g < TG; ++g) {
+      const int tok = min(16 * g + li, a.T - 1);          // rows past T re-read the last token, never stored
+      if constexpr (XF32) {
+        const float4* src = (const float4*)(a.xf + (size_t)tok * K + (size_t)b * 32 + 8 * lg);
+        xr[i][g][0] = src[0];
+        xr[i][g][1] = src[1];
+      } else {
+        xb[i][g] = *(const long*)(a.xq + (size_t)tok * K + (size_t)b * 32 + 8 * lg);
+        dx[i][g] = __low2float(a.xds[(size_t)tok * nb + b]) * 0.0625f;
+      }
+    }
+  }
+  if constexpr (XF32) {
+#pragma unroll
+    for (int i = 0; i < KPW; ++i)
+#pragma unroll
+      for (int g = 0; g < TG; ++g) {
+        const float x8[8] = {xr[i][g][0].x, xr[i][g][0].y, xr[i][g][0].z, xr[i][g][0].w,
+                             xr[i][g][1].x, xr[i][g][1].y, xr[i][g][1].z, xr[i][g][1].w};
+        float df;
+        xb[i][g] = q8_1_mfma8(x8, df);
+        dx[i][g] = df * 0.0625f;
+      }
+  }
+  float acc[NT][TG][4];
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int g = 0; g < TG; ++g)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) acc[t][g][v] = 0.f;
+#pragma unroll
+  for (int i = 0; i < KPW; ++i) {
+    if (ks.b0 + wv + NW * i < ks.b1) {                    // uniform per wave
+      v4i c[NT][TG];
+      const v4i zero = {0, 0, 0, 0};
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        const long wa = snib8(w[i][t], lg);
+#pragma unroll
+        for (int g = 0; g < TG; ++g) c[t][g] = __builtin_amdgcn_mfma_i32_16x16x32_i8(wa, xb[i][g], zero, 0, 0, 0);
+      }
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        const __half2 d01 = *(const __half2*)&dv[i][t].x, d23 = *(const __half2*)&dv[i][t].y;
+        const float dw[4] = {__low2float(d01), __high2float(d01), __low2float(d23), __high2float(d23)};
+#pragma unroll
+        for (int g = 0; g < TG; ++g)
+#pragma unroll
+          for (int v = 0; v < 4; ++v) acc[t][g][v] = fmaf(dw[v] * dx[i][g], (float)c[t][g][v], acc[t][g][v]);
+      }
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int g = 0; g < TG; ++g)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) part[wv][t][16 * g + li][4 * lg + v] = acc[t][g][v];
+  __syncthreads();
+  epilogue<NW, TT, NT, EPI>(a, part, tile0);
+}
+
 template <int TG, int NT, int NW, int EPI>
 __global__ void __launch_bounds__(NW * 64) k_mmq(const GemvArgs a) {
   extern __shared__ __align__(16) char lds[];

@@ -37,6 +37,7 @@ _SIGS = {
     "q355_attn_o_resid": [_P, _P, c_int, _P, c_int, _P, c_int, _P, c_int, _P],
     "q355_rmsnorm_fix_q8_1": [_P, _P, _P, _P, c_int, c_int, c_double, _P],
     "q355_mmq_q4_0_q8_1": [_P, _P, c_int, c_int, _P, _P, c_int, c_int, _P, _P, _P, _P, _P, _P, _P],
+    "q355_mmq_q4_0_f32": [_P, _P, c_int, c_int, _P, c_int, _P, _P],
     "q355_rmsnorm_fix_f16": [_P, _P, _P, c_int, c_int, c_double, _P],
     "q355_gemm_q4_0_f16": [_P, _P, c_int, c_int, _P, c_int, c_int, _P, _P, _P, _P, _P, _P],
     "q355_attn_decode_f16": [_P, _P, _P, _P, _P, c_int, c_int, c_int, c_int, c_double, _P, _P, c_int, _P],

@@ -143,6 +143,7 @@ int q355_rmsnorm_fix_q8_1(const int64_t* h, const float* w, int8_t* xq, void* xd
 /* Q4_0 x Q8_1 product of T tokens on v_mfma_i32_16x16x32_i8 (exact int32 block dots), N % 64 == 0.
  * epi 0: y fp32 [T][N] = W x;  5: logits y [T][N] + argmax partials pmax/pidx [T][q355_mmq_nparts(N)];
  * 6: yfix [T][N] += W x (int64 fixed point, K-sliced, integer atomics);
+ * 4: rows interleaved (gate, up): y fp32 [T][N/2] = silu(g) * u;
  * 7: rows interleaved (gate, up): Q8_1 of silu(g) * u into oq [T][N/2], ods [T][N/64].
  * Replaces gemm_q4i8_source / gemm_q4i8_ms_source with epilogues resid / swiglu_q8
  * (lab/qwen_batched.py:1093-1561; prefill), and serves batched decode in its Q8_1 mode. */
@@ -150,6 +151,13 @@ int q355_mmq_q4_0_q8_1(const uint8_t* qs, const void* d, int N, int K, const int
                        int epi, float* y, int64_t* yfix, int8_t* oq, void* ods, float* pmax, int32_t* pidx,
                        void* stream);
 int q355_mmq_nparts(int N);
+
+/* Decode batches (T <= 32): yfix [T][N] += W Q8_1(xf), the fp32 activations xf [T][K] (e.g. the SwiGLU output
+ * of epi 4) quantized to Q8_1 inside the kernel (d = fp16(amax / 127) per 32-block, q = round(x / d)), then
+ * the int8 MFMA product of q355_mmq_q4_0_q8_1 epi 6. N % 64 == 0.
+ * Replaces the quantize + MMQ down pair of the batched step (swiglu_q8 -> gemv, lab/qwen_batched.py). */
+int q355_mmq_q4_0_f32(const uint8_t* qs, const void* d, int N, int K, const float* xf, int T, int64_t* yfix,
+                      void* stream);
 
 /* ---- fp16-activation path: batched decode (config 3) ---- */
 

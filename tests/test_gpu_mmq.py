@@ -291,3 +291,32 @@ def test_mmq_tile_swiglu_q8(cuda):
         assert relerr(got, OQ.dequant_q8_1(qo, do)) < 2e-2
         assert relerr(mds.cpu().numpy()[:, blk, 0], do[:, 0]) < 5e-3
         assert (np.abs(mq.cpu().numpy()[:, cols].astype(int) - qo.astype(int)) > 1).mean() < 1e-3
+
+
+@pytest.mark.parametrize("T", [8, 32])
+def test_mmq_swiglu_f32_then_down_f32(cuda, T):
+    """The decode-batch FFN pair: gate_up with the fp32 SwiGLU epilogue (epi 4), then down from those fp32
+    values quantized to Q8_1 inside q355_mmq_q4_0_f32 -- against the oracle's SwiGLU and Q8_1 down product."""
+    import torch
+    F, K = 8960, 1536
+    g = np.random.default_rng(21).standard_normal((F, K), dtype=np.float32) * np.float32(0.02)
+    u = np.random.default_rng(22).standard_normal((F, K), dtype=np.float32) * np.float32(0.02)
+    gb, ub = gguf.quantize_q4_0(g), gguf.quantize_q4_0(u)
+    gu = gguf.take_rows_q4_0(np.concatenate([gb, ub]), K, gguf.gate_up_row_order(F))
+    W = QM.Q4Mat(gu, 2 * F, K, "cuda")
+    x = np.random.default_rng(23).standard_normal((T, K), dtype=np.float32)
+    xq, xds, q, d = q8(x)
+    m = torch.zeros(T, F, device=cuda)
+    call("q355_mmq_q4_0_q8_1", ptr(W.qs), ptr(W.d), 2 * F, K, ptr(xq), ptr(xds), T, 4, ptr(m), None, None, None,
+         None, None)
+    sync()
+    mref = OM.silu_mul(OQ.gemv_q4_0_q8_1(gb, F, K, q, d), OQ.gemv_q4_0_q8_1(ub, F, K, q, d))
+    assert relerr(m.cpu().numpy(), mref) < REL
+    Wd, bd = mat(K, F, 24)
+    h0 = np.random.default_rng(25).standard_normal((T, K), dtype=np.float32)
+    h = dev(np.round(h0.astype(np.float64) * QM.FIX_SCALE).astype(np.int64))
+    call("q355_mmq_q4_0_f32", ptr(Wd.qs), ptr(Wd.d), K, F, ptr(m), T, ptr(h))
+    sync()
+    qm, dm_, _ = OQ.quantize_q8_1(m.cpu().numpy())
+    ref = OQ.gemv_q4_0_q8_1(bd, K, F, qm, dm_)
+    assert relerr(h.cpu().numpy() / QM.FIX_SCALE - h0, ref) < REL
