@@ -159,125 +159,245 @@ __global__ void __launch_bounds__(G * W * 64) k_attn_decode(const AttnArgs a) {
 }
 
 // ---------------------------------------------------------------------------------------------
-// fp32 path on the matrix cores (the batched decode): one wave per (token j, KV head, page c), the G query
-// heads of the group are the MFMA columns (16 columns, G used). S^T = K Q^T takes K rows straight from
-// global memory as A operands; V is transposed into the wave's own LDS slice through dword gathers
-// (lane l: dims 2l, 2l + 1 of 8 keys, packed in pairs), so O^T = Vt P^T reads 8-key runs. P is rounded to
-// fp16 for the MFMA (fp32 accumulation). Output: the same partial (o, m, l) as k_attn_decode, m in
-// natural-log units. No barriers: each wave only touches its own LDS slice.
+// fp32 path on the matrix cores (the batched decode), merge included. Workgroup (token j, KV head, split
+// sp) = 4 waves, wave wv takes page c = 4 sp + wv; the G query heads of the group are the MFMA columns (16
+// columns, G used). S^T = K Q^T takes K rows straight from global memory as A operands; V is transposed
+// into the wave's own LDS slice through dword gathers (lane l: dims 2l, 2l + 1 of 8 keys, packed in pairs),
+// so O^T = Vt P^T reads 8-key runs. P is rounded to fp16 for the MFMA (fp32 accumulation), max and
+// exponent in log2 units.
+// The 4 page partials merge through LDS (o = sum_w 2^(m_w - M) o_w, L likewise). A token whose context
+// fits one split (<= 4 pages) is finished there: Q8_1 (oq/ods) or fp16 (oh), and fp32 o32 if asked.
+// Otherwise every split writes its unnormalised (o, M, L) to the workspace (the `part` buffer: per (token,
+// KV head) o [nsp][G][HD] then (M, L) [nsp][G], nsp = ceil(max_chunks / 4)) and k_attn_merge_split
+// finishes the token. A cross-workgroup last-arrival merge inside this kernel was measured slower than the
+// second launch (its coherent stores, counter round trip and coherent reloads cost more than a launch).
 typedef _Float16 ah8 __attribute__((ext_vector_type(8)));
 typedef float af4 __attribute__((ext_vector_type(4)));
 constexpr int AV_ROW = PAGE + 4;   // Vt row (one dim, 64 keys) in halves: 136 B, so the dim 2l / 2l + 1
                                    // 16 B writes spread over all banks
 
+// the finished head values of one thread (head h, dims 8 dg .. 8 dg + 7) -> the outputs
+__device__ __forceinline__ void attn_out8(const AttnArgs& a, int j, int h, int dg, const float (&o)[8], bool live) {
+  const int n = a.nh * HD;
+  const size_t e = (size_t)j * n + h * HD + 8 * dg;
+  if (live && a.o32) {
+    *(float4*)(a.o32 + e) = make_float4(o[0], o[1], o[2], o[3]);
+    *(float4*)(a.o32 + e + 4) = make_float4(o[4], o[5], o[6], o[7]);
+  }
+  if (a.oh) {
+    if (live) {
+      unsigned pk[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const __half2 v = __floats2half2_rn(o[2 * i], o[2 * i + 1]);
+        pk[i] = *reinterpret_cast<const unsigned*>(&v);
+      }
+      *(uint4*)(a.oh + e) = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+    }
+    return;
+  }
+  float df;
+  int sq;
+  const uint2 q = q8_1_x8(o, df, sq);                  // the 4 threads of a quad hold one 32-value block
+  if (live) {
+    *(uint2*)(a.oq + e) = q;
+    if ((dg & 3) == 0) a.ods[e / 32] = __halves2half2(__float2half_rn(df), __float2half_rn(df * (float)sq));
+  }
+}
+
 __global__ void __launch_bounds__(256) k_attn_decode_mfma(const AttnArgs a) {
   __shared__ __align__(16) _Float16 vt[4][HD][AV_ROW];
+  __shared__ float wml[4][16][2];
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int li = lane & 15, lg = lane >> 4;
   const int G = a.nh / a.nkv;
-  const int nc4 = (a.max_chunks + 3) / 4;
-  const int j = blockIdx.y, kvh = blockIdx.x / nc4, c = (blockIdx.x % nc4) * 4 + wv;
+  const int nsp = (a.max_chunks + 3) / 4;
+  const int j = blockIdx.y, kvh = blockIdx.x / nsp, sp = blockIdx.x % nsp, c = sp * 4 + wv;
+  // the page index does not depend on the position: both loads are in flight together
+  const int pg = a.block_table[(size_t)j * a.bt_stride + min(c, a.max_chunks - 1)];
   const int pos = a.pos[j];
-  if (c >= a.max_chunks || c * PAGE > pos) return;   // uniform per wave
+  const int nch = pos / PAGE + 1, nsplit = (nch + 3) / 4;
+  if (sp >= nsplit) return;                             // uniform per workgroup
+  const bool live = c < nch;                            // uniform per wave; page 4 sp is always live
   const int nvalid = min(PAGE, pos + 1 - c * PAGE);
-  const int pg = a.block_table[(size_t)j * a.bt_stride + c];
   const _Float16* kp = (const _Float16*)a.kcache + ((size_t)pg * a.nkv + kvh) * PAGE * HD;
   const unsigned* vp = (const unsigned*)(a.vcache + ((size_t)pg * a.nkv + kvh) * PAGE * HD);
-
-  // every load of the page first: K operands (16 B per lane per tile), V dwords, q
-  uint4 kA[4][4];
-#pragma unroll
-  for (int t = 0; t < 4; ++t)
-#pragma unroll
-    for (int cc = 0; cc < 4; ++cc) kA[t][cc] = *(const uint4*)(kp + (16 * t + li) * HD + 32 * cc + 8 * lg);
-  unsigned vr[8][8];
-#pragma unroll
-  for (int kg = 0; kg < 8; ++kg)
-#pragma unroll
-    for (int u = 0; u < 8; ++u) vr[kg][u] = vp[(kg * 8 + u) * (HD / 2) + lane];
-  ah8 qB[4];
   const int hq = kvh * G + li;
-#pragma unroll
-  for (int cc = 0; cc < 4; ++cc) {
-    uint4 q = make_uint4(0, 0, 0, 0);
-    if (li < G) q = *(const uint4*)(a.q + ((size_t)j * a.nh + hq) * HD + 32 * cc + 8 * lg);
-    qB[cc] = *reinterpret_cast<ah8*>(&q);
-  }
 
-  // S^T: keys 16t + 4lg + v (rows), head li (column)
-  af4 sc[4];
-#pragma unroll
-  for (int t = 0; t < 4; ++t) {
-    sc[t] = af4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int cc = 0; cc < 4; ++cc)
-      sc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(*reinterpret_cast<ah8*>(&kA[t][cc]), qB[cc], sc[t], 0, 0, 0);
-  }
-  const float scale = (float)a.scale, sl2 = scale * 1.4426950408889634f;
-  float bm = -INFINITY;
-#pragma unroll
-  for (int t = 0; t < 4; ++t)
-#pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      if (16 * t + 4 * lg + v >= nvalid) sc[t][v] = -INFINITY;
-      bm = fmaxf(bm, sc[t][v]);
-    }
-  bm = fmaxf(bm, __shfl_xor(bm, 16));
-  bm = fmaxf(bm, __shfl_xor(bm, 32));                  // key 0 of the page is always valid: finite
-  const float mnat = bm * scale, ml2 = bm * sl2;
-  float rs = 0.f;
-  ah8 pB[2];
-#pragma unroll
-  for (int t = 0; t < 4; ++t)
-#pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      const float p = __builtin_amdgcn_exp2f(fmaf(sc[t][v], sl2, -ml2));
-      rs += p;
-      pB[t >> 1][4 * (t & 1) + v] = (_Float16)p;
-    }
-  rs += __shfl_xor(rs, 16);
-  rs += __shfl_xor(rs, 32);
-
-  // V -> Vt in this wave's LDS slice (keys past the context zeroed: p = 0 there, V may hold anything)
-#pragma unroll
-  for (int kg = 0; kg < 8; ++kg) {
-    u32x4 lo, hi;
-#pragma unroll
-    for (int jj = 0; jj < 4; ++jj) {
-      const unsigned v0 = kg * 8 + 2 * jj < nvalid ? vr[kg][2 * jj] : 0u;
-      const unsigned v1 = kg * 8 + 2 * jj + 1 < nvalid ? vr[kg][2 * jj + 1] : 0u;
-      lo[jj] = __builtin_amdgcn_perm(v1, v0, 0x05040100u);
-      hi[jj] = __builtin_amdgcn_perm(v1, v0, 0x07060302u);
-    }
-    *(u32x4*)&vt[wv][2 * lane][kg * 8] = lo;
-    *(u32x4*)&vt[wv][2 * lane + 1][kg * 8] = hi;
-  }
-  __builtin_amdgcn_s_waitcnt(0xc07f);                   // lgkmcnt(0): this wave's LDS writes landed
-  __builtin_amdgcn_wave_barrier();
-
-  // O^T = Vt P^T; 32-key chunk cc2 in k-slot order 8g + i -> key 32 cc2 + 4g + i (i < 4), + 16 + 4g + i - 4
   af4 acc[8];
 #pragma unroll
   for (int dt = 0; dt < 8; ++dt) acc[dt] = af4{0.f, 0.f, 0.f, 0.f};
+  float ml2 = -INFINITY, rs = 0.f;
+  if (live) {
+    // every load of the page first: K operands (16 B per lane per tile), V dwords, q
+    uint4 kA[4][4];
 #pragma unroll
-  for (int cc2 = 0; cc2 < 2; ++cc2)
+    for (int t = 0; t < 4; ++t)
 #pragma unroll
-    for (int dt = 0; dt < 8; ++dt) {
-      const _Float16* row = &vt[wv][16 * dt + li][0];
-      const uint2 lo = *(const uint2*)(row + 32 * cc2 + 4 * lg);
-      const uint2 hi = *(const uint2*)(row + 32 * cc2 + 16 + 4 * lg);
-      uint4 vv = make_uint4(lo.x, lo.y, hi.x, hi.y);
-      acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(*reinterpret_cast<ah8*>(&vv), pB[cc2], acc[dt], 0, 0, 0);
+      for (int cc = 0; cc < 4; ++cc) kA[t][cc] = *(const uint4*)(kp + (16 * t + li) * HD + 32 * cc + 8 * lg);
+    unsigned vr[8][8];
+#pragma unroll
+    for (int kg = 0; kg < 8; ++kg)
+#pragma unroll
+      for (int u = 0; u < 8; ++u) vr[kg][u] = vp[(kg * 8 + u) * (HD / 2) + lane];
+    ah8 qB[4];
+#pragma unroll
+    for (int cc = 0; cc < 4; ++cc) {
+      uint4 q = make_uint4(0, 0, 0, 0);
+      if (li < G) q = *(const uint4*)(a.q + ((size_t)j * a.nh + hq) * HD + 32 * cc + 8 * lg);
+      qB[cc] = *reinterpret_cast<ah8*>(&q);
     }
-  if (li < G) {
-    double* P = a.part + (((size_t)j * a.nh + hq) * a.max_chunks + c) * (HD + 2);
+
+    // S^T: keys 16t + 4lg + v (rows), head li (column)
+    af4 sc[4];
 #pragma unroll
-    for (int dt = 0; dt < 8; ++dt) {
-      ((double2*)(P + 16 * dt + 4 * lg))[0] = make_double2((double)acc[dt][0], (double)acc[dt][1]);
-      ((double2*)(P + 16 * dt + 4 * lg))[1] = make_double2((double)acc[dt][2], (double)acc[dt][3]);
+    for (int t = 0; t < 4; ++t) {
+      sc[t] = af4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int cc = 0; cc < 4; ++cc)
+        sc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(*reinterpret_cast<ah8*>(&kA[t][cc]), qB[cc], sc[t], 0, 0, 0);
     }
-    if (lg == 0) { P[HD] = (double)mnat; P[HD + 1] = (double)rs; }
+    const float sl2 = (float)a.scale * 1.4426950408889634f;
+    float bm = -INFINITY;
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        if (16 * t + 4 * lg + v >= nvalid) sc[t][v] = -INFINITY;
+        bm = fmaxf(bm, sc[t][v]);
+      }
+    bm = fmaxf(bm, __shfl_xor(bm, 16));
+    bm = fmaxf(bm, __shfl_xor(bm, 32));                 // key 0 of the page is always valid: finite
+    ml2 = bm * sl2;
+    ah8 pB[2];
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const float p = __builtin_amdgcn_exp2f(fmaf(sc[t][v], sl2, -ml2));
+        rs += p;
+        pB[t >> 1][4 * (t & 1) + v] = (_Float16)p;
+      }
+    rs += __shfl_xor(rs, 16);
+    rs += __shfl_xor(rs, 32);
+
+    // V -> Vt in this wave's LDS slice (keys past the context zeroed: p = 0 there, V may hold anything)
+#pragma unroll
+    for (int kg = 0; kg < 8; ++kg) {
+      u32x4 lo, hi;
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) {
+        const unsigned v0 = kg * 8 + 2 * jj < nvalid ? vr[kg][2 * jj] : 0u;
+        const unsigned v1 = kg * 8 + 2 * jj + 1 < nvalid ? vr[kg][2 * jj + 1] : 0u;
+        lo[jj] = __builtin_amdgcn_perm(v1, v0, 0x05040100u);
+        hi[jj] = __builtin_amdgcn_perm(v1, v0, 0x07060302u);
+      }
+      *(u32x4*)&vt[wv][2 * lane][kg * 8] = lo;
+      *(u32x4*)&vt[wv][2 * lane + 1][kg * 8] = hi;
+    }
+    __builtin_amdgcn_s_waitcnt(0xc07f);                 // lgkmcnt(0): this wave's LDS writes landed
+    __builtin_amdgcn_wave_barrier();
+
+    // O^T = Vt P^T; 32-key chunk cc2 in k-slot order 8g + i -> key 32 cc2 + 4g + i (i < 4), + 16 + 4g + i - 4
+#pragma unroll
+    for (int cc2 = 0; cc2 < 2; ++cc2)
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) {
+        const _Float16* row = &vt[wv][16 * dt + li][0];
+        const uint2 lo = *(const uint2*)(row + 32 * cc2 + 4 * lg);
+        const uint2 hi = *(const uint2*)(row + 32 * cc2 + 16 + 4 * lg);
+        uint4 vv = make_uint4(lo.x, lo.y, hi.x, hi.y);
+        acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(*reinterpret_cast<ah8*>(&vv), pB[cc2], acc[dt], 0, 0, 0);
+      }
   }
+
+  // the 4 page partials -> LDS (over the Vt slices), merged per (head, 8 dims) by thread t
+  __syncthreads();
+  float* po = (float*)&vt[0][0][0];                     // [4 waves][16 heads][HD]
+#pragma unroll
+  for (int dt = 0; dt < 8; ++dt) *(af4*)(po + (wv * 16 + li) * HD + 16 * dt + 4 * lg) = acc[dt];
+  if (lg == 0) {
+    wml[wv][li][0] = ml2;
+    wml[wv][li][1] = rs;
+  }
+  __syncthreads();
+  const int h = threadIdx.x >> 4, dg = threadIdx.x & 15;   // quads share h: whole quads are live or not
+  const bool hl = h < G;
+  float o[8], M = -INFINITY, L = 0.f;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) M = fmaxf(M, wml[w][h][0]);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) o[i] = 0.f;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    const float f = __builtin_amdgcn_exp2f(wml[w][h][0] - M);   // 0 for pages past the context
+    L = fmaf(f, wml[w][h][1], L);
+    const float4 x0 = *(const float4*)(po + (w * 16 + h) * HD + 8 * dg);
+    const float4 x1 = *(const float4*)(po + (w * 16 + h) * HD + 8 * dg + 4);
+    o[0] = fmaf(f, x0.x, o[0]); o[1] = fmaf(f, x0.y, o[1]); o[2] = fmaf(f, x0.z, o[2]); o[3] = fmaf(f, x0.w, o[3]);
+    o[4] = fmaf(f, x1.x, o[4]); o[5] = fmaf(f, x1.y, o[5]); o[6] = fmaf(f, x1.z, o[6]); o[7] = fmaf(f, x1.w, o[7]);
+  }
+
+  if (nsplit > 1) {                                     // split partial -> workspace; k_attn_merge_split ends it
+    float* wo = (float*)a.part + ((size_t)j * a.nkv + kvh) * ((size_t)nsp * G * (HD + 2));
+    float* wm = wo + (size_t)nsp * G * HD;
+    if (hl) {
+      float4* dst = (float4*)(wo + ((size_t)sp * G + h) * HD + 8 * dg);
+      dst[0] = make_float4(o[0], o[1], o[2], o[3]);
+      dst[1] = make_float4(o[4], o[5], o[6], o[7]);
+      if (dg == 0) *(float2*)(wm + ((size_t)sp * G + h) * 2) = make_float2(M, L);
+    }
+    return;
+  }
+  const float inv = hl ? 1.f / L : 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) o[i] *= inv;
+  attn_out8(a, j, kvh * G + (hl ? h : 0), dg, o, hl);
+}
+
+// Merge of the split partials of k_attn_decode_mfma for tokens whose context spans several splits: one
+// workgroup per (KV head, token), thread t = (head t / 16, dims 8 (t % 16) ..); every split's (M, L) and 8
+// values are loaded before the first use (nsplit <= 16).
+__global__ void __launch_bounds__(256) k_attn_merge_split(const AttnArgs a) {
+  const int G = a.nh / a.nkv;
+  const int nsp = (a.max_chunks + 3) / 4;
+  const int kvh = blockIdx.x, j = blockIdx.y;
+  const int nsplit = (a.pos[j] / PAGE + 1 + 3) / 4;
+  if (nsplit == 1) return;                              // finished by the attention kernel
+  const int h = threadIdx.x >> 4, dg = threadIdx.x & 15;
+  const bool hl = h < G;
+  const int hh = hl ? h : 0;
+  const float* wo = (const float*)a.part + ((size_t)j * a.nkv + kvh) * ((size_t)nsp * G * (HD + 2));
+  const float* wm = wo + (size_t)nsp * G * HD;
+  float2 ml[16];
+  float4 x0[16], x1[16];
+#pragma unroll
+  for (int s = 0; s < 16; ++s)
+    if (s < nsplit) {
+      ml[s] = *(const float2*)(wm + ((size_t)s * G + hh) * 2);
+      x0[s] = *(const float4*)(wo + ((size_t)s * G + hh) * HD + 8 * dg);
+      x1[s] = *(const float4*)(wo + ((size_t)s * G + hh) * HD + 8 * dg + 4);
+    }
+  float M = -INFINITY;
+#pragma unroll
+  for (int s = 0; s < 16; ++s)
+    if (s < nsplit) M = fmaxf(M, ml[s].x);
+  float o[8], L = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) o[i] = 0.f;
+#pragma unroll
+  for (int s = 0; s < 16; ++s)
+    if (s < nsplit) {
+      const float f = __builtin_amdgcn_exp2f(ml[s].x - M);
+      L = fmaf(f, ml[s].y, L);
+      o[0] = fmaf(f, x0[s].x, o[0]); o[1] = fmaf(f, x0[s].y, o[1]); o[2] = fmaf(f, x0[s].z, o[2]);
+      o[3] = fmaf(f, x0[s].w, o[3]); o[4] = fmaf(f, x1[s].x, o[4]); o[5] = fmaf(f, x1[s].y, o[5]);
+      o[6] = fmaf(f, x1[s].z, o[6]); o[7] = fmaf(f, x1[s].w, o[7]);
+    }
+  const float inv = 1.f / L;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) o[i] *= inv;
+  attn_out8(a, j, kvh * G + hh, dg, o, hl);
 }
 
 // ---------------------------------------------------------------------------------------------

@@ -16,6 +16,7 @@ __global__ void k_blockdots(const uint8_t*, int, int, const int8_t*, int, int*);
 template <int G>
 __global__ void k_attn_decode(const AttnArgs);
 __global__ void k_attn_merge(const AttnArgs);
+__global__ void k_attn_merge_split(const AttnArgs);
 __global__ void k_rmsnorm_fix_q8_1(const long long*, const float*, int8_t*, half2*, int, double);
 __global__ void k_qkv_finish(GemvArgs, long long*);
 }  // namespace q355
@@ -290,6 +291,7 @@ extern "C" int q355_attn_decode(const void* q, const void* kcache, const void* v
   REQUIRE(T > 0 && T <= 65535, "attn_decode: T=%d", T);
   REQUIRE((oq == nullptr) == (ods == nullptr), "attn_decode: oq and ods go together");
   REQUIRE(oq || !o32, "attn_decode: o32 needs the merge outputs oq/ods");
+  REQUIRE(oq || !fp32, "attn_decode: fp32 = 1 merges in the same launch: oq/ods required");
   AttnArgs a = {};
   a.q = (const __half*)q; a.kcache = (const __half*)kcache; a.vcache = (const __half*)vcache;
   a.pos = pos; a.block_table = block_table; a.bt_stride = bt_stride; a.nh = nh; a.nkv = nkv;
@@ -297,8 +299,11 @@ extern "C" int q355_attn_decode(const void* q, const void* kcache, const void* v
   a.oq = oq; a.ods = (half2*)ods; a.o32 = o32;
   hipStream_t s = (hipStream_t)stream;
   const dim3 grid(nkv * max_chunks, T);
-  if (fp32) {
+  if (fp32) {                                           // attention (4-page merge inside) + split merge
     hipLaunchKernelGGL(k_attn_decode_mfma, dim3(nkv * ((max_chunks + 3) / 4), T), dim3(256), 0, s, a);
+    if (int e = launched("attn_decode")) return e;
+    hipLaunchKernelGGL(k_attn_merge_split, dim3(nkv, T), dim3(256), 0, s, a);
+    return launched("attn_merge_split");
   } else {
     switch (nh / nkv) {
       case 4: hipLaunchKernelGGL((k_attn_decode<4, double, 2>), grid, dim3(512), 0, s, a); break;
@@ -327,8 +332,8 @@ extern "C" int q355_attn_decode_f16(const void* q, const void* kcache, const voi
   hipStream_t s = (hipStream_t)stream;
   hipLaunchKernelGGL(k_attn_decode_mfma, dim3(nkv * ((max_chunks + 3) / 4), T), dim3(256), 0, s, a);
   if (int e = launched("attn_decode_f16")) return e;
-  hipLaunchKernelGGL(k_attn_merge, dim3(T, nh), dim3(64), 0, s, a);
-  return launched("attn_merge");
+  hipLaunchKernelGGL(k_attn_merge_split, dim3(nkv, T), dim3(256), 0, s, a);
+  return launched("attn_merge_split");
 }
 
 extern "C" int q355_attn_o_resid(const uint8_t* qs, const void* d, int N, const double* part, int max_chunks,

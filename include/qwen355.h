@@ -115,12 +115,14 @@ int q355_embed_q4_0(const uint8_t* qs, const void* d, int V, int H, const int32_
                     void* stream);
 
 /* Decode GQA attention, split-K over 64-position pages: token j attends to positions 0..pos[j] of its
- * sequence (block_table row j), in f64. Writes the unnormalised partials part f64 [T][nh][max_chunks][130]
- * (o[128], running max, sum) of every live chunk; max_chunks >= (max pos)/64 + 1, <= 64.
- * If oq/ods are given it also merges them (second launch): Q8_1 oq int8 [T][nh*128], ods half2
- * [T][nh*4], and optionally fp32 o32 [T][nh*128]. GQA group nh/nkv in {4, 6, 8}.
- * fp32 = 0: scores, softmax and P.V in f64 (the batch-1 path, exact against the f64 oracle); fp32 = 1: in fp32
- * (the batched path, whose projections also accumulate in fp32).
+ * sequence (block_table row j); max_chunks >= (max pos)/64 + 1, <= 64; GQA group nh/nkv in {4, 6, 8}.
+ * fp32 = 0 (the batch-1 path, exact against the f64 oracle): scores, softmax and P.V in f64; writes the
+ * unnormalised partials part f64 [T][nh][max_chunks][130] (o[128], running max, sum) of every live chunk,
+ * and if oq/ods are given merges them (second launch) into Q8_1 oq int8 [T][nh*128], ods half2 [T][nh*4],
+ * optionally fp32 o32 [T][nh*128].
+ * fp32 = 1 (the batched path): fp16 matrix-core products, fp32 softmax, 4-page partials merged inside the
+ * attention launch and the rest by a second launch; oq/ods required (o32 optional); part is scratch
+ * (fp32 split partials, no initial contents needed).
  * Replaces ATTN2 / ATTN4 (lab/qwen_kernels.py:358-442, 517-605). */
 int q355_attn_decode(const void* q, const void* kcache, const void* vcache, const int32_t* pos,
                      const int32_t* block_table, int bt_stride, int nh, int nkv, int max_chunks, double scale,
@@ -175,8 +177,8 @@ int q355_rmsnorm_fix_f16(const int64_t* h, const float* w, void* xh, int T, int 
 int q355_gemm_q4_0_f16(const uint8_t* qs, const void* d, int N, int K, const void* xh, int T, int epi, float* y,
                        int64_t* yfix, void* yh, float* pmax, int32_t* pidx, void* stream);
 
-/* Batched decode attention (fp16 MFMA, fp32 softmax; the GQA group's heads as MFMA columns) + f64 merge of
- * the page partials -> fp16 oh [T][nh*128]. Arguments as q355_attn_decode; part is its scratch.
+/* Batched decode attention (fp16 MFMA, fp32 softmax; the GQA group's heads as MFMA columns) + merge of the
+ * page partials -> fp16 oh [T][nh*128]. Arguments and the part scratch as q355_attn_decode with fp32 = 1.
  * Replaces the batched ATTN4 + combine of scripts/qwen_batched_decode.py:156-187. */
 int q355_attn_decode_f16(const void* q, const void* kcache, const void* vcache, const int32_t* pos,
                          const int32_t* block_table, int bt_stride, int nh, int nkv, int max_chunks, double scale,

@@ -101,6 +101,42 @@ def test_attn_decode_longest_context(cuda, fp32):
         assert relerr(o32[j].cpu().numpy(), ref) < 1e-3
 
 
+def test_attn_decode_fp32_splits(cuda):
+    """The fp32 path's two-level merge (4 pages inside a workgroup, then the splits): contexts of 1 to 9
+    splits, one scratch buffer reused by calls with different T, fp16 and Q8_1 outputs."""
+    import torch
+    nh, nkv, mc = 12, 2, 36
+    rng = np.random.default_rng(7)
+    Tmax = 6
+    kc = rng.standard_normal((Tmax * mc, nkv, 64, 128)).astype(np.float16)
+    vc = rng.standard_normal((Tmax * mc, nkv, 64, 128)).astype(np.float16)
+    bt = rng.permutation(Tmax * mc).astype(np.int32).reshape(Tmax, mc)
+    q = rng.standard_normal((Tmax, nh * 128)).astype(np.float16)
+    part = torch.full((Tmax, nh, mc, 130), float('nan'), dtype=torch.float64, device=cuda)
+    kcd, vcd, btd, qd = dev(kc), dev(vc), dev(bt), dev(q)
+    for T, positions in [(6, [64 * mc - 1, 0, 255, 256, 1000, 2047]), (2, [300, 1500]), (5, [70, 2200, 9, 511, 512])]:
+        pos = np.array(positions, np.int32)
+        oq = torch.zeros(T, nh * 128, dtype=torch.int8, device=cuda)
+        ods = torch.zeros(T, nh * 4, 2, dtype=torch.float16, device=cuda)
+        o32 = torch.zeros(T, nh * 128, device=cuda)
+        oh = torch.zeros(T, nh * 128, dtype=torch.float16, device=cuda)
+        posd = dev(pos)
+        call("q355_attn_decode", ptr(qd), ptr(kcd), ptr(vcd), ptr(posd), ptr(btd), mc, nh, nkv, mc,
+             1 / math.sqrt(128), ptr(part), ptr(oq), ptr(ods), ptr(o32), T, 1)
+        call("q355_attn_decode_f16", ptr(qd), ptr(kcd), ptr(vcd), ptr(posd), ptr(btd), mc, nh, nkv, mc,
+             1 / math.sqrt(128), ptr(part), ptr(oh), T)
+        torch.cuda.synchronize()
+        for j in range(T):
+            K = np.concatenate([kc[bt[j, p]] for p in range(mc)], axis=1)
+            V = np.concatenate([vc[bt[j, p]] for p in range(mc)], axis=1)
+            ref = OM.attn_decode(q[j].reshape(nh, 128), K, V, int(pos[j]) + 1, nh, nkv)
+            assert relerr(o32[j].cpu().numpy(), ref) < 1e-3, (T, j)
+            assert relerr(oh[j].float().cpu().numpy(), ref) < 2e-3, (T, j)
+        rq, rd, _ = OQ.quantize_q8_1(o32.cpu().numpy())
+        assert np.array_equal(oq.cpu().numpy(), rq)
+        assert np.array_equal(ods.cpu().numpy()[..., 0], rd.astype(np.float16))
+
+
 @pytest.mark.parametrize("T", [1, 64])
 def test_mmq_decode_batch_extremes(cuda, T):
     """The int8 MFMA product at one token and at 64 tokens (four 16-token workgroups)."""
