@@ -159,13 +159,13 @@ __global__ void __launch_bounds__(G * W * 64) k_attn_decode(const AttnArgs a) {
 }
 
 // ---------------------------------------------------------------------------------------------
-// fp32 path on the matrix cores (the batched decode), merge included. Workgroup (token j, KV head, split
-// sp) = 4 waves, wave wv takes page c = 4 sp + wv; the G query heads of the group are the MFMA columns (16
-// columns, G used). S^T = K Q^T takes K rows straight from global memory as A operands; V is transposed
+// fp32 path on the matrix cores (the batched decode). Workgroup (token j, KV head, split sp) = 4 pages
+// c = 4 sp .. 4 sp + 3, one wave per KW keys of them (KW = 64: a page per wave); the G query heads of the
+// group are the MFMA columns (16 columns, G used). S^T = K Q^T takes K rows straight from global memory as A operands; V is transposed
 // into the wave's own LDS slice through dword gathers (lane l: dims 2l, 2l + 1 of 8 keys, packed in pairs),
 // so O^T = Vt P^T reads 8-key runs. P is rounded to fp16 for the MFMA (fp32 accumulation), max and
 // exponent in log2 units.
-// The 4 page partials merge through LDS (o = sum_w 2^(m_w - M) o_w, L likewise). A token whose context
+// The wave partials merge through LDS (o = sum_w 2^(m_w - M) o_w, L likewise). A token whose context
 // fits one split (<= 4 pages) is finished there: Q8_1 (oq/ods) or fp16 (oh), and fp32 o32 if asked.
 // Otherwise every split writes its unnormalised (o, M, L) to the workspace (the `part` buffer: per (token,
 // KV head) o [nsp][G][HD] then (M, L) [nsp][G], nsp = ceil(max_chunks / 4)) and k_attn_merge_split
@@ -173,8 +173,6 @@ __global__ void __launch_bounds__(G * W * 64) k_attn_decode(const AttnArgs a) {
 // second launch (its coherent stores, counter round trip and coherent reloads cost more than a launch).
 typedef _Float16 ah8 __attribute__((ext_vector_type(8)));
 typedef float af4 __attribute__((ext_vector_type(4)));
-constexpr int AV_ROW = PAGE + 4;   // Vt row (one dim, 64 keys) in halves: 136 B, so the dim 2l / 2l + 1
-                                   // 16 B writes spread over all banks
 
 // the finished head values of one thread (head h, dims 8 dg .. 8 dg + 7) -> the outputs
 __device__ __forceinline__ void attn_out8(const AttnArgs& a, int j, int h, int dg, const float (&o)[8], bool live) {
@@ -205,23 +203,26 @@ __device__ __forceinline__ void attn_out8(const AttnArgs& a, int j, int h, int d
   }
 }
 
-__global__ void __launch_bounds__(256) k_attn_decode_mfma(const AttnArgs a) {
-  __shared__ __align__(16) _Float16 vt[4][HD][AV_ROW];
-  __shared__ float wml[4][16][2];
+template <int KW>
+__global__ void __launch_bounds__(4 * PAGE / KW * 64) k_attn_decode_mfma(const AttnArgs a) {
+  constexpr int NWV = 4 * PAGE / KW, ROW = KW + 4;     // waves; Vt row (one dim, KW keys) in halves
+  __shared__ __align__(16) _Float16 vt[NWV][HD][ROW];
+  __shared__ float wml[NWV][16][2];
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int li = lane & 15, lg = lane >> 4;
   const int G = a.nh / a.nkv;
   const int nsp = (a.max_chunks + 3) / 4;
-  const int j = blockIdx.y, kvh = blockIdx.x / nsp, sp = blockIdx.x % nsp, c = sp * 4 + wv;
+  const int j = blockIdx.y, kvh = blockIdx.x / nsp, sp = blockIdx.x % nsp;
+  const int c = sp * 4 + wv / (PAGE / KW), k0 = (wv % (PAGE / KW)) * KW;   // page, first key in it
   // the page index does not depend on the position: both loads are in flight together
   const int pg = a.block_table[(size_t)j * a.bt_stride + min(c, a.max_chunks - 1)];
   const int pos = a.pos[j];
   const int nch = pos / PAGE + 1, nsplit = (nch + 3) / 4;
   if (sp >= nsplit) return;                             // uniform per workgroup
-  const bool live = c < nch;                            // uniform per wave; page 4 sp is always live
-  const int nvalid = min(PAGE, pos + 1 - c * PAGE);
-  const _Float16* kp = (const _Float16*)a.kcache + ((size_t)pg * a.nkv + kvh) * PAGE * HD;
-  const unsigned* vp = (const unsigned*)(a.vcache + ((size_t)pg * a.nkv + kvh) * PAGE * HD);
+  const int nvalid = min(KW, pos + 1 - c * PAGE - k0);  // keys of this wave inside the context
+  const bool live = nvalid > 0;                         // uniform per wave; wave 0 is always live
+  const _Float16* kp = (const _Float16*)a.kcache + (((size_t)pg * a.nkv + kvh) * PAGE + k0) * HD;
+  const unsigned* vp = (const unsigned*)(a.vcache + (((size_t)pg * a.nkv + kvh) * PAGE + k0) * HD);
   const int hq = kvh * G + li;
 
   af4 acc[8];
@@ -229,15 +230,15 @@ __global__ void __launch_bounds__(256) k_attn_decode_mfma(const AttnArgs a) {
   for (int dt = 0; dt < 8; ++dt) acc[dt] = af4{0.f, 0.f, 0.f, 0.f};
   float ml2 = -INFINITY, rs = 0.f;
   if (live) {
-    // every load of the page first: K operands (16 B per lane per tile), V dwords, q
-    uint4 kA[4][4];
+    // every load first: K operands (16 B per lane per 16-key tile), V dwords, q
+    uint4 kA[KW / 16][4];
 #pragma unroll
-    for (int t = 0; t < 4; ++t)
+    for (int t = 0; t < KW / 16; ++t)
 #pragma unroll
       for (int cc = 0; cc < 4; ++cc) kA[t][cc] = *(const uint4*)(kp + (16 * t + li) * HD + 32 * cc + 8 * lg);
-    unsigned vr[8][8];
+    unsigned vr[KW / 8][8];
 #pragma unroll
-    for (int kg = 0; kg < 8; ++kg)
+    for (int kg = 0; kg < KW / 8; ++kg)
 #pragma unroll
       for (int u = 0; u < 8; ++u) vr[kg][u] = vp[(kg * 8 + u) * (HD / 2) + lane];
     ah8 qB[4];
@@ -249,9 +250,9 @@ __global__ void __launch_bounds__(256) k_attn_decode_mfma(const AttnArgs a) {
     }
 
     // S^T: keys 16t + 4lg + v (rows), head li (column)
-    af4 sc[4];
+    af4 sc[KW / 16];
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
+    for (int t = 0; t < KW / 16; ++t) {
       sc[t] = af4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int cc = 0; cc < 4; ++cc)
@@ -260,18 +261,18 @@ __global__ void __launch_bounds__(256) k_attn_decode_mfma(const AttnArgs a) {
     const float sl2 = (float)a.scale * 1.4426950408889634f;
     float bm = -INFINITY;
 #pragma unroll
-    for (int t = 0; t < 4; ++t)
+    for (int t = 0; t < KW / 16; ++t)
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
         if (16 * t + 4 * lg + v >= nvalid) sc[t][v] = -INFINITY;
         bm = fmaxf(bm, sc[t][v]);
       }
     bm = fmaxf(bm, __shfl_xor(bm, 16));
-    bm = fmaxf(bm, __shfl_xor(bm, 32));                 // key 0 of the page is always valid: finite
+    bm = fmaxf(bm, __shfl_xor(bm, 32));                 // key 0 of a live wave is valid: finite
     ml2 = bm * sl2;
-    ah8 pB[2];
+    ah8 pB[KW / 32];
 #pragma unroll
-    for (int t = 0; t < 4; ++t)
+    for (int t = 0; t < KW / 16; ++t)
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
         const float p = __builtin_amdgcn_exp2f(fmaf(sc[t][v], sl2, -ml2));
@@ -283,7 +284,7 @@ __global__ void __launch_bounds__(256) k_attn_decode_mfma(const AttnArgs a) {
 
     // V -> Vt in this wave's LDS slice (keys past the context zeroed: p = 0 there, V may hold anything)
 #pragma unroll
-    for (int kg = 0; kg < 8; ++kg) {
+    for (int kg = 0; kg < KW / 8; ++kg) {
       u32x4 lo, hi;
 #pragma unroll
       for (int jj = 0; jj < 4; ++jj) {
@@ -300,7 +301,7 @@ __global__ void __launch_bounds__(256) k_attn_decode_mfma(const AttnArgs a) {
 
     // O^T = Vt P^T; 32-key chunk cc2 in k-slot order 8g + i -> key 32 cc2 + 4g + i (i < 4), + 16 + 4g + i - 4
 #pragma unroll
-    for (int cc2 = 0; cc2 < 2; ++cc2)
+    for (int cc2 = 0; cc2 < KW / 32; ++cc2)
 #pragma unroll
       for (int dt = 0; dt < 8; ++dt) {
         const _Float16* row = &vt[wv][16 * dt + li][0];
@@ -311,9 +312,9 @@ __global__ void __launch_bounds__(256) k_attn_decode_mfma(const AttnArgs a) {
       }
   }
 
-  // the 4 page partials -> LDS (over the Vt slices), merged per (head, 8 dims) by thread t
+  // the wave partials -> LDS (over the Vt slices), merged per (head, 8 dims) by thread t < 256
   __syncthreads();
-  float* po = (float*)&vt[0][0][0];                     // [4 waves][16 heads][HD]
+  float* po = (float*)&vt[0][0][0];                     // [NWV waves][16 heads][HD]
 #pragma unroll
   for (int dt = 0; dt < 8; ++dt) *(af4*)(po + (wv * 16 + li) * HD + 16 * dt + 4 * lg) = acc[dt];
   if (lg == 0) {
@@ -321,16 +322,17 @@ __global__ void __launch_bounds__(256) k_attn_decode_mfma(const AttnArgs a) {
     wml[wv][li][1] = rs;
   }
   __syncthreads();
+  if (threadIdx.x >= 256) return;
   const int h = threadIdx.x >> 4, dg = threadIdx.x & 15;   // quads share h: whole quads are live or not
   const bool hl = h < G;
   float o[8], M = -INFINITY, L = 0.f;
 #pragma unroll
-  for (int w = 0; w < 4; ++w) M = fmaxf(M, wml[w][h][0]);
+  for (int w = 0; w < NWV; ++w) M = fmaxf(M, wml[w][h][0]);
 #pragma unroll
   for (int i = 0; i < 8; ++i) o[i] = 0.f;
 #pragma unroll
-  for (int w = 0; w < 4; ++w) {
-    const float f = __builtin_amdgcn_exp2f(wml[w][h][0] - M);   // 0 for pages past the context
+  for (int w = 0; w < NWV; ++w) {
+    const float f = __builtin_amdgcn_exp2f(wml[w][h][0] - M);   // 0 for waves past the context
     L = fmaf(f, wml[w][h][1], L);
     const float4 x0 = *(const float4*)(po + (w * 16 + h) * HD + 8 * dg);
     const float4 x1 = *(const float4*)(po + (w * 16 + h) * HD + 8 * dg + 4);
