@@ -1,7 +1,7 @@
 """Benchmark of the MI355X Qwen2.5 Q4_0 hot path (BASELINE.json metric:
 "decode tok/s at batch 1/8/32 (Qwen2.5-1.5B-shape Q4_0); GEMV HBM GB/s").
 
-  python bench.py [--gpus 1] [--steps 256] [--warmup 8] [--no-cpu] [--quick]
+  python bench.py [--gpus 1] [--steps 256] [--warmup 8] [--no-cpu] [--quick] [--prefill-only]
 
 Workload: the full 28-layer Qwen2.5-1.5B-shape model with random weights
 (seeded, fp32 N(0, 0.02) quantized to Q4_0; tied Q4_0 embedding/head), a 128-token prompt of
@@ -236,6 +236,8 @@ def main():
     ap.add_argument("--quick", action="store_true", help="decode only (no roofline / GEMV / CPU legs)")
     ap.add_argument("--copy-probe", action="store_true",
                     help="only run a 64 MiB device-to-device copy 4 times (HBM counter calibration for rocprofv3 --pmc)")
+    ap.add_argument("--prefill-only", action="store_true",
+                    help="only the config-4 prefill leg (for rocprofv3 MFMA counters), one JSON line")
     ap.add_argument("--paired", type=int, default=0, metavar="ROUNDS",
                     help="instead of the contract line: paired A/B rounds (graph vs persistent step, A/A control, "
                          "batched B=8), one JSON line of ratio statistics")
@@ -265,6 +267,10 @@ def main():
     t0 = time.time()
     w = QM.random_weights(cfg, seed=0)
     log(f"weights generated in {time.time() - t0:.1f} s")
+    if args.prefill_only:
+        dm = QM.DeviceModel(w, cfg, maxlen=2048 + 64)
+        print(json.dumps({"prefill": prefill(dm)}), flush=True)
+        return
     prompt_len = 128
     maxlen = prompt_len + args.warmup + args.steps + 64
     dm = QM.DeviceModel(w, cfg, maxlen=max(2048 + 64, maxlen))
