@@ -655,6 +655,27 @@ extern "C" int q355_qkv_finish(int64_t* acc, const float* bias, const float* rop
   return launched("qkv_finish");
 }
 
+// QKV product of the prefill with the finish fused into the LDS-tiled kernel's epilogue: every output has one
+// writer (no K split), so no int64 accumulator, no second launch.
+extern "C" int q355_mmq_qkv_rope(const uint8_t* qs, const void* d, int N, int K, const int8_t* xq, const void* xds,
+                                 int T, const float* bias, const float* rope_cos, const float* rope_sin,
+                                 const int32_t* pos, const int32_t* block_table, int bt_stride, int seq_stride,
+                                 void* kcache, void* vcache, void* qout, int nh, int nkv, void* stream) {
+  if (int e = check_mat("mmq_qkv_rope", qs, d, N, K)) return e;
+  REQUIRE(xq && xds && bias && rope_cos && rope_sin && pos && block_table && kcache && vcache && qout,
+          "mmq_qkv_rope: null pointer");
+  REQUIRE(nh > 0 && nkv > 0 && N == (nh + 2 * nkv) * HD && N % 128 == 0,
+          "mmq_qkv_rope: N=%d must be (nh + 2 nkv) * 128 = %d and a multiple of 128", N, (nh + 2 * nkv) * HD);
+  REQUIRE(T >= 1 && T <= 65535 * 64 && bt_stride > 0 && (seq_stride == 0 || seq_stride == 1),
+          "mmq_qkv_rope: T=%d bt_stride=%d seq_stride=%d", T, bt_stride, seq_stride);
+  GemvArgs a = {};
+  a.qs = qs; a.d = (const __half*)d; a.N = N; a.K = K; a.T = T; a.xq = xq; a.xds = (const half2*)xds;
+  a.aux = bias; a.rope_cos = rope_cos; a.rope_sin = rope_sin; a.pos = pos; a.block_table = block_table;
+  a.bt_stride = bt_stride; a.seq_stride = seq_stride;
+  a.kcache = (__half*)kcache; a.vcache = (__half*)vcache; a.qout = (__half*)qout; a.nh = nh; a.nkv = nkv;
+  return launch_mmq_big<EPI_QKV>(a, (hipStream_t)stream);
+}
+
 static int pf_max_splits(int max_ctx) { return ((max_ctx - 1) / PAGE) / PF_SPLIT_PAGES + 1; }
 
 extern "C" int64_t q355_attn_prefill_ws_bytes(int P, int max_ctx, int nh, int nkv) {

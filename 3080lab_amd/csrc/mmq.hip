@@ -578,6 +578,35 @@ __global__ void __launch_bounds__(256) k_mmq_tile(const GemvArgs a) {
         a.pmax[(size_t)tok * np + rt0 / 4] = bv;
         a.pidx[(size_t)tok * np + rt0 / 4] = bi;
       }
+    } else if (EPI == EPI_QKV) {
+      // + bias, RoPE, fp16 q / K / V (one f64 -> fp16 rounding each, as k_qkv_finish): this lane's rows
+      // 4 lg + v of each tile are the RoPE pairs (v = 0, 1) and (2, 3) of the device row order
+      if (ok) {
+        const int nq = a.nh * HD, nk = a.nkv * HD;
+        const int pos = a.pos[tok];
+        const int pg = a.block_table[(size_t)(tok * a.seq_stride) * a.bt_stride + pos / PAGE];
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+          for (int pp = 0; pp < 2; ++pp) {
+            const int row = (rt0 + t) * 16 + 4 * lg + 2 * pp;
+            const double v0 = (double)acc[t][g][2 * pp] + (double)a.aux[row];
+            const double v1 = (double)acc[t][g][2 * pp + 1] + (double)a.aux[row + 1];
+            if (row < nq + nk) {
+              const int i = (row % HD) >> 1;           // pair (dim i, dim i + 64)
+              const double c = a.rope_cos[(size_t)pos * (HD / 2) + i], sn = a.rope_sin[(size_t)pos * (HD / 2) + i];
+              const __half lo = half_rn(v0 * c - v1 * sn), hi = half_rn(v1 * c + v0 * sn);
+              __half* dst = row < nq ? a.qout + (size_t)tok * nq + (row / HD) * HD
+                                     : a.kcache + (((size_t)pg * a.nkv + (row - nq) / HD) * PAGE + pos % PAGE) * HD;
+              dst[i] = lo;
+              dst[i + HD / 2] = hi;
+            } else {
+              const int rv = row - nq - nk;
+              __half2* vd = (__half2*)(a.vcache + (((size_t)pg * a.nkv + rv / HD) * PAGE + pos % PAGE) * HD + rv % HD);
+              *vd = __halves2half2(half_rn(v0), half_rn(v1));
+            }
+          }
+      }
     } else if (EPI == EPI_SWIGLU_Q8) {
       // this lane holds outputs 8t + 2lg, 8t + 2lg + 1 of its wave's 32; the 4 lanes of token li hold all 32
       float o[4][2];

@@ -244,11 +244,18 @@ def flash_prefill_v3_source(maxlen: int = 4096, q8: bool = True) -> KernelSpec:
     return KernelSpec("q355_attn_prefill")
 
 
+# chunks of at least this many tokens run the QKV product on the LDS-tiled kernel with the finish in its
+# epilogue (q355_mmq_qkv_rope: 16 x ceil(P / 64) workgroups); shorter ones keep the K-split product into the
+# int64 accumulator plus q355_qkv_finish, which has parallelism enough at small P
+QKV_FUSED_MIN_P = 1024
+
+
 class Prefill:
     """Chunked prefill of one sequence into a batch-1 Decoder's paged KV cache (scripts/qwen_prefill.py:196-246).
 
     chunk(ids, pos0) runs P prompt tokens at positions pos0 .. pos0 + P - 1 through all layers at once:
-      embed -> per layer: rmsnorm_fix_q8_1, MMQ qkv (int64 accumulator), qkv_finish (bias, RoPE, K/V write),
+      embed -> per layer: rmsnorm_fix_q8_1, MMQ qkv with bias + RoPE + K/V write in its epilogue
+      (P >= QKV_FUSED_MIN_P; else MMQ qkv into an int64 accumulator + qkv_finish),
       attn_prefill (causal, fp16 MFMA), quant_q8_1, MMQ o (+= h), rmsnorm_fix_q8_1, MMQ gate_up (SwiGLU -> Q8_1),
       MMQ down (+= h) -> final norm + head on the last token -> dec.tok = argmax, dec.pos = pos0 + P.
     The decoder then continues greedy decode from that state."""
@@ -281,10 +288,16 @@ class Prefill:
         L = m.layers[i]
         call("q355_rmsnorm_fix_q8_1", ptr(self.h), ptr(L["ln1"]), ptr(self.xq), ptr(self.xds), P, c.H, c.eps)
         W = L["qkv"]
-        call("q355_mmq_q4_0_q8_1", ptr(W.qs), ptr(W.d), W.N, W.K, ptr(self.xq), ptr(self.xds), P, 6,
-             None, ptr(self.qkv_acc), None, None, None, None)
-        call("q355_qkv_finish", ptr(self.qkv_acc), ptr(L["qkv_b"]), ptr(m.cos), ptr(m.sin), ptr(self.pos),
-             ptr(d.block_table), d.max_chunks, 0, ptr(d.kc[i]), ptr(d.vc[i]), ptr(self.q), c.NH, c.NKV, P)
+        if P >= QKV_FUSED_MIN_P:
+            # one writer per output: the finish (bias, RoPE, K/V write) runs in the GEMM epilogue
+            call("q355_mmq_qkv_rope", ptr(W.qs), ptr(W.d), W.N, W.K, ptr(self.xq), ptr(self.xds), P, ptr(L["qkv_b"]),
+                 ptr(m.cos), ptr(m.sin), ptr(self.pos), ptr(d.block_table), d.max_chunks, 0, ptr(d.kc[i]),
+                 ptr(d.vc[i]), ptr(self.q), c.NH, c.NKV)
+        else:
+            call("q355_mmq_q4_0_q8_1", ptr(W.qs), ptr(W.d), W.N, W.K, ptr(self.xq), ptr(self.xds), P, 6,
+                 None, ptr(self.qkv_acc), None, None, None, None)
+            call("q355_qkv_finish", ptr(self.qkv_acc), ptr(L["qkv_b"]), ptr(m.cos), ptr(m.sin), ptr(self.pos),
+                 ptr(d.block_table), d.max_chunks, 0, ptr(d.kc[i]), ptr(d.vc[i]), ptr(self.q), c.NH, c.NKV, P)
         call("q355_attn_prefill", ptr(self.q), ptr(d.kc[i]), ptr(d.vc[i]), ptr(d.block_table), pos0, P, c.NH, c.NKV,
              self.scale, ptr(self.att), ptr(self.attn_ws), self.attn_ws.numel() * 4)
         call("q355_quant_q8_1", ptr(self.att), ptr(self.xq), ptr(self.xds), P, c.NH * c.HD)

@@ -135,3 +135,75 @@ def test_prefill_chunked_equals_one_chunk(small):
     top2 = np.partition(lg, -2)[-2:]
     if top2[1] - top2[0] >= NEAR_TIE:
         assert int(a.tok.item()) == int(b.tok.item())
+
+
+def test_mmq_qkv_rope_equals_finish(cuda):
+    """The QKV product with the finish in the tiled kernel's epilogue writes the same q and K/V cache rows as
+    the K-split product into the int64 accumulator followed by q355_qkv_finish (both round once from f64)."""
+    import torch
+    c = QM.Config(L=1, V=1024)
+    N, K, T, pos0 = c.nqkv, c.H, 1100, 37
+    rng = np.random.default_rng(11)
+    from lab import gguf
+    W = QM.Q4Mat(gguf.quantize_q4_0(rng.standard_normal((N, K), dtype=np.float32) * np.float32(0.02)), N, K, "cuda")
+    x = torch.from_numpy(rng.standard_normal((T, K), dtype=np.float32)).cuda()
+    xq = torch.zeros(T, K, dtype=torch.int8, device=cuda)
+    xds = torch.zeros(T, K // 32, 2, dtype=torch.float16, device=cuda)
+    call("q355_quant_q8_1", ptr(x), ptr(xq), ptr(xds), T, K)
+    bias = torch.from_numpy(rng.standard_normal(N).astype(np.float32)).cuda()
+    maxlen = 1216
+    ang = np.arange(maxlen)[:, None] * (1e6 ** (-np.arange(64) * 2 / 128))[None, :]
+    cos = torch.from_numpy(np.cos(ang).astype(np.float32)).cuda()
+    sin = torch.from_numpy(np.sin(ang).astype(np.float32)).cuda()
+    pos = torch.arange(pos0, pos0 + T, dtype=torch.int32, device=cuda)
+    n_pages = maxlen // 64
+    table = torch.from_numpy(rng.permutation(n_pages).astype(np.int32)).cuda()
+    outs = []
+    for fused in (True, False):
+        kc = torch.zeros(n_pages, c.NKV, 64, 128, dtype=torch.float16, device=cuda)
+        vc = torch.zeros_like(kc)
+        q = torch.zeros(T, c.NH * 128, dtype=torch.float16, device=cuda)
+        if fused:
+            call("q355_mmq_qkv_rope", ptr(W.qs), ptr(W.d), N, K, ptr(xq), ptr(xds), T, ptr(bias), ptr(cos), ptr(sin),
+                 ptr(pos), ptr(table), n_pages, 0, ptr(kc), ptr(vc), ptr(q), c.NH, c.NKV)
+        else:
+            acc = torch.zeros(T, N, dtype=torch.int64, device=cuda)
+            call("q355_mmq_q4_0_q8_1", ptr(W.qs), ptr(W.d), N, K, ptr(xq), ptr(xds), T, 6, None, ptr(acc),
+                 None, None, None, None)
+            call("q355_qkv_finish", ptr(acc), ptr(bias), ptr(cos), ptr(sin), ptr(pos), ptr(table), n_pages, 0,
+                 ptr(kc), ptr(vc), ptr(q), c.NH, c.NKV, T)
+        torch.cuda.synchronize()
+        outs.append([t.cpu().numpy() for t in (q, kc, vc)])
+    for a, b in zip(*outs):
+        ulp = np.abs(a.view(np.int16).astype(np.int32) - b.view(np.int16).astype(np.int32))
+        assert ulp.max() <= 1 and (ulp > 0).mean() < 1e-3
+    # every cache row of positions pos0 .. pos0 + T - 1 was written (none of the untouched rows)
+    kc = outs[0][1]
+    rows = np.abs(kc).sum(axis=(1, 3)) > 0                 # [page, slot]
+    want = np.zeros_like(rows)
+    for p in range(pos0, pos0 + T):
+        want[table.cpu().numpy()[p // 64], p % 64] = True
+    assert np.array_equal(rows, want)
+
+
+def test_prefill_fused_qkv_equals_split(small, monkeypatch):
+    """A chunk long enough for the fused QKV epilogue leaves the same cache, hidden state and next token as the
+    accumulator + finish path (forced by raising the threshold)."""
+    import torch
+    w, dm, om = small
+    dm2 = QM.DeviceModel(w, CFG_S, maxlen=1216)
+    prompt = np.random.default_rng(8).integers(0, CFG_S.V, 1100)
+    res = []
+    for thr in (QB.QKV_FUSED_MIN_P, 1 << 30):
+        monkeypatch.setattr(QB, "QKV_FUSED_MIN_P", thr)
+        dec = QM.Decoder(dm2, T=1, max_ctx=1216)
+        pf = QB.Prefill(dec, max_chunk=1100)
+        pf.chunk(prompt, 0)
+        torch.cuda.synchronize()
+        res.append((pf.hidden_f64(1100).cpu().numpy(), [dec.kc[i].float().cpu().numpy() for i in range(CFG_S.L)],
+                    int(dec.tok.item())))
+        del pf, dec
+    assert relerr(res[0][0], res[1][0]) < 1e-3
+    for a, b in zip(res[0][1], res[1][1]):
+        assert relerr(a, b) < 1e-3
+    assert res[0][2] == res[1][2]
