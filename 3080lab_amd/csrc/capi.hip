@@ -683,16 +683,17 @@ extern "C" int64_t q355_attn_prefill_ws_bytes(int P, int max_ctx, int nh, int nk
   return (int64_t)(pf_ws_floats((P + PF_QB - 1) / PF_QB, nkv, nh / nkv, pf_max_splits(max_ctx)) * sizeof(float));
 }
 
-extern "C" int q355_attn_prefill(const void* q, const void* kcache, const void* vcache, const int32_t* block_table,
-                                 int pos0, int P, int nh, int nkv, float scale, float* out, void* ws,
-                                 int64_t ws_bytes, void* stream) {
-  REQUIRE(q && kcache && vcache && block_table && out, "attn_prefill: null pointer");
+static int attn_prefill(const void* q, const void* kcache, const void* vcache, const int32_t* block_table, int pos0,
+                        int P, int nh, int nkv, float scale, float* out, int8_t* oq, void* ods, void* ws,
+                        int64_t ws_bytes, hipStream_t stream) {
+  REQUIRE(q && kcache && vcache && block_table && (out || (oq && ods)), "attn_prefill: null pointer");
   REQUIRE(P >= 1 && pos0 >= 0, "attn_prefill: P=%d pos0=%d", P, pos0);
   REQUIRE(nh > 0 && nkv > 0 && nh % nkv == 0 && nh / nkv >= 4 && nh / nkv <= 8 && nkv <= 65535,
           "attn_prefill: nh=%d nkv=%d (4 to 8 query heads per KV head)", nh, nkv);
   PrefillAttnArgs a = {};
   a.q = (const __half*)q; a.kcache = (const __half*)kcache; a.vcache = (const __half*)vcache;
   a.block_table = block_table; a.pos0 = pos0; a.P = P; a.nh = nh; a.nkv = nkv; a.scale = scale; a.out = out;
+  a.oq = oq; a.ods = (half2*)ods;
   const int nqb = (P + PF_QB - 1) / PF_QB;
   int splits = 1;
   if (ws) {
@@ -703,8 +704,24 @@ extern "C" int q355_attn_prefill(const void* q, const void* kcache, const void* 
     a.ws = (float*)ws;
     a.max_splits = splits;
   }
-  hipLaunchKernelGGL(k_attn_prefill, dim3(nqb, splits, nkv), dim3(64 * (nh / nkv)), 0, (hipStream_t)stream, a);
+  hipLaunchKernelGGL(k_attn_prefill, dim3(nqb, splits, nkv), dim3(64 * (nh / nkv)), 0, stream, a);
   return launched("attn_prefill");
+}
+
+extern "C" int q355_attn_prefill(const void* q, const void* kcache, const void* vcache, const int32_t* block_table,
+                                 int pos0, int P, int nh, int nkv, float scale, float* out, void* ws,
+                                 int64_t ws_bytes, void* stream) {
+  REQUIRE(out, "attn_prefill: null output");
+  return attn_prefill(q, kcache, vcache, block_table, pos0, P, nh, nkv, scale, out, nullptr, nullptr, ws, ws_bytes,
+                      (hipStream_t)stream);
+}
+
+extern "C" int q355_attn_prefill_q8_1(const void* q, const void* kcache, const void* vcache,
+                                      const int32_t* block_table, int pos0, int P, int nh, int nkv, float scale,
+                                      int8_t* oq, void* ods, void* ws, int64_t ws_bytes, void* stream) {
+  REQUIRE(oq && ods, "attn_prefill_q8_1: null output");
+  return attn_prefill(q, kcache, vcache, block_table, pos0, P, nh, nkv, scale, nullptr, oq, ods, ws, ws_bytes,
+                      (hipStream_t)stream);
 }
 
 // ------------------------------------------------------------------------------------------------

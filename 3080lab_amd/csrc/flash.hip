@@ -252,15 +252,60 @@ __global__ void __launch_bounds__(512) k_attn_prefill(const PrefillAttnArgs a) {
     }
   }
 #pragma unroll
-  for (int cb = 0; cb < CBN; ++cb)
-    if (qi[cb] < a.P) {
-      const float inv = 1.f / l[cb];
+  for (int cb = 0; cb < CBN; ++cb) {
+    const float inv = 1.f / l[cb];
+    if (a.oq) {
+      // Q8_1 of the output row (the values the fp32 path stores, quantized as q355_quant_q8_1 does): block
+      // bk = dims 32 bk .. 32 bk + 31 lives in tiles dt = 2 bk, 2 bk + 1 of the 4 lanes li + 16 g
+#pragma unroll
+      for (int bk = 0; bk < 4; ++bk) {
+        float x[2][4];
+        float amax = 0.f;
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            x[h][v] = acc[cb][2 * bk + h][v] * inv;
+            amax = fmaxf(amax, fabsf(x[h][v]));
+          }
+        amax = fmaxf(amax, __shfl_xor(amax, 16));
+        amax = fmaxf(amax, __shfl_xor(amax, 32));
+        const __half d16 = __float2half_rn(amax / 127.0f);
+        const float df = __half2float(d16);
+        int sq = 0;
+        unsigned pk[2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          pk[h] = 0;
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            int q = 0;
+            if (df != 0.0f) {
+              q = (int)roundf(x[h][v] / df);
+              q = q > 127 ? 127 : (q < -127 ? -127 : q);
+            }
+            sq += q;
+            pk[h] |= (unsigned)(q & 255) << (8 * v);
+          }
+        }
+        sq += __shfl_xor(sq, 16);
+        sq += __shfl_xor(sq, 32);
+        if (qi[cb] < a.P) {
+          int8_t* o = a.oq + (size_t)qi[cb] * nq + hq * HD;
+          *(unsigned*)(o + 32 * bk + 4 * lg) = pk[0];
+          *(unsigned*)(o + 32 * bk + 16 + 4 * lg) = pk[1];
+          if (lg == 0)
+            a.ods[((size_t)qi[cb] * nq + hq * HD) / 32 + bk] = __halves2half2(d16, __float2half_rn(df * (float)sq));
+        }
+      }
+    } else if (qi[cb] < a.P) {
       float* o = a.out + (size_t)qi[cb] * nq + hq * HD;
 #pragma unroll
       for (int dt = 0; dt < 8; ++dt)
         *(float4*)(o + 16 * dt + 4 * lg) = make_float4(acc[cb][dt][0] * inv, acc[cb][dt][1] * inv,
                                                        acc[cb][dt][2] * inv, acc[cb][dt][3] * inv);
     }
+  }
 }
 
 }  // namespace q355

@@ -91,7 +91,9 @@ struct PrefillAttnArgs {
   const int* block_table;      // the sequence's page ids, >= (pos0 + P - 1) / PAGE + 1 entries
   int pos0, P, nh, nkv;
   float scale;
-  float* out;                  // [P][nh*HD] fp32
+  float* out;                  // [P][nh*HD] fp32, or (oq set) instead:
+  int8_t* oq;                  // Q8_1 of the output [P][nh*HD] int8 and
+  half2* ods;                  //   [P][nh*HD/32] (d, d * sum q)
   // split over keys (null: one workgroup per query block takes all its keys): partials
   // [n_qblocks][nkv][max_splits][G][CBN][8][64] float4 (O^T in MFMA accumulator order), m / l
   // [n_qblocks][nkv][max_splits][G][CBN][16][2], arrival counters [n_qblocks][nkv]

@@ -43,6 +43,7 @@ _SIGS = {
     "q355_attn_decode_f16": [_P, _P, _P, _P, _P, c_int, c_int, c_int, c_int, c_double, _P, _P, c_int, _P],
     "q355_mmq_nparts": [c_int],
     "q355_attn_prefill": [_P, _P, _P, _P, c_int, c_int, c_int, c_int, c_float, _P, _P, ctypes.c_int64, _P],
+    "q355_attn_prefill_q8_1": [_P, _P, _P, _P, c_int, c_int, c_int, c_int, c_float, _P, _P, _P, ctypes.c_int64, _P],
     "q355_attn_prefill_ws_bytes": [c_int, c_int, c_int, c_int],
     "q355_mega_ws_bytes": [c_int, c_int],
     "q355_mega_layer_bytes": [],

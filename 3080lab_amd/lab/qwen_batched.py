@@ -240,8 +240,9 @@ class BatchedDecoder:
 
 def flash_prefill_v3_source(maxlen: int = 4096, q8: bool = True) -> KernelSpec:
     """Causal prefill flash attention (lab/qwen_batched.py:1795-2037) -> q355_attn_prefill (fp16 MFMA,
-    fp32 accumulation); its output is quantized to Q8_1 by QUANT_Q8 for the O projection."""
-    return KernelSpec("q355_attn_prefill")
+    fp32 accumulation, fp32 output) or, with q8 (lab/qwen_batched.py:1811-1848), q355_attn_prefill_q8_1: the
+    output quantized to Q8_1 for the O projection in the same launch."""
+    return KernelSpec("q355_attn_prefill_q8_1" if q8 else "q355_attn_prefill")
 
 
 # chunks of at least this many tokens run the QKV product on the LDS-tiled kernel with the finish in its
@@ -256,7 +257,7 @@ class Prefill:
     chunk(ids, pos0) runs P prompt tokens at positions pos0 .. pos0 + P - 1 through all layers at once:
       embed -> per layer: rmsnorm_fix_q8_1, MMQ qkv with bias + RoPE + K/V write in its epilogue
       (P >= QKV_FUSED_MIN_P; else MMQ qkv into an int64 accumulator + qkv_finish),
-      attn_prefill (causal, fp16 MFMA), quant_q8_1, MMQ o (+= h), rmsnorm_fix_q8_1, MMQ gate_up (SwiGLU -> Q8_1),
+      attn_prefill_q8_1 (causal, fp16 MFMA, Q8_1 output), MMQ o (+= h), rmsnorm_fix_q8_1, MMQ gate_up (SwiGLU -> Q8_1),
       MMQ down (+= h) -> final norm + head on the last token -> dec.tok = argmax, dec.pos = pos0 + P.
     The decoder then continues greedy decode from that state."""
 
@@ -272,7 +273,6 @@ class Prefill:
         self.xds = torch.zeros(P, max(H, c.FFN) // 32, 2, dtype=torch.float16, device=dev)
         self.qkv_acc = torch.zeros(P, c.nqkv, dtype=torch.int64, device=dev)
         self.q = torch.zeros(P, c.NH * c.HD, dtype=torch.float16, device=dev)
-        self.att = torch.zeros(P, c.NH * c.HD, dtype=torch.float32, device=dev)
         self.mq = torch.zeros(P, c.FFN, dtype=torch.int8, device=dev)
         self.mds = torch.zeros(P, c.FFN // 32, 2, dtype=torch.float16, device=dev)
         self.ids = torch.zeros(P, dtype=torch.int32, device=dev)
@@ -298,9 +298,8 @@ class Prefill:
                  None, ptr(self.qkv_acc), None, None, None, None)
             call("q355_qkv_finish", ptr(self.qkv_acc), ptr(L["qkv_b"]), ptr(m.cos), ptr(m.sin), ptr(self.pos),
                  ptr(d.block_table), d.max_chunks, 0, ptr(d.kc[i]), ptr(d.vc[i]), ptr(self.q), c.NH, c.NKV, P)
-        call("q355_attn_prefill", ptr(self.q), ptr(d.kc[i]), ptr(d.vc[i]), ptr(d.block_table), pos0, P, c.NH, c.NKV,
-             self.scale, ptr(self.att), ptr(self.attn_ws), self.attn_ws.numel() * 4)
-        call("q355_quant_q8_1", ptr(self.att), ptr(self.xq), ptr(self.xds), P, c.NH * c.HD)
+        call("q355_attn_prefill_q8_1", ptr(self.q), ptr(d.kc[i]), ptr(d.vc[i]), ptr(d.block_table), pos0, P, c.NH,
+             c.NKV, self.scale, ptr(self.xq), ptr(self.xds), ptr(self.attn_ws), self.attn_ws.numel() * 4)
         W = L["o"]
         call("q355_mmq_q4_0_q8_1", ptr(W.qs), ptr(W.d), W.N, W.K, ptr(self.xq), ptr(self.xds), P, 6,
              None, ptr(self.h), None, None, None, None)

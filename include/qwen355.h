@@ -211,6 +211,12 @@ int q355_mmq_qkv_rope(const uint8_t* qs, const void* d, int N, int K, const int8
  * Replaces flash_prefill_v3_source (lab/qwen_batched.py:1795-2037). */
 int q355_attn_prefill(const void* q, const void* kcache, const void* vcache, const int32_t* block_table, int pos0,
                       int P, int nh, int nkv, float scale, float* out, void* ws, int64_t ws_bytes, void* stream);
+/* q355_attn_prefill with the output quantized to Q8_1 in the same launch (oq int8 [P][nh*128], ods half2
+ * [P][nh*4]): the values q355_attn_prefill stores, quantized exactly as q355_quant_q8_1 does.
+ * Replaces flash_prefill_v3_source(q8=True) (lab/qwen_batched.py:1811-1848). */
+int q355_attn_prefill_q8_1(const void* q, const void* kcache, const void* vcache, const int32_t* block_table,
+                           int pos0, int P, int nh, int nkv, float scale, int8_t* oq, void* ods, void* ws,
+                           int64_t ws_bytes, void* stream);
 /* Workspace bytes of q355_attn_prefill for chunks of up to P queries with pos0 + P <= max_ctx (-1: bad sizes). */
 int64_t q355_attn_prefill_ws_bytes(int P, int max_ctx, int nh, int nkv);
 

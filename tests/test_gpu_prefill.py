@@ -61,6 +61,16 @@ def test_attn_prefill_matches_oracle(cuda, P, pos0, nh, nkv, split):
     if split:
         cnt = ws[-((P + 15) // 16) * nkv:].view(torch.int32)
         assert int(cnt.abs().sum()) == 0
+    # the Q8_1-output form quantizes exactly the values the fp32 form stores
+    oq = torch.zeros(P, nh * 128, dtype=torch.int8, device=cuda)
+    ods = torch.zeros(P, nh * 4, 2, dtype=torch.float16, device=cuda)
+    call("q355_attn_prefill_q8_1", ptr(q_t), ptr(kc_t), ptr(vc_t), ptr(table_t), pos0, P, nh, nkv,
+         1.0 / math.sqrt(128), ptr(oq), ptr(ods), ptr(ws) if split else None, nb)
+    xq = torch.zeros_like(oq)
+    xds = torch.zeros_like(ods)
+    call("q355_quant_q8_1", ptr(out), ptr(xq), ptr(xds), P, nh * 128)
+    torch.cuda.synchronize()
+    assert torch.equal(oq, xq) and torch.equal(ods, xds)
 
 
 def test_attn_prefill_bad_args(cuda):
@@ -69,6 +79,8 @@ def test_attn_prefill_bad_args(cuda):
         call("q355_attn_prefill", 1, 1, 1, 1, 0, 0, 12, 2, 0.1, 1, None, 0)
     with pytest.raises(HipError, match="workspace"):
         call("q355_attn_prefill", 1, 1, 1, 1, 0, 2048, 12, 2, 0.1, 1, 1, 100)
+    with pytest.raises(HipError, match="null output"):
+        call("q355_attn_prefill_q8_1", 1, 1, 1, 1, 0, 16, 12, 2, 0.1, None, 1, None, 0)
 
 
 CFG_S = QM.Config(L=2, V=4096)
