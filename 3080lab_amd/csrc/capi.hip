@@ -399,17 +399,22 @@ static int launch_mmq(GemvArgs a, int KS, hipStream_t s) {
   return launched("mmq");
 }
 
-// Prefill sizes (STORE, RESID_FIX, SWIGLU_Q8 with at least one 128 x 64 tile per CU): the LDS-tiled kernel,
-// 2 x 2 waves of 64 rows x 64 tokens (32 tokens when 64-token tiles leave fewer than 2 workgroups per CU).
-// One K slice: each output has exactly one writer, so RESID_FIX is a plain read-add-write.
+// Prefill sizes (STORE, RESID_FIX, SWIGLU_Q8, QKV with at least one 128 x 64 tile per CU): the LDS-tiled
+// kernel, workgroups of 128 rows x 64 tokens (2 x 2 waves of 64 x 32; 165 VGPRs: three per CU). One K slice: each output
+// has exactly one writer, so RESID_FIX is a plain read-add-write. Measured at P = 2048: gate_up 247.6 us with
+// 128-token workgroups (two per CU) against 223.5 us with 64-token ones.
 template <int EPI>
 static int launch_mmq_big(GemvArgs a, hipStream_t s) {
-  const bool tg4 = (a.N / 128) * ((a.T + 127) / 128) >= 512;
-  constexpr size_t lds4 = 2 * LdsTile<2, 2, 4, TILE_CB>::BUF, lds2 = 2 * LdsTile<2, 2, 2, TILE_CB>::BUF;
-  if (tg4) {
-    hipLaunchKernelGGL((k_mmq_tile<2, 2, 4, EPI>), dim3(a.N / 128, 1, (a.T + 127) / 128), dim3(256), lds4, s, a);
+  const int rt = a.N / 128, tt2 = (a.T + 63) / 64;
+  if ((rt * tt2) % 256 == 0 || rt * tt2 >= 1024) {
+    constexpr size_t lds2 = 2 * LdsTile<2, 2, 2, TILE_CB>::BUF;
+    hipLaunchKernelGGL((k_mmq_tile<2, 2, 2, EPI>), dim3(rt, 1, tt2), dim3(256), lds2, s, a);
   } else {
-    hipLaunchKernelGGL((k_mmq_tile<2, 2, 2, EPI>), dim3(a.N / 128, 1, (a.T + 63) / 64), dim3(256), lds2, s, a);
+    // 32-token workgroups: twice the workgroups, so a grid that would leave some CUs with one 64-token
+    // workgroup and others with two (N = 1536: 384 of them) spreads evenly (768); measured 166.6 -> 150.6 us
+    // for the P = 2048 down product (64-row workgroups of 2 waves: 186 us)
+    constexpr size_t lds1 = 2 * LdsTile<2, 2, 1, TILE_CB>::BUF;
+    hipLaunchKernelGGL((k_mmq_tile<2, 2, 1, EPI>), dim3(rt, 1, (a.T + 31) / 32), dim3(256), lds1, s, a);
   }
   return launched("mmq");
 }
