@@ -406,13 +406,13 @@ static int launch_mmq(GemvArgs a, int KS, hipStream_t s) {
 template <int EPI>
 static int launch_mmq_big(GemvArgs a, hipStream_t s) {
   const int rt = a.N / 128, tt2 = (a.T + 63) / 64;
-  if ((rt * tt2) % 256 == 0 || rt * tt2 >= 1024) {
+  if (rt * tt2 >= 768) {                           // three or more 64-token workgroups per CU
     constexpr size_t lds2 = 2 * LdsTile<2, 2, 2, TILE_CB>::BUF;
     hipLaunchKernelGGL((k_mmq_tile<2, 2, 2, EPI>), dim3(rt, 1, tt2), dim3(256), lds2, s, a);
   } else {
-    // 32-token workgroups: twice the workgroups, so a grid that would leave some CUs with one 64-token
-    // workgroup and others with two (N = 1536: 384 of them) spreads evenly (768); measured 166.6 -> 150.6 us
-    // for the P = 2048 down product (64-row workgroups of 2 waves: 186 us)
+    // 32-token workgroups: twice the workgroups for grids that give CUs fewer than three 64-token ones, or
+    // an uneven number (N = 1536: 384 of them): measured at P = 2048, down 166.6 -> 150.6 us, qkv (512 ->
+    // 1024 workgroups) 49.9 -> 42.5 us; 64-row workgroups of 2 waves instead: down 186 us
     constexpr size_t lds1 = 2 * LdsTile<2, 2, 1, TILE_CB>::BUF;
     hipLaunchKernelGGL((k_mmq_tile<2, 2, 1, EPI>), dim3(rt, 1, (a.T + 31) / 32), dim3(256), lds1, s, a);
   }
