@@ -267,8 +267,7 @@ __global__ void __launch_bounds__(4 * PAGE / KW * 64) k_attn_decode_mfma(const A
         if (16 * t + 4 * lg + v >= nvalid) sc[t][v] = -INFINITY;
         bm = fmaxf(bm, sc[t][v]);
       }
-    bm = fmaxf(bm, __shfl_xor(bm, 16));
-    bm = fmaxf(bm, __shfl_xor(bm, 32));                 // key 0 of a live wave is valid: finite
+    bm = col4_max(bm);                                  // key 0 of a live wave is valid: finite
     ml2 = bm * sl2;
     ah8 pB[KW / 32];
 #pragma unroll
@@ -279,8 +278,7 @@ __global__ void __launch_bounds__(4 * PAGE / KW * 64) k_attn_decode_mfma(const A
         rs += p;
         pB[t >> 1][4 * (t & 1) + v] = (_Float16)p;
       }
-    rs += __shfl_xor(rs, 16);
-    rs += __shfl_xor(rs, 32);
+    rs = col4_sum(rs);
 
     // V -> Vt in this wave's LDS slice (keys past the context zeroed: p = 0 there, V may hold anything)
 #pragma unroll

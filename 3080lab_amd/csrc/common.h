@@ -233,6 +233,29 @@ __device__ __forceinline__ int q8_1_lane32(float x, half2* ds, bool leader) {
   return q;
 }
 
+// Reductions over the 4 lanes l % 16 + 16 g (the MFMA accumulator column) with gfx950's permlane swaps, no
+// LDS round trip: v_permlane16_swap / v_permlane32_swap of a register with itself leave lane l holding
+// {x[l], x[l ^ 16]} (resp. {x[l], x[l ^ 32]}) in the two results, in either order, so the max or sum of the
+// pair is the xor-partner reduction.
+__device__ __forceinline__ float col4_max(float v) {
+  auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float col4_sum(float v) {
+  auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ int col4_isum(int v) {
+  auto r = __builtin_amdgcn_permlane16_swap((unsigned)v, (unsigned)v, false, false);
+  v = (int)r[0] + (int)r[1];
+  r = __builtin_amdgcn_permlane32_swap((unsigned)v, (unsigned)v, false, false);
+  return (int)r[0] + (int)r[1];
+}
+
 // Device-coherent relaxed accesses (agent scope): stores reach the memory every XCD reads and loads bypass
 // the non-coherent caches, so workgroups on different XCDs can exchange data without cache maintenance.
 template <typename T>

@@ -159,8 +159,7 @@ __global__ void __launch_bounds__(512) k_attn_prefill(const PrefillAttnArgs a) {
       float bm = -INFINITY;                                // raw-score max; scaled once below
 #pragma unroll
       for (int t = 0; t < 4; ++t) bm = fmaxf(bm, fmaxf(fmaxf(s[cb][t][0], s[cb][t][1]), fmaxf(s[cb][t][2], s[cb][t][3])));
-      bm = fmaxf(bm, __shfl_xor(bm, 16));
-      bm = fmaxf(bm, __shfl_xor(bm, 32));
+      bm = col4_max(bm);
       const float mn = fmaxf(m[cb], bm * sl2);
       const float ms = mn == -INFINITY ? 0.f : mn;         // fully masked so far: keep exp2 finite
       const float alpha = __builtin_amdgcn_exp2f(m[cb] - ms);
@@ -173,8 +172,7 @@ __global__ void __launch_bounds__(512) k_attn_prefill(const PrefillAttnArgs a) {
           rs += p;
           pB[cb][t >> 1][4 * (t & 1) + v] = (_Float16)p;
         }
-      rs += __shfl_xor(rs, 16);
-      rs += __shfl_xor(rs, 32);
+      rs = col4_sum(rs);
       l[cb] = l[cb] * alpha + rs;
       m[cb] = mn;
       if (__any(alpha != 1.f)) {                           // the running max moved for some query of the wave
@@ -268,8 +266,7 @@ __global__ void __launch_bounds__(512) k_attn_prefill(const PrefillAttnArgs a) {
             x[h][v] = acc[cb][2 * bk + h][v] * inv;
             amax = fmaxf(amax, fabsf(x[h][v]));
           }
-        amax = fmaxf(amax, __shfl_xor(amax, 16));
-        amax = fmaxf(amax, __shfl_xor(amax, 32));
+        amax = col4_max(amax);
         const __half d16 = __float2half_rn(amax / 127.0f);
         const float df = __half2float(d16);
         int sq = 0;
@@ -288,8 +285,7 @@ __global__ void __launch_bounds__(512) k_attn_prefill(const PrefillAttnArgs a) {
             pk[h] |= (unsigned)(q & 255) << (8 * v);
           }
         }
-        sq += __shfl_xor(sq, 16);
-        sq += __shfl_xor(sq, 32);
+        sq = col4_isum(sq);
         if (qi[cb] < a.P) {
           int8_t* o = a.oq + (size_t)qi[cb] * nq + hq * HD;
           *(unsigned*)(o + 32 * bk + 4 * lg) = pk[0];
