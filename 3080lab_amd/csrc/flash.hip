@@ -24,9 +24,9 @@ namespace q355 {
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef float f4 __attribute__((ext_vector_type(4)));
 
+constexpr int KP = 2;              // KV pages per step of the key loop
 constexpr int FK_ROW = HD + 8;     // K row in LDS (halves), padded
-constexpr int FV_ROW = PAGE + 4;   // Vt row (one dim, 64 keys) in LDS (halves): 136 B, so the transposing
-                                   // 16 B writes of dims 2l and 2l + 1 spread over all banks
+constexpr int FV_ROW = KP * PAGE + 4;   // Vt row (one dim, KP pages of keys) in LDS (halves), padded
 
 __device__ __forceinline__ h8 as_h8(uint4 v) { return *reinterpret_cast<h8*>(&v); }
 
@@ -40,7 +40,7 @@ constexpr int CBN = PF_QB / 16;      // 16-query MFMA column blocks per wave
 // to arrive (counter per query block and KV head, reset by it) merges them and writes the output. Partials
 // and counters use device-coherent accesses: the splits may run on different XCDs.
 __global__ void __launch_bounds__(512) k_attn_prefill(const PrefillAttnArgs a) {
-  __shared__ __align__(16) _Float16 ks[PAGE][FK_ROW];
+  __shared__ __align__(16) _Float16 ks[KP * PAGE][FK_ROW];
   __shared__ __align__(16) _Float16 vt[HD][FV_ROW];
   const int G = a.nh / a.nkv;
   const int qb = gridDim.x - 1 - blockIdx.x, split = blockIdx.y, kvh = blockIdx.z;
@@ -72,26 +72,27 @@ __global__ void __launch_bounds__(512) k_attn_prefill(const PrefillAttnArgs a) {
   // staging: K as 1024 16 B pieces (key e / 16, dims 8 (e % 16) ..); V transposed: lane l of wave w takes
   // dims 2l, 2l + 1 of the 8-key groups w, w + G, ...: 8 dword loads per group, packed into two 16 B rows
   constexpr int VMAX = 2;                                // V key groups per thread (G >= 4)
-  u32x4 kr[4];
-  unsigned vr[VMAX][8];
+  u32x4 kr[KP][4];
+  unsigned vr[KP][VMAX][8];
   const int kper = (1024 + nthr - 1) / nthr, vper = (8 + G - 1) / G;
   // the page ids of this workgroup's key range, read once (each page's loads then wait on one latency)
   __shared__ int pages[64];
   for (int i = threadIdx.x; i < nkb - kb0 && i < 64; i += nthr) pages[i] = a.block_table[kb0 + i];
   __syncthreads();
 #define Q355_LOAD_PAGE(kb)                                                                     \
-  {                                                                                            \
-    const int pg_ = (kb) - kb0 < 64 ? pages[(kb) - kb0] : a.block_table[kb];                   \
+  _Pragma("unroll") for (int p_ = 0; p_ < KP; ++p_) {                                          \
+    const int kbp_ = min((kb) + p_, nkb - 1);   /* past the range: a repeat, masked (diag step) */ \
+    const int pg_ = kbp_ - kb0 < 64 ? pages[kbp_ - kb0] : a.block_table[kbp_];                 \
     const u32x4* kp_ = (const u32x4*)(a.kcache + ((size_t)pg_ * a.nkv + kvh) * PAGE * HD);     \
     const unsigned* vp_ = (const unsigned*)(a.vcache + ((size_t)pg_ * a.nkv + kvh) * PAGE * HD); \
     _Pragma("unroll") for (int i = 0; i < 4; ++i) {                                            \
       const int e = threadIdx.x + nthr * i;                                                    \
-      if (i < kper && e < 1024) kr[i] = kp_[e];                                                \
+      if (i < kper && e < 1024) kr[p_][i] = kp_[e];                                            \
     }                                                                                          \
     _Pragma("unroll") for (int i = 0; i < VMAX; ++i) {                                         \
       const int kg = wv + G * i;                                                               \
       if (i < vper && kg < 8)                                                                  \
-        _Pragma("unroll") for (int u = 0; u < 8; ++u) vr[i][u] = vp_[(kg * 8 + u) * (HD / 2) + lane]; \
+        _Pragma("unroll") for (int u = 0; u < 8; ++u) vr[p_][i][u] = vp_[(kg * 8 + u) * (HD / 2) + lane]; \
     }                                                                                          \
   }
 
@@ -106,34 +107,37 @@ __global__ void __launch_bounds__(512) k_attn_prefill(const PrefillAttnArgs a) {
   }
 
   Q355_LOAD_PAGE(kb0);
-  for (int kb = kb0; kb < nkb; ++kb) {
-    __syncthreads();                                       // previous page's LDS reads are done
+  for (int kb = kb0; kb < nkb; kb += KP) {
+    __syncthreads();                                       // previous step's LDS reads are done
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int e = threadIdx.x + nthr * i;
-      if (i < kper && e < 1024) *(u32x4*)&ks[e >> 4][(e & 15) * 8] = kr[i];
-    }
+    for (int p = 0; p < KP; ++p) {
 #pragma unroll
-    for (int i = 0; i < VMAX; ++i) {
-      const int kg = wv + G * i;
-      if (i < vper && kg < 8) {
-        u32x4 lo, hi;
+      for (int i = 0; i < 4; ++i) {
+        const int e = threadIdx.x + nthr * i;
+        if (i < kper && e < 1024) *(u32x4*)&ks[p * PAGE + (e >> 4)][(e & 15) * 8] = kr[p][i];
+      }
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          lo[j] = __builtin_amdgcn_perm(vr[i][2 * j + 1], vr[i][2 * j], 0x05040100u);
-          hi[j] = __builtin_amdgcn_perm(vr[i][2 * j + 1], vr[i][2 * j], 0x07060302u);
+      for (int i = 0; i < VMAX; ++i) {
+        const int kg = wv + G * i;
+        if (i < vper && kg < 8) {
+          u32x4 lo, hi;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            lo[j] = __builtin_amdgcn_perm(vr[p][i][2 * j + 1], vr[p][i][2 * j], 0x05040100u);
+            hi[j] = __builtin_amdgcn_perm(vr[p][i][2 * j + 1], vr[p][i][2 * j], 0x07060302u);
+          }
+          *(u32x4*)&vt[2 * lane][p * PAGE + kg * 8] = lo;
+          *(u32x4*)&vt[2 * lane + 1][p * PAGE + kg * 8] = hi;
         }
-        *(u32x4*)&vt[2 * lane][kg * 8] = lo;
-        *(u32x4*)&vt[2 * lane + 1][kg * 8] = hi;
       }
     }
     __syncthreads();
-    Q355_LOAD_PAGE(min(kb + 1, nkb - 1));                  // next page (clamped: unconditional), in flight now
+    Q355_LOAD_PAGE(min(kb + KP, nkb - 1));                 // next step (clamped: unconditional), in flight now
 
     // S^T tiles: keys 16t + (4g + v), query li of column block cb; each K operand feeds both blocks
-    f4 s[CBN][4];
+    f4 s[CBN][4 * KP];
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
+    for (int t = 0; t < 4 * KP; ++t) {
 #pragma unroll
       for (int cb = 0; cb < CBN; ++cb) s[cb][t] = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -143,29 +147,30 @@ __global__ void __launch_bounds__(512) k_attn_prefill(const PrefillAttnArgs a) {
         for (int cb = 0; cb < CBN; ++cb) s[cb][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kA, qf[cb][c], s[cb][t], 0, 0, 0);
       }
     }
-    h8 pB[CBN][2];
-    // causal mask only where the page reaches past the block's first query (uniform); queries past P need
-    // none: each query column of S, P and O is independent and is never stored
-    const bool diag = (kb + 1) * PAGE - 1 > a.pos0 + qb * PF_QB;
+    h8 pB[CBN][2 * KP];
+    // causal mask only where the step reaches past the block's first query (uniform; this includes the step
+    // with a repeated page past the range); queries past P need none: each query column of S, P and O is
+    // independent and is never stored
+    const bool diag = (kb + KP) * PAGE - 1 > a.pos0 + qb * PF_QB;
 #pragma unroll
     for (int cb = 0; cb < CBN; ++cb) {
       if (diag) {
 #pragma unroll
-        for (int t = 0; t < 4; ++t)
+        for (int t = 0; t < 4 * KP; ++t)
 #pragma unroll
           for (int v = 0; v < 4; ++v)
             if (kb * PAGE + 16 * t + 4 * lg + v > qpos[cb]) s[cb][t][v] = -INFINITY;
       }
       float bm = -INFINITY;                                // raw-score max; scaled once below
 #pragma unroll
-      for (int t = 0; t < 4; ++t) bm = fmaxf(bm, fmaxf(fmaxf(s[cb][t][0], s[cb][t][1]), fmaxf(s[cb][t][2], s[cb][t][3])));
+      for (int t = 0; t < 4 * KP; ++t) bm = fmaxf(bm, fmaxf(fmaxf(s[cb][t][0], s[cb][t][1]), fmaxf(s[cb][t][2], s[cb][t][3])));
       bm = col4_max(bm);
       const float mn = fmaxf(m[cb], bm * sl2);
       const float ms = mn == -INFINITY ? 0.f : mn;         // fully masked so far: keep exp2 finite
       const float alpha = __builtin_amdgcn_exp2f(m[cb] - ms);
       float rs = 0.f;
 #pragma unroll
-      for (int t = 0; t < 4; ++t)
+      for (int t = 0; t < 4 * KP; ++t)
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
           const float p = __builtin_amdgcn_exp2f(fmaf(s[cb][t][v], sl2, -ms));
@@ -180,9 +185,9 @@ __global__ void __launch_bounds__(512) k_attn_prefill(const PrefillAttnArgs a) {
         for (int t = 0; t < 8; ++t) acc[cb][t] *= alpha;
       }
     }
-    // O^T += Vt P^T over two 32-key chunks; each Vt operand feeds both blocks
+    // O^T += Vt P^T over 2 KP 32-key chunks; each Vt operand feeds every block
 #pragma unroll
-    for (int c = 0; c < 2; ++c)
+    for (int c = 0; c < 2 * KP; ++c)
 #pragma unroll
       for (int dt = 0; dt < 8; ++dt) {
         const _Float16* row = &vt[16 * dt + li][0];
