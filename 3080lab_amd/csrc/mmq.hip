@@ -18,6 +18,8 @@
 
 namespace q355 {
 
+typedef float v16f __attribute__((ext_vector_type(16)));
+
 typedef int v4i __attribute__((ext_vector_type(4)));
 
 // nibbles of one Q4_0 row half (8 bytes) -> the 8 int8 values 16 (q - 8) of k-group g
@@ -492,27 +494,27 @@ __global__ void __launch_bounds__(256) k_mmq_tile(const GemvArgs a) {
 #pragma unroll 1
     for (int blk = 0; blk < CB; ++blk) {
       long w[4];
-      float4 dw[4];
 #pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        w[t] = snib8(*(const uint2*)(sA + (t * CB + blk) * 256 + li * 16 + (lg & 1) * 8), lg);
-        dw[t] = *(const float4*)(sW + (t * CB + blk) * 64 + lg * 16);
-      }
+      for (int t = 0; t < 4; ++t) w[t] = snib8(*(const uint2*)(sA + (t * CB + blk) * 256 + li * 16 + (lg & 1) * 8), lg);
+      // the block scales d_w d_x of all 4 x 16 x 16 outputs of a token group in ONE 4-block outer product on
+      // the matrix cores (v_mfma_f32_16x16x1f32: block t = tile t; lane 16 t + r supplies d_w of row r, every
+      // lane d_x of its token li; lane l receives d_w[t][4 lg + v] d_x[li] in register 4 t + v): the 16
+      // exact fp32 products that would otherwise be 16 VALU multiplies
+      const float wl = *(const float*)(sW + (lg * CB + blk) * 64 + li * 4);
 #pragma unroll
       for (int g = 0; g < TG; ++g) {
         const long bx = *(const long*)(sB + ((g * CB + blk) * 16 + li) * 32 + (lg ^ ((li >> 3) << 1)) * 8);
         const float dx = sX[blk * TW + g * 16 + li];
         const v4i zero = {0, 0, 0, 0};
+        const v16f zf = {};
+        const v16f sc = __builtin_amdgcn_mfma_f32_16x16x1f32(wl, dx, zf, 0, 0, 0);
         v4i c[4];
 #pragma unroll
         for (int t = 0; t < 4; ++t) c[t] = __builtin_amdgcn_mfma_i32_16x16x32_i8(w[t], bx, zero, 0, 0, 0);
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          acc[t][g][0] = fmaf(dw[t].x * dx, (float)c[t][0], acc[t][g][0]);
-          acc[t][g][1] = fmaf(dw[t].y * dx, (float)c[t][1], acc[t][g][1]);
-          acc[t][g][2] = fmaf(dw[t].z * dx, (float)c[t][2], acc[t][g][2]);
-          acc[t][g][3] = fmaf(dw[t].w * dx, (float)c[t][3], acc[t][g][3]);
-        }
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+          for (int v = 0; v < 4; ++v) acc[t][g][v] = fmaf(sc[4 * t + v], (float)c[t][v], acc[t][g][v]);
       }
     }
     if (more) {
