@@ -81,6 +81,10 @@ def test_attn_prefill_bad_args(cuda):
         call("q355_attn_prefill", 1, 1, 1, 1, 0, 2048, 12, 2, 0.1, 1, 1, 100)
     with pytest.raises(HipError, match="null output"):
         call("q355_attn_prefill_q8_1", 1, 1, 1, 1, 0, 16, 12, 2, 0.1, None, 1, None, 0)
+    with pytest.raises(HipError, match="mmq_qkv_rope"):        # N must be (nh + 2 nkv) * 128
+        call("q355_mmq_qkv_rope", 16, 16, 1024, 1536, 16, 16, 64, 16, 16, 16, 16, 16, 4, 0, 16, 16, 16, 12, 2)
+    with pytest.raises(HipError, match="mmq_qkv_rope"):        # seq_stride is 0 or 1
+        call("q355_mmq_qkv_rope", 16, 16, 2048, 1536, 16, 16, 64, 16, 16, 16, 16, 16, 4, 2, 16, 16, 16, 12, 2)
 
 
 CFG_S = QM.Config(L=2, V=4096)
