@@ -448,6 +448,13 @@ static int launch_mmq_r_tg(const GemvArgs& a, hipStream_t s) {
     hipLaunchKernelGGL((k_mmq_r<TG, 5, 8, 6, EPI, XF32>), dim3(a.N / 80), dim3(512), 0, s, a);
     return launched("mmq");
   }
+  if constexpr (EPI == EPI_QKV && !XF32) {
+    // one writer per output (no K split): 16-row workgroups of 8 waves x 6 blocks, bias + RoPE + K/V write
+    // in the epilogue (a RoPE pair sits in adjacent rows of one tile)
+    if (a.N % 16 || nb > 8 * 6) return -1;
+    hipLaunchKernelGGL((k_mmq_r<TG, 1, 8, 6, EPI, XF32>), dim3(a.N / 16), dim3(512), 0, s, a);
+    return launched("mmq");
+  }
   if constexpr (EPI == EPI_RESID_FIX && XF32) {
     if (a.N % 64) return -1;
     if (nb >= 64) {
@@ -660,8 +667,9 @@ extern "C" int q355_qkv_finish(int64_t* acc, const float* bias, const float* rop
   return launched("qkv_finish");
 }
 
-// QKV product of the prefill with the finish fused into the LDS-tiled kernel's epilogue: every output has one
-// writer (no K split), so no int64 accumulator, no second launch.
+// QKV product with the finish fused into its epilogue: every output has one writer (no K split), so no int64
+// accumulator and no second launch. Decode batches (T <= 32, K <= 1536) run the register-resident kernel,
+// larger T the LDS-tiled one.
 extern "C" int q355_mmq_qkv_rope(const uint8_t* qs, const void* d, int N, int K, const int8_t* xq, const void* xds,
                                  int T, const float* bias, const float* rope_cos, const float* rope_sin,
                                  const int32_t* pos, const int32_t* block_table, int bt_stride, int seq_stride,
@@ -678,6 +686,11 @@ extern "C" int q355_mmq_qkv_rope(const uint8_t* qs, const void* d, int N, int K,
   a.aux = bias; a.rope_cos = rope_cos; a.rope_sin = rope_sin; a.pos = pos; a.block_table = block_table;
   a.bt_stride = bt_stride; a.seq_stride = seq_stride;
   a.kcache = (__half*)kcache; a.vcache = (__half*)vcache; a.qout = (__half*)qout; a.nh = nh; a.nkv = nkv;
+  if (T <= 32) {                                     // decode batches: register-resident, all tokens per workgroup
+    const int r = T <= 16 ? launch_mmq_r_tg<1, EPI_QKV, false>(a, (hipStream_t)stream)
+                          : launch_mmq_r_tg<2, EPI_QKV, false>(a, (hipStream_t)stream);
+    if (r >= 0) return r;
+  }
   return launch_mmq_big<EPI_QKV>(a, (hipStream_t)stream);
 }
 

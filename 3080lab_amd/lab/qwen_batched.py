@@ -157,10 +157,10 @@ class BatchedDecoder:
         m, c, B = self.m, self.cfg, self.B
         L = m.layers[i]
         self._norm(L["ln1"])
-        self._mmq(L["qkv"], self.xq, self.xds, 6, yfix=self.qkv_acc)
-        call("q355_qkv_finish", ptr(self.qkv_acc), ptr(L["qkv_b"]), ptr(m.cos), ptr(m.sin), ptr(self.pos),
-             ptr(self.block_table), self.max_chunks, 1, ptr(self.kc[i]), ptr(self.vc[i]), ptr(self.q),
-             c.NH, c.NKV, B)
+        W = L["qkv"]                 # bias, RoPE and the K/V write in the product's epilogue
+        call("q355_mmq_qkv_rope", ptr(W.qs), ptr(W.d), W.N, W.K, ptr(self.xq), ptr(self.xds), B, ptr(L["qkv_b"]),
+             ptr(m.cos), ptr(m.sin), ptr(self.pos), ptr(self.block_table), self.max_chunks, 1, ptr(self.kc[i]),
+             ptr(self.vc[i]), ptr(self.q), c.NH, c.NKV)
         call("q355_attn_decode", ptr(self.q), ptr(self.kc[i]), ptr(self.vc[i]), ptr(self.pos), ptr(self.block_table),
              self.max_chunks, c.NH, c.NKV, self.max_chunks, self.scale, ptr(self.part), ptr(self.aq), ptr(self.ads),
              None, B, 1)

@@ -191,8 +191,8 @@ int q355_qkv_finish(int64_t* acc, const float* bias, const float* rope_cos, cons
                     const int32_t* pos, const int32_t* block_table, int bt_stride, int seq_stride, void* kcache,
                     void* vcache, void* qout, int nh, int nkv, int T, void* stream);
 
-/* Prefill QKV: Q4_0 x Q8_1 product of T tokens on the LDS-tiled int8 MFMA kernel with the QKV finish in its
- * epilogue: + bias, RoPE, fp16 q out [T][nh*128], fp16 K/V cache rows at pos[j] of sequence j * seq_stride
+/* QKV: Q4_0 x Q8_1 product of T tokens on int8 MFMA (register-resident for T <= 32 and K <= 1536, LDS-tiled
+ * otherwise) with the QKV finish in its epilogue: + bias, RoPE, fp16 q out [T][nh*128], fp16 K/V cache rows at pos[j] of sequence j * seq_stride
  * (arguments as q355_qkv_finish). N = (nh + 2 nkv) * 128 in the device row order, N % 128 == 0.
  * Replaces gemm_q4i8_ms_source with the 'biasf_kv' epilogue (lab/qwen_batched.py:1271-1561, 1316-1362). */
 int q355_mmq_qkv_rope(const uint8_t* qs, const void* d, int N, int K, const int8_t* xq, const void* xds, int T,

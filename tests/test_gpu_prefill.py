@@ -153,13 +153,15 @@ def test_prefill_chunked_equals_one_chunk(small):
         assert int(a.tok.item()) == int(b.tok.item())
 
 
-def test_mmq_qkv_rope_equals_finish(cuda):
-    """The QKV product with the finish in the tiled kernel's epilogue writes the same q and K/V cache rows as
-    the K-split product into the int64 accumulator followed by q355_qkv_finish (both round once from f64)."""
+@pytest.mark.parametrize("T,seq_stride", [(1100, 0), (8, 1), (32, 1), (5, 1), (20, 1)])
+def test_mmq_qkv_rope_equals_finish(cuda, T, seq_stride):
+    """The QKV product with the finish in its epilogue (tiled kernel for a prefill chunk, register-resident for
+    decode batches of one token per sequence) writes the same q and K/V cache rows as the K-split product into
+    the int64 accumulator followed by q355_qkv_finish (both round once from f64)."""
     import torch
     c = QM.Config(L=1, V=1024)
-    N, K, T, pos0 = c.nqkv, c.H, 1100, 37
-    rng = np.random.default_rng(11)
+    N, K = c.nqkv, c.H
+    rng = np.random.default_rng(11 + T)
     from lab import gguf
     W = QM.Q4Mat(gguf.quantize_q4_0(rng.standard_normal((N, K), dtype=np.float32) * np.float32(0.02)), N, K, "cuda")
     x = torch.from_numpy(rng.standard_normal((T, K), dtype=np.float32)).cuda()
@@ -171,9 +173,17 @@ def test_mmq_qkv_rope_equals_finish(cuda):
     ang = np.arange(maxlen)[:, None] * (1e6 ** (-np.arange(64) * 2 / 128))[None, :]
     cos = torch.from_numpy(np.cos(ang).astype(np.float32)).cuda()
     sin = torch.from_numpy(np.sin(ang).astype(np.float32)).cuda()
-    pos = torch.arange(pos0, pos0 + T, dtype=torch.int32, device=cuda)
-    n_pages = maxlen // 64
-    table = torch.from_numpy(rng.permutation(n_pages).astype(np.int32)).cuda()
+    if seq_stride == 0:                                       # one sequence, positions 37 .. 37 + T - 1
+        pos_np = np.arange(37, 37 + T, dtype=np.int32)
+        bt_stride = n_pages = maxlen // 64
+        table_np = rng.permutation(n_pages).astype(np.int32)
+    else:                                                     # one token per sequence, scattered pages
+        bt_stride = 8
+        n_pages = T * bt_stride
+        pos_np = rng.integers(0, bt_stride * 64, T).astype(np.int32)
+        table_np = rng.permutation(n_pages).astype(np.int32).reshape(T, bt_stride)
+    pos = torch.from_numpy(pos_np).cuda()
+    table = torch.from_numpy(table_np).cuda()
     outs = []
     for fused in (True, False):
         kc = torch.zeros(n_pages, c.NKV, 64, 128, dtype=torch.float16, device=cuda)
@@ -181,24 +191,24 @@ def test_mmq_qkv_rope_equals_finish(cuda):
         q = torch.zeros(T, c.NH * 128, dtype=torch.float16, device=cuda)
         if fused:
             call("q355_mmq_qkv_rope", ptr(W.qs), ptr(W.d), N, K, ptr(xq), ptr(xds), T, ptr(bias), ptr(cos), ptr(sin),
-                 ptr(pos), ptr(table), n_pages, 0, ptr(kc), ptr(vc), ptr(q), c.NH, c.NKV)
+                 ptr(pos), ptr(table), bt_stride, seq_stride, ptr(kc), ptr(vc), ptr(q), c.NH, c.NKV)
         else:
             acc = torch.zeros(T, N, dtype=torch.int64, device=cuda)
             call("q355_mmq_q4_0_q8_1", ptr(W.qs), ptr(W.d), N, K, ptr(xq), ptr(xds), T, 6, None, ptr(acc),
                  None, None, None, None)
-            call("q355_qkv_finish", ptr(acc), ptr(bias), ptr(cos), ptr(sin), ptr(pos), ptr(table), n_pages, 0,
-                 ptr(kc), ptr(vc), ptr(q), c.NH, c.NKV, T)
+            call("q355_qkv_finish", ptr(acc), ptr(bias), ptr(cos), ptr(sin), ptr(pos), ptr(table), bt_stride,
+                 seq_stride, ptr(kc), ptr(vc), ptr(q), c.NH, c.NKV, T)
         torch.cuda.synchronize()
         outs.append([t.cpu().numpy() for t in (q, kc, vc)])
     for a, b in zip(*outs):
         ulp = np.abs(a.view(np.int16).astype(np.int32) - b.view(np.int16).astype(np.int32))
         assert ulp.max() <= 1 and (ulp > 0).mean() < 1e-3
-    # every cache row of positions pos0 .. pos0 + T - 1 was written (none of the untouched rows)
-    kc = outs[0][1]
-    rows = np.abs(kc).sum(axis=(1, 3)) > 0                 # [page, slot]
+    # exactly the cache rows of the T (sequence, position) pairs were written
+    rows = np.abs(outs[0][1]).sum(axis=(1, 3)) > 0                 # [page, slot]
     want = np.zeros_like(rows)
-    for p in range(pos0, pos0 + T):
-        want[table.cpu().numpy()[p // 64], p % 64] = True
+    for j, p in enumerate(pos_np):
+        pg = table_np[p // 64] if seq_stride == 0 else table_np[j, p // 64]
+        want[pg, p % 64] = True
     assert np.array_equal(rows, want)
 
 
