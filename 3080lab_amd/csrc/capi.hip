@@ -571,6 +571,11 @@ static int launch_gemm_f16(GemvArgs a, int KS, hipStream_t s) {
 template <int TG, int EPI>
 static int launch_gemm_f16r_tg(const GemvArgs& a, hipStream_t s) {
   const int nb = a.K / 32;
+  if constexpr (EPI == EPI_QKV) {                    // no K split: 16-row workgroups, finish in the epilogue
+    if (a.N % 16 || nb > 8 * 6) return -1;
+    hipLaunchKernelGGL((k_gemm_f16r<TG, 1, 8, 6, EPI>), dim3(a.N / 16), dim3(512), 0, s, a);
+    return launched("gemm_f16");
+  }
   if (EPI == EPI_RESID_FIX) {
     if (a.N % 64) return -1;
     if (nb >= 64) {                                  // long K (down): 8 waves x 4 blocks per slice
@@ -641,6 +646,27 @@ extern "C" int q355_gemm_q4_0_f16(const uint8_t* qs, const void* d, int N, int K
     default:
       return fail(Q355_EINVAL, "gemm_q4_0_f16: epi=%d (0 store, 5 logits, 6 resid_fix, 8 swiglu_f16)", epi);
   }
+}
+
+// QKV of the fp16 batched path (T <= 32) with bias, RoPE and the K/V write in the product's epilogue.
+extern "C" int q355_gemm_f16_qkv_rope(const uint8_t* qs, const void* d, int N, int K, const void* xh, int T,
+                                     const float* bias, const float* rope_cos, const float* rope_sin,
+                                     const int32_t* pos, const int32_t* block_table, int bt_stride, int seq_stride,
+                                     void* kcache, void* vcache, void* qout, int nh, int nkv, void* stream) {
+  if (int e = check_mat("gemm_f16_qkv_rope", qs, d, N, K)) return e;
+  REQUIRE(xh && bias && rope_cos && rope_sin && pos && block_table && kcache && vcache && qout,
+          "gemm_f16_qkv_rope: null pointer");
+  REQUIRE(nh > 0 && nkv > 0 && N == (nh + 2 * nkv) * HD, "gemm_f16_qkv_rope: N=%d must be (nh + 2 nkv) * 128", N);
+  REQUIRE(T >= 1 && T <= 32 && K <= 1536 && bt_stride > 0 && (seq_stride == 0 || seq_stride == 1),
+          "gemm_f16_qkv_rope: T=%d K=%d bt_stride=%d seq_stride=%d (T <= 32, K <= 1536)", T, K, bt_stride, seq_stride);
+  GemvArgs a = {};
+  a.qs = qs; a.d = (const __half*)d; a.N = N; a.K = K; a.T = T; a.xh = (const __half*)xh;
+  a.aux = bias; a.rope_cos = rope_cos; a.rope_sin = rope_sin; a.pos = pos; a.block_table = block_table;
+  a.bt_stride = bt_stride; a.seq_stride = seq_stride;
+  a.kcache = (__half*)kcache; a.vcache = (__half*)vcache; a.qout = (__half*)qout; a.nh = nh; a.nkv = nkv;
+  const int r = T <= 16 ? launch_gemm_f16r_tg<1, EPI_QKV>(a, (hipStream_t)stream)
+                        : launch_gemm_f16r_tg<2, EPI_QKV>(a, (hipStream_t)stream);
+  return r >= 0 ? r : fail(Q355_EINVAL, "gemm_f16_qkv_rope: unsupported shape N=%d K=%d", N, K);
 }
 
 extern "C" int q355_rmsnorm_fix_f16(const int64_t* h, const float* w, void* xh, int T, int H, double eps,

@@ -52,6 +52,8 @@ _SIGS = {
     "q355_qkv_finish": [_P, _P, _P, _P, _P, _P, c_int, c_int, _P, _P, _P, c_int, c_int, c_int, _P],
     "q355_mmq_qkv_rope": [_P, _P, c_int, c_int, _P, _P, c_int, _P, _P, _P, _P, _P, c_int, c_int, _P, _P, _P, c_int,
                           c_int, _P],
+    "q355_gemm_f16_qkv_rope": [_P, _P, c_int, c_int, _P, c_int, _P, _P, _P, _P, _P, c_int, c_int, _P, _P, _P,
+                               c_int, c_int, _P],
 }
 # entry points returning something other than an int status
 _VALUE_FUNCS = {"q355_head_nparts", "q355_mmq_nparts", "q355_mega_ws_bytes", "q355_mega_layer_bytes",

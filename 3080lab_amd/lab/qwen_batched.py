@@ -98,7 +98,6 @@ class BatchedDecoder:
         self.xds = torch.zeros(B, max(H, c.FFN) // 32, 2, dtype=torch.float16, device=dev)
         self.mq = torch.zeros(B, c.FFN, dtype=torch.int8, device=dev)
         self.mds = torch.zeros(B, c.FFN // 32, 2, dtype=torch.float16, device=dev)
-        self.qkv_acc = torch.zeros(B, c.nqkv, dtype=torch.int64, device=dev)
         self.q = torch.zeros(B, c.NH * c.HD, dtype=torch.float16, device=dev)
         self.part = torch.zeros(B, c.NH, self.max_chunks, c.HD + 2, dtype=torch.float64, device=dev)
         self.aq = torch.zeros(B, c.NH * c.HD, dtype=torch.int8, device=dev)
@@ -139,10 +138,10 @@ class BatchedDecoder:
         m, c, B = self.m, self.cfg, self.B
         L = m.layers[i]
         self._normh(L["ln1"])
-        self._gemm(L["qkv"], self.xh, 6, yfix=self.qkv_acc)
-        call("q355_qkv_finish", ptr(self.qkv_acc), ptr(L["qkv_b"]), ptr(m.cos), ptr(m.sin), ptr(self.pos),
-             ptr(self.block_table), self.max_chunks, 1, ptr(self.kc[i]), ptr(self.vc[i]), ptr(self.q),
-             c.NH, c.NKV, B)
+        W = L["qkv"]                 # bias, RoPE and the K/V write in the product's epilogue
+        call("q355_gemm_f16_qkv_rope", ptr(W.qs), ptr(W.d), W.N, W.K, ptr(self.xh), B, ptr(L["qkv_b"]), ptr(m.cos),
+             ptr(m.sin), ptr(self.pos), ptr(self.block_table), self.max_chunks, 1, ptr(self.kc[i]), ptr(self.vc[i]),
+             ptr(self.q), c.NH, c.NKV)
         call("q355_attn_decode_f16", ptr(self.q), ptr(self.kc[i]), ptr(self.vc[i]), ptr(self.pos),
              ptr(self.block_table), self.max_chunks, c.NH, c.NKV, self.max_chunks, self.scale, ptr(self.part),
              ptr(self.ah), B)

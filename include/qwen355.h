@@ -184,6 +184,14 @@ int q355_attn_decode_f16(const void* q, const void* kcache, const void* vcache, 
                          const int32_t* block_table, int bt_stride, int nh, int nkv, int max_chunks, double scale,
                          double* part, void* oh, int T, void* stream);
 
+/* QKV of the fp16 batched path: Q4_0 x fp16 activations xh [T][K] on fp16 MFMA (T <= 32, K <= 1536) with bias,
+ * RoPE and the K/V cache write in the epilogue (arguments otherwise as q355_mmq_qkv_rope).
+ * Replaces gemv_v2_source with the 'biasf_kv' epilogue (lab/qwen_batched.py:467-680, 1316-1362). */
+int q355_gemm_f16_qkv_rope(const uint8_t* qs, const void* d, int N, int K, const void* xh, int T, const float* bias,
+                           const float* rope_cos, const float* rope_sin, const int32_t* pos, const int32_t* block_table,
+                           int bt_stride, int seq_stride, void* kcache, void* vcache, void* qout, int nh, int nkv,
+                           void* stream);
+
 /* QKV epilogue of the MFMA path: acc int64 fixed point [T][nqkv] (device row order) -> + bias, RoPE, fp16
  * q out [T][nh*128], fp16 K/V cache rows at pos[j] of sequence j * seq_stride; acc is zeroed.
  * Replaces 'biasf_kv' (lab/qwen_batched.py:1316-1362) and the RoPE/KV-write head of ATTN4. */

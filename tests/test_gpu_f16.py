@@ -162,3 +162,45 @@ def test_attn_decode_f16(cuda, positions):
         V = np.concatenate([vc[bt[j, p]] for p in range(max_chunks)], axis=1)
         ref = OM.attn_decode(q[j].reshape(c.NH, c.HD), K, V, int(pos[j]) + 1, c.NH, c.NKV)
         assert relerr(oh[j].float().cpu().numpy(), ref) < 2e-3   # fp16 P on the matrix cores, fp16 output
+
+
+@pytest.mark.parametrize("T", [5, 8, 20, 32])
+def test_gemm_f16_qkv_rope_equals_finish(cuda, T):
+    """QKV with bias, RoPE and the K/V write in the fp16 product's epilogue equals the K-split product into the
+    int64 accumulator followed by q355_qkv_finish (one token per sequence, scattered pages)."""
+    import torch
+    c = QM.Config(L=1, V=1024)
+    N, K = c.nqkv, c.H
+    W, _ = mat(N, K, 40 + T)
+    rng = np.random.default_rng(T)
+    x = dev(acts(T, K, T + 1))
+    bias = dev(rng.standard_normal(N).astype(np.float32))
+    maxlen, bt_stride = 1024, 8
+    ang = np.arange(maxlen)[:, None] * (1e6 ** (-np.arange(64) * 2 / 128))[None, :]
+    cos, sin = dev(np.cos(ang).astype(np.float32)), dev(np.sin(ang).astype(np.float32))
+    pos = dev(rng.integers(0, bt_stride * 64, T).astype(np.int32))
+    table = dev(rng.permutation(T * bt_stride).astype(np.int32).reshape(T, bt_stride))
+    outs = []
+    for fused in (True, False):
+        kc = torch.zeros(T * bt_stride, c.NKV, 64, 128, dtype=torch.float16, device=cuda)
+        vc = torch.zeros_like(kc)
+        q = torch.zeros(T, c.NH * 128, dtype=torch.float16, device=cuda)
+        if fused:
+            call("q355_gemm_f16_qkv_rope", ptr(W.qs), ptr(W.d), N, K, ptr(x), T, ptr(bias), ptr(cos), ptr(sin),
+                 ptr(pos), ptr(table), bt_stride, 1, ptr(kc), ptr(vc), ptr(q), c.NH, c.NKV)
+        else:
+            acc = torch.zeros(T, N, dtype=torch.int64, device=cuda)
+            call("q355_gemm_q4_0_f16", ptr(W.qs), ptr(W.d), N, K, ptr(x), T, 6, None, ptr(acc), None, None, None)
+            call("q355_qkv_finish", ptr(acc), ptr(bias), ptr(cos), ptr(sin), ptr(pos), ptr(table), bt_stride, 1,
+                 ptr(kc), ptr(vc), ptr(q), c.NH, c.NKV, T)
+        sync()
+        outs.append([t.cpu().numpy() for t in (q, kc, vc)])
+    # the fused product sums all of K in one fp32 accumulator, the split one in K slices: the fp32 sums differ
+    # in their last bits, so an fp16 output may round one or two ulps apart
+    for a, b in zip(*outs):
+        ulp = np.abs(a.view(np.int16).astype(np.int32) - b.view(np.int16).astype(np.int32))
+        assert ulp.max() <= 2 and (ulp > 0).mean() < 1e-3
+        assert relerr(a.astype(np.float32), b.astype(np.float32)) < 2e-3
+    with pytest.raises(HipError, match="T <= 32"):
+        call("q355_gemm_f16_qkv_rope", ptr(W.qs), ptr(W.d), N, K, ptr(x), 33, ptr(bias), ptr(cos), ptr(sin),
+             ptr(pos), ptr(table), bt_stride, 1, ptr(kc), ptr(vc), ptr(q), c.NH, c.NKV)

@@ -152,11 +152,13 @@ def test_qkv_finish_matches_fused_epilogue(cuda):
          ptr(dm.cos), ptr(dm.sin), ptr(a.pos), ptr(a.block_table), a.max_chunks, 1, ptr(a.kc[0]), ptr(a.vc[0]), ptr(a.q),
          cfg.NH, cfg.NKV, T)
     b._norm(L["ln1"])
-    b._mmq(L["qkv"], b.xq, b.xds, 6, yfix=b.qkv_acc)
-    call("q355_qkv_finish", ptr(b.qkv_acc), ptr(L["qkv_b"]), ptr(dm.cos), ptr(dm.sin), ptr(b.pos), ptr(b.block_table),
+    import torch
+    acc = torch.zeros(T, cfg.nqkv, dtype=torch.int64, device=cuda)
+    b._mmq(L["qkv"], b.xq, b.xds, 6, yfix=acc)
+    call("q355_qkv_finish", ptr(acc), ptr(L["qkv_b"]), ptr(dm.cos), ptr(dm.sin), ptr(b.pos), ptr(b.block_table),
          b.max_chunks, 1, ptr(b.kc[0]), ptr(b.vc[0]), ptr(b.q), cfg.NH, cfg.NKV, T)
     sync()
-    assert int(b.qkv_acc.abs().sum()) == 0
+    assert int(acc.abs().sum()) == 0
     assert relerr(b.q.float().cpu().numpy(), a.q.float().cpu().numpy()) < 2e-3
     for j in range(T):
         p = int(pos[j])
