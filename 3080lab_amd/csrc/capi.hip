@@ -481,8 +481,10 @@ static int launch_mmq_tg(const GemvArgs& a, int KS, hipStream_t s) {
   }
   if constexpr (EPI == EPI_LOGITS)
     if (a.N % 128 == 0 && a.N >= 128 * 256 && a.T <= 64) return launch_mmq_logits_tile(a, s);
+  // prefill sizes: the LDS-tiled kernel; from 512 tokens on always, so a prompt split into chunks of >= 512
+  // tokens computes every row with the same kernel (and the same summation order) as one chunk
   if constexpr (EPI == EPI_STORE || EPI == EPI_RESID_FIX || EPI == EPI_SWIGLU_Q8)
-    if (a.N % 128 == 0 && (a.N / 128) * ((a.T + 63) / 64) >= 256) return launch_mmq_big<EPI>(a, s);
+    if (a.N % 128 == 0 && (a.T >= 512 || (a.N / 128) * ((a.T + 63) / 64) >= 256)) return launch_mmq_big<EPI>(a, s);
   // up to 64 tokens (decode batches): 16-token workgroups, several per CU, hide each other's latencies;
   // prefill sizes: 32- or 64-token workgroups reuse every staged weight block 2 or 4 times
   if (a.T <= 64) return launch_mmq<1, EPI>(a, KS, s);

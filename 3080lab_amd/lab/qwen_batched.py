@@ -245,9 +245,10 @@ def flash_prefill_v3_source(maxlen: int = 4096, q8: bool = True) -> KernelSpec:
 
 
 # chunks of at least this many tokens run the QKV product on the LDS-tiled kernel with the finish in its
-# epilogue (q355_mmq_qkv_rope: 16 x ceil(P / 64) workgroups); shorter ones keep the K-split product into the
-# int64 accumulator plus q355_qkv_finish, which has parallelism enough at small P
-QKV_FUSED_MIN_P = 1024
+# epilogue (q355_mmq_qkv_rope); shorter ones keep the K-split product into the int64 accumulator plus
+# q355_qkv_finish, which has parallelism enough at small P. From 512 tokens on every product of a chunk runs
+# the LDS-tiled kernel, so chunking a prompt into pieces of >= 512 tokens gives the same results bit for bit.
+QKV_FUSED_MIN_P = 512
 
 
 class Prefill:
