@@ -123,7 +123,9 @@ __global__ void __launch_bounds__(NW * 64) k_mmq_r(const GemvArgs a) {
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int li = lane & 15, lg = lane >> 4;
   const int tile0 = blockIdx.x * NT;
-  uint2 w[KPW][NT], dv[KPW][NT];
+  constexpr int NQ = (NT + 3) / 4;                      // 4-tile groups of the scale outer products
+  uint2 w[KPW][NT];
+  float dwl[KPW][NQ];                                   // d_w of row li of tile 4 q + lg (0 past NT)
   long xb[KPW][TG];
   float dx[KPW][TG];
   float4 xr[XF32 ? KPW : 1][XF32 ? TG : 1][2];
@@ -134,7 +136,11 @@ __global__ void __launch_bounds__(NW * 64) k_mmq_r(const GemvArgs a) {
     for (int t = 0; t < NT; ++t) {
       const size_t base = ((size_t)(tile0 + t) * nb + b) * 16;
       w[i][t] = ((const uint2*)a.qs)[(base + li) * 2 + (lg & 1)];
-      dv[i][t] = ((const uint2*)a.d)[(base >> 2) + lg];
+    }
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+      const int t = 4 * q + lg;
+      dwl[i][q] = t < NT ? __half2float(a.d[((size_t)(tile0 + t) * nb + b) * 16 + li]) : 0.f;
     }
 #pragma unroll
     for (int g = 0; g < TG; ++g) {
@@ -179,14 +185,19 @@ __global__ void __launch_bounds__(NW * 64) k_mmq_r(const GemvArgs a) {
 #pragma unroll
         for (int g = 0; g < TG; ++g) c[t][g] = __builtin_amdgcn_mfma_i32_16x16x32_i8(wa, xb[i][g], zero, 0, 0, 0);
       }
+      // d_w d_x of every output from 4-block outer products on the matrix cores (lane 16 b + r: d_w of row r
+      // of tile 4 q + b; lane l receives d_w[tile][4 lg + v] d_x[token li] in register 4 (tile % 4) + v)
 #pragma unroll
-      for (int t = 0; t < NT; ++t) {
-        const __half2 d01 = *(const __half2*)&dv[i][t].x, d23 = *(const __half2*)&dv[i][t].y;
-        const float dw[4] = {__low2float(d01), __high2float(d01), __low2float(d23), __high2float(d23)};
+      for (int g = 0; g < TG; ++g) {
+        const v16f zf = {};
+        v16f sc[NQ];
 #pragma unroll
-        for (int g = 0; g < TG; ++g)
+        for (int q = 0; q < NQ; ++q) sc[q] = __builtin_amdgcn_mfma_f32_16x16x1f32(dwl[i][q], dx[i][g], zf, 0, 0, 0);
 #pragma unroll
-          for (int v = 0; v < 4; ++v) acc[t][g][v] = fmaf(dw[v] * dx[i][g], (float)c[t][g][v], acc[t][g][v]);
+        for (int t = 0; t < NT; ++t)
+#pragma unroll
+          for (int v = 0; v < 4; ++v)
+            acc[t][g][v] = fmaf(sc[t >> 2][4 * (t & 3) + v], (float)c[t][g][v], acc[t][g][v]);
       }
     }
   }
