@@ -39,9 +39,12 @@ constexpr int TILE_CB = 4;                           // K blocks per LDS chunk
 // any of their results is scaled, so the matrix-core latency overlaps instead of stalling each product.
 // Weights enter as 16 (q - 8) (snib8) and xd holds d_x / 16, so d_w xd (16 dot') = d_w d_x (dot - 8 sum q_x)
 // exactly, with no activation sums.
+// dwl[q]: d_w of row li of tile 4 q + lg (0 past NT); the d_w d_x products of all outputs come from 4-block
+// outer products on the matrix cores (lane l receives d_w[tile][4 lg + v] d_x[token li] in register
+// 4 (tile % 4) + v).
 template <int NT, int TG>
-__device__ __forceinline__ void mmq_block(const uint2 (&w)[NT], const uint2 (&dv)[NT], const int8_t* __restrict__ xq, int xstride,
-                                          const float* xd, int ld, int bb, int li, int lg, float (&acc)[NT][TG][4]) {
+__device__ __forceinline__ void mmq_block(const uint2 (&w)[NT], const float (&dwl)[(NT + 3) / 4], const int8_t* __restrict__ xq,
+                                          int xstride, const float* xd, int ld, int bb, int li, int lg, float (&acc)[NT][TG][4]) {
   v4i c[NT][TG];
   float dx[TG];
   const v4i zero = {0, 0, 0, 0};
@@ -55,13 +58,15 @@ __device__ __forceinline__ void mmq_block(const uint2 (&w)[NT], const uint2 (&dv
       c[t][g] = __builtin_amdgcn_mfma_i32_16x16x32_i8(snib8(w[t], lg), bx, zero, 0, 0, 0);
   }
 #pragma unroll
-  for (int t = 0; t < NT; ++t) {
-    const __half2 d01 = *(const __half2*)&dv[t].x, d23 = *(const __half2*)&dv[t].y;
-    const float dw[4] = {__low2float(d01), __high2float(d01), __low2float(d23), __high2float(d23)};
+  for (int g = 0; g < TG; ++g) {
+    const v16f zf = {};
+    v16f sc[(NT + 3) / 4];
 #pragma unroll
-    for (int g = 0; g < TG; ++g)
+    for (int q = 0; q < (NT + 3) / 4; ++q) sc[q] = __builtin_amdgcn_mfma_f32_16x16x1f32(dwl[q], dx[g], zf, 0, 0, 0);
 #pragma unroll
-      for (int v = 0; v < 4; ++v) acc[t][g][v] = fmaf(dw[v] * dx[g], (float)c[t][g][v], acc[t][g][v]);
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) acc[t][g][v] = fmaf(sc[t >> 2][4 * (t & 3) + v], (float)c[t][g][v], acc[t][g][v]);
   }
 }
 
@@ -229,15 +234,15 @@ __global__ void __launch_bounds__(NW * 64) k_mmq(const GemvArgs a) {
   const int tile0 = blockIdx.x * NT;
 
   const uint2* __restrict__ qs = (const uint2*)a.qs;
-  const uint2* __restrict__ dd = (const uint2*)a.d;   // 4 fp16 scales = rows 4*lg .. 4*lg+3
-  const uint2* wq[NT];                              // this lane's nibbles / scales of block 0, per tile
-  const uint2* wd[NT];
+  constexpr int NQ = (NT + 3) / 4;
+  const uint2* wq[NT];                              // this lane's nibbles of block 0, per tile
+  const __half* wd[NQ];                             // the scale of row li of tile 4 q + lg, block 0
 #pragma unroll
-  for (int t = 0; t < NT; ++t) {
-    wq[t] = qs + ((size_t)(tile0 + t) * nb * 16 + li) * 2 + (lg & 1);
-    wd[t] = dd + (size_t)(tile0 + t) * nb * 4 + lg;
-  }
-  uint2 wA[NT], dA[NT], wB[NT], dB[NT];
+  for (int t = 0; t < NT; ++t) wq[t] = qs + ((size_t)(tile0 + t) * nb * 16 + li) * 2 + (lg & 1);
+#pragma unroll
+  for (int q = 0; q < NQ; ++q) wd[q] = a.d + (size_t)(tile0 + min(4 * q + lg, NT - 1)) * nb * 16 + li;
+  uint2 wA[NT], wB[NT];
+  float dA[NQ], dB[NQ];
   float acc[NT][TG][4];
 #pragma unroll
   for (int t = 0; t < NT; ++t)
@@ -248,13 +253,12 @@ __global__ void __launch_bounds__(NW * 64) k_mmq(const GemvArgs a) {
 
   for (int c0 = ks.b0; c0 < ks.b1; c0 += ch) {      // chunks of the K slice
     const int nbc = min(ch, ks.b1 - c0);
-    auto load_blk = [&](int bb, uint2 (&w)[NT], uint2 (&dv)[NT]) {
+    auto load_blk = [&](int bb, uint2 (&w)[NT], float (&dv)[NQ]) {
       const int b = c0 + min(bb, nbc - 1);
 #pragma unroll
-      for (int t = 0; t < NT; ++t) {
-        w[t] = wq[t][b * 32];
-        dv[t] = wd[t][b * 4];
-      }
+      for (int t = 0; t < NT; ++t) w[t] = wq[t][b * 32];
+#pragma unroll
+      for (int q = 0; q < NQ; ++q) dv[q] = 4 * q + lg < NT ? __half2float(wd[q][b * 16]) : 0.f;
     };
     load_blk(wv, wA, dA);                           // first weights of the chunk before the staging
     if (c0 != ks.b0) __syncthreads();               // previous chunk's LDS reads are done
@@ -262,7 +266,7 @@ __global__ void __launch_bounds__(NW * 64) k_mmq(const GemvArgs a) {
     __syncthreads();
     Q355_TRACE_POINT(1);
 
-    auto compute_blk = [&](int bb, const uint2 (&w)[NT], const uint2 (&dv)[NT]) {
+    auto compute_blk = [&](int bb, const uint2 (&w)[NT], const float (&dv)[NQ]) {
       mmq_block<NT, TG>(w, dv, xq, xstride, xd, ch, bb, li, lg, acc);
     };
     // 2-deep pipeline over this wave's blocks wv, wv + NW, ... of the chunk
@@ -356,9 +360,10 @@ __global__ void __launch_bounds__(NW * 64) k_mmq_reg(const GemvArgs a) {
   for (int i = 0; i < KPW; ++i) {
     const int bb = wv + NW * i;
     if (bb < nbs) {                                     // uniform per wave
-      uint2 dv[NT];
+      float dv[(NT + 3) / 4];                           // wsc as fp16 [NT][nbs][16 rows]
 #pragma unroll
-      for (int t = 0; t < NT; ++t) dv[t] = wsc[(t * nbs + bb) * 4 + lg];
+      for (int q = 0; q < (NT + 3) / 4; ++q)
+        dv[q] = 4 * q + lg < NT ? __half2float(((const __half*)wsc)[((4 * q + lg) * nbs + bb) * 16 + li]) : 0.f;
       mmq_block<NT, TG>(w[i], dv, xq, xstride, xd, nbs, bb, li, lg, acc);
     }
   }
