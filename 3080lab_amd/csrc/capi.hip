@@ -577,32 +577,33 @@ static int launch_gemm_f16r_tg(const GemvArgs& a, hipStream_t s) {
     if (a.N % 16 || nb > 8 * 6) return -1;
     hipLaunchKernelGGL((k_gemm_f16r<TG, 1, 8, 6, EPI>), dim3(a.N / 16), dim3(512), 0, s, a);
     return launched("gemm_f16");
-  }
-  if (EPI == EPI_RESID_FIX) {
-    if (a.N % 64) return -1;
-    if (nb >= 64) {                                  // long K (down): 8 waves x 4 blocks per slice
-      const int KS = (nb + 31) / 32;
-      hipLaunchKernelGGL((k_gemm_f16r<TG, 4, 8, 4, EPI>), dim3(a.N / 64, KS), dim3(512), 0, s, a);
+  } else {
+    if (EPI == EPI_RESID_FIX) {
+      if (a.N % 64) return -1;
+      if (nb >= 64) {                                  // long K (down): 8 waves x 4 blocks per slice
+        const int KS = (nb + 31) / 32;
+        hipLaunchKernelGGL((k_gemm_f16r<TG, 4, 8, 4, EPI>), dim3(a.N / 64, KS), dim3(512), 0, s, a);
+        return launched("gemm_f16");
+      }
+      int KS = 1;
+      while ((a.N / 64) * KS < 256 && nb / (KS + 1) >= 4) ++KS;
+      while ((nb + KS - 1) / KS > 4 * 8) ++KS;
+      const int per = (nb + KS - 1) / KS;
+      const dim3 grid(a.N / 64, KS);
+      if (per <= 4 * 2) hipLaunchKernelGGL((k_gemm_f16r<TG, 4, 4, 2, EPI>), grid, dim3(256), 0, s, a);
+      else if (per <= 4 * 4) hipLaunchKernelGGL((k_gemm_f16r<TG, 4, 4, 4, EPI>), grid, dim3(256), 0, s, a);
+      else hipLaunchKernelGGL((k_gemm_f16r<TG, 4, 4, 8, EPI>), grid, dim3(256), 0, s, a);
       return launched("gemm_f16");
     }
-    int KS = 1;
-    while ((a.N / 64) * KS < 256 && nb / (KS + 1) >= 4) ++KS;
-    while ((nb + KS - 1) / KS > 4 * 8) ++KS;
-    const int per = (nb + KS - 1) / KS;
-    const dim3 grid(a.N / 64, KS);
-    if (per <= 4 * 2) hipLaunchKernelGGL((k_gemm_f16r<TG, 4, 4, 2, EPI>), grid, dim3(256), 0, s, a);
-    else if (per <= 4 * 4) hipLaunchKernelGGL((k_gemm_f16r<TG, 4, 4, 4, EPI>), grid, dim3(256), 0, s, a);
-    else hipLaunchKernelGGL((k_gemm_f16r<TG, 4, 4, 8, EPI>), grid, dim3(256), 0, s, a);
+    if (nb > 8 * 6) return -1;
+    if (a.N % 80 == 0 && a.N / 80 <= 256) {
+      hipLaunchKernelGGL((k_gemm_f16r<TG, 5, 8, 6, EPI>), dim3(a.N / 80), dim3(512), 0, s, a);
+    } else {
+      if (a.N % 64) return -1;
+      hipLaunchKernelGGL((k_gemm_f16r<TG, 4, 8, 6, EPI>), dim3(a.N / 64), dim3(512), 0, s, a);
+    }
     return launched("gemm_f16");
   }
-  if (nb > 8 * 6) return -1;
-  if (a.N % 80 == 0 && a.N / 80 <= 256) {
-    hipLaunchKernelGGL((k_gemm_f16r<TG, 5, 8, 6, EPI>), dim3(a.N / 80), dim3(512), 0, s, a);
-  } else {
-    if (a.N % 64) return -1;
-    hipLaunchKernelGGL((k_gemm_f16r<TG, 4, 8, 6, EPI>), dim3(a.N / 64), dim3(512), 0, s, a);
-  }
-  return launched("gemm_f16");
 }
 
 template <int EPI>

@@ -172,6 +172,11 @@ __global__ void __launch_bounds__(NW * 64) k_gemm_f16r(const GemvArgs a) {
       xb[i][g] = *(const fh8*)(a.xh + (size_t)tok * K + (size_t)b * 32 + 8 * lg);
     }
   }
+  QkvPre qp = {};
+  if constexpr (EPI == EPI_QKV) {
+    static_assert(NT * TT * 16 <= NW * 64, "one QKV output per thread");
+    qp = qkv_prefetch<TT, NT>(a, tile0);
+  }
   ff4 acc[NT][TG];
 #pragma unroll
   for (int t = 0; t < NT; ++t)
@@ -195,7 +200,8 @@ __global__ void __launch_bounds__(NW * 64) k_gemm_f16r(const GemvArgs a) {
 #pragma unroll
       for (int v = 0; v < 4; ++v) part[wv][t][16 * g + li][4 * lg + v] = acc[t][g][v];
   __syncthreads();
-  epilogue<NW, TT, NT, EPI>(a, part, tile0);
+  if constexpr (EPI == EPI_QKV) qkv_store<NW, TT, NT>(a, part, tile0, qp);
+  else epilogue<NW, TT, NT, EPI>(a, part, tile0);
 }
 
 }  // namespace q355

@@ -413,6 +413,60 @@ __device__ __forceinline__ void epilogue(const GemvArgs& a, A (&part)[NW][NT][T]
   }
 }
 
+// QKV epilogue whose per-element inputs (position, page id, RoPE cos/sin, the two biases) are loaded at kernel
+// start: their dependent loads (position -> page and table rows) overlap the products instead of following
+// the reduction. One output element per thread (NT * T * 16 <= blockDim.x); same f64 arithmetic as the
+// EPI_QKV branch of epilogue().
+struct QkvPre {
+  int t, j, r, pos, pg;
+  float c, s, b0, b1;
+  bool live;
+};
+
+template <int T, int NT>
+__device__ __forceinline__ QkvPre qkv_prefetch(const GemvArgs& a, int tile0) {
+  QkvPre q = {};
+  const int e = threadIdx.x;
+  q.t = e / (T * 16);
+  q.j = (e >> 4) % T;
+  q.r = e & 15;
+  q.live = e < NT * T * 16 && q.j < a.T;
+  if (!q.live) return q;
+  const int row = (tile0 + q.t) * 16 + q.r;
+  q.pos = a.pos[q.j];
+  q.pg = a.block_table[(size_t)((a.tok_base + q.j) * a.seq_stride) * a.bt_stride + q.pos / PAGE];
+  const int i = (row % HD) >> 1;
+  q.c = a.rope_cos[(size_t)q.pos * (HD / 2) + i];
+  q.s = a.rope_sin[(size_t)q.pos * (HD / 2) + i];
+  q.b0 = a.aux[row];
+  q.b1 = a.aux[row ^ 1];
+  return q;
+}
+
+template <int NW, int T, int NT, typename A>
+__device__ __forceinline__ void qkv_store(const GemvArgs& a, A (&part)[NW][NT][T][16], int tile0, const QkvPre& q) {
+  if (!q.live) return;
+  const int row = (tile0 + q.t) * 16 + q.r;
+  const int nq = a.nh * HD, nk = a.nkv * HD;
+  const double v = row_value<NW, T, NT>(part, q.t, q.j, q.r) + (double)q.b0;
+  if (row < nq + nk) {
+    const double v2 = row_value<NW, T, NT>(part, q.t, q.j, q.r ^ 1) + (double)q.b1;
+    const int e2 = row % HD, i = e2 >> 1, hi = e2 & 1;
+    const double c = q.c, s = q.s;
+    const double lo_v = hi ? v2 : v, hi_v = hi ? v : v2;
+    const double out = hi ? (hi_v * c + lo_v * s) : (lo_v * c - hi_v * s);
+    const int dim = i + (HD / 2) * hi;
+    if (row < nq) {
+      a.qout[(size_t)q.j * nq + (row / HD) * HD + dim] = half_rn(out);
+    } else {
+      a.kcache[(((size_t)q.pg * a.nkv + (row - nq) / HD) * PAGE + q.pos % PAGE) * HD + dim] = half_rn(out);
+    }
+  } else {
+    const int rv = row - nq - nk;
+    a.vcache[(((size_t)q.pg * a.nkv + rv / HD) * PAGE + q.pos % PAGE) * HD + rv % HD] = half_rn(v);
+  }
+}
+
 // ---------------------------------------------------------------------------------------------
 // The GEMV: T tokens (1..4), NT 16-row tiles per workgroup, NW waves splitting the K slice 4*NW ways,
 // KPL K-blocks per lane (compile time, so all weight loads are issued before the first use).

@@ -172,6 +172,11 @@ __global__ void __launch_bounds__(NW * 64) k_mmq_r(const GemvArgs a) {
         dx[i][g] = df * 0.0625f;
       }
   }
+  QkvPre qp = {};
+  if constexpr (EPI == EPI_QKV) {
+    static_assert(NT * TT * 16 <= NW * 64, "one QKV output per thread");
+    qp = qkv_prefetch<TT, NT>(a, tile0);
+  }
   float acc[NT][TG][4];
 #pragma unroll
   for (int t = 0; t < NT; ++t)
@@ -213,7 +218,8 @@ __global__ void __launch_bounds__(NW * 64) k_mmq_r(const GemvArgs a) {
 #pragma unroll
       for (int v = 0; v < 4; ++v) part[wv][t][16 * g + li][4 * lg + v] = acc[t][g][v];
   __syncthreads();
-  epilogue<NW, TT, NT, EPI>(a, part, tile0);
+  if constexpr (EPI == EPI_QKV) qkv_store<NW, TT, NT>(a, part, tile0, qp);
+  else epilogue<NW, TT, NT, EPI>(a, part, tile0);
 }
 
 template <int TG, int NT, int NW, int EPI>
