@@ -524,7 +524,7 @@ extern "C" int q355_mmq_q4_0_q8_1(const uint8_t* qs, const void* d, int N, int K
       a.oq = oq; a.ods = (half2*)ods;
       return launch_mmq_tg<EPI_SWIGLU_Q8>(a, 1, s);
     case 5:
-      REQUIRE(y && pmax && pidx, "mmq_q4_0_q8_1: logits needs y, pmax, pidx");
+      REQUIRE(pmax && pidx, "mmq_q4_0_q8_1: logits needs pmax, pidx (y optional)");
       a.y = y; a.pmax = pmax; a.pidx = pidx;
       return launch_mmq_tg<EPI_LOGITS>(a, 1, s);
     default:
@@ -631,7 +631,7 @@ extern "C" int q355_gemm_q4_0_f16(const uint8_t* qs, const void* d, int N, int K
       a.y = y;
       return launch_gemm_f16_tg<EPI_STORE>(a, 1, s);
     case 5:
-      REQUIRE(y && pmax && pidx, "gemm_q4_0_f16: logits needs y, pmax, pidx");
+      REQUIRE(pmax && pidx, "gemm_q4_0_f16: logits needs pmax, pidx (y optional)");
       a.y = y; a.pmax = pmax; a.pidx = pidx;
       return launch_gemm_f16_tg<EPI_LOGITS>(a, 1, s);
     case 6: {

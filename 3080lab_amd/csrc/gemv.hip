@@ -303,7 +303,7 @@ __device__ __forceinline__ void epilogue(const GemvArgs& a, A (&part)[NW][NT][T]
         int idx = 0x7fffffff;
         for (int rr = l; rr < NT * 16; rr += 64) {   // rows in increasing order: strict '>' keeps the lowest
           const float x = (float)row_value<NW, T, NT>(part, rr >> 4, j, rr & 15);
-          a.y[(size_t)j * N + tile0 * 16 + rr] = x;
+          if (a.y) a.y[(size_t)j * N + tile0 * 16 + rr] = x;   // optional fp32 logits
           if (x > v) { v = x; idx = tile0 * 16 + rr; }
         }
 #pragma unroll

@@ -584,7 +584,7 @@ __global__ void __launch_bounds__(256) k_mmq_tile(const GemvArgs a) {
       int bi = 0x7fffffff;
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
-        if (ok)
+        if (ok && a.y)                                   // fp32 logits are optional: the argmax needs only partials
           *(float4*)(a.y + (size_t)tok * N + (rt0 + t) * 16 + 4 * lg) =
               make_float4(acc[t][g][0], acc[t][g][1], acc[t][g][2], acc[t][g][3]);
 #pragma unroll

@@ -74,10 +74,14 @@ class BatchedDecoder:
     sequences in a seeded random order (the block table is a permutation), so the kernels are exercised
     on non-contiguous pages."""
 
-    def __init__(self, m: DeviceModel, B: int, max_ctx: int, page_seed: int = 0, act: str = "q8"):
+    def __init__(self, m: DeviceModel, B: int, max_ctx: int, page_seed: int = 0, act: str = "q8",
+                 keep_logits: bool = False):
         """act "q8" (default: Q4_0 x Q8_1 int8 MMQ on MFMA): Q8_1 activations on the int8
         MMQ kernels; "f16": fp16 activations and fp16-dequantized weights on the fp16 matrix cores, the
-        reference's own batched decode arithmetic (gemv_v2_source, lab/qwen_batched.py:467-680)."""
+        reference's own batched decode arithmetic (gemv_v2_source, lab/qwen_batched.py:467-680).
+        keep_logits: also write the fp32 logits [B][V] (19 MB at B = 32) to self.logits; the greedy token
+        needs only the head's per-64-row argmax partials."""
+        self.keep_logits = keep_logits
         import torch
         c = m.cfg
         if m.head_q6k is not None:
@@ -183,7 +187,8 @@ class BatchedDecoder:
             self.layer(i)
         # the LM head runs on Q8_1 activations in both modes (the int8 LDS-tiled kernel reads its 131 MB once)
         self._norm(m.norm)
-        self._mmq(e, self.xq, self.xds, 5, y=self.logits, pmax=self.pmax, pidx=self.pidx)
+        self._mmq(e, self.xq, self.xds, 5, y=self.logits if self.keep_logits else None, pmax=self.pmax,
+                  pidx=self.pidx)
         call("q355_finish", ptr(self.pmax), ptr(self.pidx), self.nparts, ptr(self.tok), ptr(self.pos), self.B)
 
     def capture(self):

@@ -143,7 +143,7 @@ int q355_rmsnorm_fix_q8_1(const int64_t* h, const float* w, int8_t* xq, void* xd
                           void* stream);
 
 /* Q4_0 x Q8_1 product of T tokens on v_mfma_i32_16x16x32_i8 (exact int32 block dots), N % 64 == 0.
- * epi 0: y fp32 [T][N] = W x;  5: logits y [T][N] + argmax partials pmax/pidx [T][q355_mmq_nparts(N)];
+ * epi 0: y fp32 [T][N] = W x;  5: argmax partials pmax/pidx [T][q355_mmq_nparts(N)] and, if y is given, logits y [T][N];
  * 6: yfix [T][N] += W x (int64 fixed point, K-sliced, integer atomics);
  * 4: rows interleaved (gate, up): y fp32 [T][N/2] = silu(g) * u;
  * 7: rows interleaved (gate, up): Q8_1 of silu(g) * u into oq [T][N/2], ods [T][N/64].

@@ -66,7 +66,7 @@ def test_config3_batch_isolation(full, act):
     p2[[0, 5]] = p1[[0, 5]]
     out = []
     for prompts in (p1, p2):
-        bd = QB.BatchedDecoder(dm, B=B, max_ctx=128, page_seed=B, act=act)
+        bd = QB.BatchedDecoder(dm, B=B, max_ctx=128, page_seed=B, act=act, keep_logits=True)
         bd.prefill_tokens(prompts)
         toks = bd.generate(steps)
         out.append((toks, bd.logits.cpu().numpy()))

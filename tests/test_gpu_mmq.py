@@ -129,6 +129,12 @@ def test_mmq_logits_argmax(cuda, V, T):
     assert relerr(yy[:, rows], OQ.gemv_q4_0_q8_1(rows_of(b, V, K, rows), len(rows), K, q, d)) < REL
     assert tok.cpu().numpy().tolist() == [int(np.argmax(r)) for r in yy]
     assert pos.cpu().numpy().tolist() == [1] * T
+    # without the fp32 logits output: the same argmax partials
+    pm2, pi2 = torch.zeros_like(pm), torch.zeros_like(pi)
+    call("q355_mmq_q4_0_q8_1", ptr(W.qs), ptr(W.d), V, K, ptr(xq), ptr(xds), T, 5, None, None, None, None, ptr(pm2),
+         ptr(pi2))
+    sync()
+    assert torch.equal(pm, pm2) and torch.equal(pi, pi2)
 
 
 def test_qkv_finish_matches_fused_epilogue(cuda):
