@@ -532,6 +532,45 @@ extern "C" int q355_mmq_q4_0_q8_1(const uint8_t* qs, const void* d, int N, int K
   }
 }
 
+// Batched decode, int8 path: attention without its merge launch, then the O projection whose activation
+// staging merges the split partials (and quantizes to Q8_1) per head.
+extern "C" int q355_attn_decode_partials(const void* q, const void* kcache, const void* vcache, const int32_t* pos,
+                                         const int32_t* block_table, int bt_stride, int nh, int nkv, int max_chunks,
+                                         double scale, double* part, int8_t* oq, void* ods, int T, void* stream) {
+  REQUIRE(q && kcache && vcache && pos && block_table && part && oq && ods, "attn_decode_partials: null pointer");
+  REQUIRE(nh > 0 && nkv > 0 && nh % nkv == 0 && nh / nkv <= 16, "attn_decode_partials: nh=%d nkv=%d", nh, nkv);
+  REQUIRE(max_chunks > 0 && max_chunks <= bt_stride && max_chunks <= 64, "attn_decode_partials: max_chunks=%d", max_chunks);
+  REQUIRE(T > 0 && T <= 65535, "attn_decode_partials: T=%d", T);
+  AttnArgs a = {};
+  a.q = (const __half*)q; a.kcache = (const __half*)kcache; a.vcache = (const __half*)vcache;
+  a.pos = pos; a.block_table = block_table; a.bt_stride = bt_stride; a.nh = nh; a.nkv = nkv;
+  a.max_chunks = max_chunks; a.scale = scale; a.part = part; a.oq = oq; a.ods = (half2*)ods;
+  hipLaunchKernelGGL(k_attn_decode_mfma<ATTN_KW>, dim3(nkv * ((max_chunks + 3) / 4), T), dim3(4 * 64 / ATTN_KW * 64), 0,
+                     (hipStream_t)stream, a);
+  return launched("attn_decode_partials");
+}
+
+extern "C" int q355_mmq_attn_o_resid(const uint8_t* qs, const void* d, int N, const double* part, int max_chunks,
+                                     const int32_t* pos, int nh, int nkv, const int8_t* xq, const void* xds,
+                                     int64_t* h, int T, void* stream) {
+  const int K = nh * HD;
+  if (int e = check_mat("mmq_attn_o_resid", qs, d, N, K)) return e;
+  REQUIRE(part && pos && xq && xds && h, "mmq_attn_o_resid: null pointer");
+  REQUIRE(nh > 0 && nkv > 0 && nh % nkv == 0 && N % 64 == 0, "mmq_attn_o_resid: N=%d nh=%d nkv=%d", N, nh, nkv);
+  REQUIRE(max_chunks > 0 && max_chunks <= 64 && T >= 1 && T <= 65535 * 16, "mmq_attn_o_resid: max_chunks=%d T=%d",
+          max_chunks, T);
+  GemvArgs a = {};
+  a.qs = qs; a.d = (const __half*)d; a.N = N; a.K = K; a.T = T; a.xq = xq; a.xds = (const half2*)xds;
+  a.attn_part = part; a.attn_max_chunks = max_chunks; a.pos = pos; a.nh = nh; a.nkv = nkv; a.yfix = (long long*)h;
+  // one K slice per head (4 blocks), 16 tokens per workgroup
+  constexpr int TT = 16, NT = 4, NW = 4, per = 4;
+  const size_t xb = (size_t)TT * (per * 32 + 16) + (size_t)TT * per * 8 + (size_t)NT * per * 32;
+  const size_t pb = (size_t)NW * NT * TT * 16 * 4;
+  hipLaunchKernelGGL((k_mmq_reg<1, NT, NW, 1, EPI_RESID_FIX, true>), dim3(N / 64, nh, (T + TT - 1) / TT), dim3(256),
+                     xb > pb ? xb : pb, (hipStream_t)stream, a);
+  return launched("mmq_attn_o_resid");
+}
+
 extern "C" int q355_mmq_nparts(int N) { return N / 64; }
 
 extern "C" int q355_mmq_q4_0_f32(const uint8_t* qs, const void* d, int N, int K, const float* xf, int T,

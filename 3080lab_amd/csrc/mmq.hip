@@ -93,6 +93,66 @@ __device__ __forceinline__ void stage_x(const GemvArgs& a, int8_t* xq, float* xd
   }
 }
 
+// Stage the O projection's activations of one K slice that is exactly one query head (4 blocks) by merging
+// the batched attention's split partials (k_attn_decode_mfma's workspace: per (token, KV head) record o
+// [nsp][G][HD] then (M, L) [nsp][G]) and quantizing to Q8_1 -- the arithmetic of k_attn_merge_split, so the
+// same bytes -- instead of reading a merged activation. Tokens whose context fits one split were finished by
+// the attention kernel: their Q8_1 is read from xq / xds. Thread: token j = tid / 16, dims 8 (tid % 16) ..
+template <int TT, int NW>
+__device__ __forceinline__ void stage_attn(const GemvArgs& a, int8_t* xq, float* xd, int xstride, int ld, int tok0,
+                                           int ntok, int b0) {
+  static_assert(TT * 16 == NW * 64, "one thread per (token, 8 dims)");
+  const int j = threadIdx.x >> 4, dg = threadIdx.x & 15;
+  const int G = a.nh / a.nkv, h = b0 / 4, kvh = h / G, hl = h % G;
+  const int nsp = (a.attn_max_chunks + 3) / 4;
+  const int tok = tok0 + j;
+  const bool live = j < ntok;
+  const int nsplit = live ? (a.pos[tok] / PAGE + 1 + 3) / 4 : 1;
+  uint2 pk = make_uint2(0, 0);
+  float dx = 0.f;
+  if (live && nsplit > 1) {                            // uniform per token (16 threads)
+    const float* wo = (const float*)a.attn_part + ((size_t)tok * a.nkv + kvh) * ((size_t)nsp * G * (HD + 2));
+    const float* wm = wo + (size_t)nsp * G * HD;
+    float2 ml[16];
+    float4 x0[16], x1[16];
+#pragma unroll
+    for (int sp = 0; sp < 16; ++sp)
+      if (sp < nsplit) {
+        ml[sp] = *(const float2*)(wm + ((size_t)sp * G + hl) * 2);
+        x0[sp] = *(const float4*)(wo + ((size_t)sp * G + hl) * HD + 8 * dg);
+        x1[sp] = *(const float4*)(wo + ((size_t)sp * G + hl) * HD + 8 * dg + 4);
+      }
+    float M = -INFINITY;
+#pragma unroll
+    for (int sp = 0; sp < 16; ++sp)
+      if (sp < nsplit) M = fmaxf(M, ml[sp].x);
+    float o[8], L = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) o[i] = 0.f;
+#pragma unroll
+    for (int sp = 0; sp < 16; ++sp)
+      if (sp < nsplit) {
+        const float f = __builtin_amdgcn_exp2f(ml[sp].x - M);
+        L = fmaf(f, ml[sp].y, L);
+        o[0] = fmaf(f, x0[sp].x, o[0]); o[1] = fmaf(f, x0[sp].y, o[1]); o[2] = fmaf(f, x0[sp].z, o[2]);
+        o[3] = fmaf(f, x0[sp].w, o[3]); o[4] = fmaf(f, x1[sp].x, o[4]); o[5] = fmaf(f, x1[sp].y, o[5]);
+        o[6] = fmaf(f, x1[sp].z, o[6]); o[7] = fmaf(f, x1[sp].w, o[7]);
+      }
+    const float inv = 1.f / L;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) o[i] *= inv;
+    float df;
+    int sq;
+    pk = q8_1_x8(o, df, sq);                           // the 4 threads of a quad hold one 32-value block
+    dx = df * 0.0625f;
+  } else if (live) {
+    pk = *(const uint2*)(a.xq + (size_t)tok * a.K + (size_t)h * HD + 8 * dg);
+    dx = __low2float(a.xds[(size_t)tok * (a.K / 32) + h * 4 + (dg >> 2)]) * 0.0625f;
+  }
+  *(uint2*)(xq + (size_t)j * xstride + 8 * dg) = pk;
+  if ((dg & 3) == 0) xd[j * ld + (dg >> 2)] = dx;
+}
+
 // Q8_1 of the 8 fp32 values this lane holds of one 32-block whose 4 quarters sit in lanes l, l ^ 16, l ^ 32,
 // l ^ 48 (the MFMA B-operand layout): d = fp16(amax / 127), q = round(x / d) (as a product with 1 / d).
 __device__ __forceinline__ long q8_1_mfma8(const float (&x)[8], float& df) {
@@ -319,7 +379,7 @@ __global__ void __launch_bounds__(NW * 64) k_mmq(const GemvArgs a) {
 // the activations are staged (wave wv takes blocks b0 + wv + NW i, i < KPW; the slice must have at most
 // NW * KPW blocks), so the HBM latency is paid once per workgroup instead of once per pipeline step. The
 // slice's scales go through LDS with the activations (registers hold only the nibbles).
-template <int TG, int NT, int NW, int KPW, int EPI>
+template <int TG, int NT, int NW, int KPW, int EPI, bool ATT = false>
 __global__ void __launch_bounds__(NW * 64) k_mmq_reg(const GemvArgs a) {
   extern __shared__ __align__(16) char lds[];
   Q355_TRACE_POINT(0);
@@ -351,8 +411,9 @@ __global__ void __launch_bounds__(NW * 64) k_mmq_reg(const GemvArgs a) {
     const int t = e / (nbs * 4), bb = (e / 4) % nbs, q = e & 3;
     wsc[e] = dd[(((size_t)(tile0 + t) * nb + ks.b0 + bb) * 16 >> 2) + q];
   }
-  // activations of the slice -> LDS
-  stage_x<TT, NW>(a, xq, xd, xstride, nbs, tok0, ntok, ks.b0, nbs);
+  // activations of the slice -> LDS (ATT: merged from the attention's split partials, one head per slice)
+  if constexpr (ATT) stage_attn<TT, NW>(a, xq, xd, xstride, nbs, tok0, ntok, ks.b0);
+  else stage_x<TT, NW>(a, xq, xd, xstride, nbs, tok0, ntok, ks.b0, nbs);
   __syncthreads();
   Q355_TRACE_POINT(1);
   float acc[NT][TG][4];

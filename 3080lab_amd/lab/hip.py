@@ -18,6 +18,8 @@ LIB_PATH = Path(__file__).resolve().parents[1] / "lib" / "libqwen355.so"
 _P = c_void_p
 # name -> argtypes (all return int status)
 _SIGS = {
+    "q355_attn_decode_partials": [_P, _P, _P, _P, _P, c_int, c_int, c_int, c_int, c_double, _P, _P, _P, c_int, _P],
+    "q355_mmq_attn_o_resid": [_P, _P, c_int, _P, c_int, _P, c_int, c_int, _P, _P, _P, c_int, _P],
     "q355_quant_q8_1": [_P, _P, _P, c_int, c_int, _P],
     "q355_rmsnorm_q8_1": [_P, _P, _P, _P, c_int, c_int, c_float, _P],
     "q355_gemv_q4_0_q8_1": [_P, _P, c_int, c_int, _P, _P, c_int, _P, _P, c_int, _P],

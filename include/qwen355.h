@@ -177,6 +177,23 @@ int q355_rmsnorm_fix_f16(const int64_t* h, const float* w, void* xh, int T, int 
 int q355_gemm_q4_0_f16(const uint8_t* qs, const void* d, int N, int K, const void* xh, int T, int epi, float* y,
                        int64_t* yfix, void* yh, float* pmax, int32_t* pidx, void* stream);
 
+/* The batched int8 path's attention without its merge launch: as q355_attn_decode with fp32 = 1, but tokens
+ * whose context spans several 4-page splits leave only their split partials in part (for
+ * q355_mmq_attn_o_resid); tokens of <= 256 positions are finished into oq/ods.
+ * Replaces the batched ATTN4 of scripts/qwen_batched_decode.py:156-187 (its combine moves into the O product). */
+int q355_attn_decode_partials(const void* q, const void* kcache, const void* vcache, const int32_t* pos,
+                              const int32_t* block_table, int bt_stride, int nh, int nkv, int max_chunks, double scale,
+                              double* part, int8_t* oq, void* ods, int T, void* stream);
+
+/* O projection + residual of the batched int8 path with the attention merge in its activation staging:
+ * h[T][N] += Wo . Q8_1(merge(part)) per head (one K slice per head), reading xq/xds for tokens that
+ * q355_attn_decode_partials finished itself. The same bytes as q355_attn_decode's merge followed by
+ * q355_mmq_q4_0_q8_1 (epi 6). K = nh * 128.
+ * Replaces the batched combine + gemv_v2_source 'resid' for o (scripts/qwen_batched_decode.py:156-187). */
+int q355_mmq_attn_o_resid(const uint8_t* qs, const void* d, int N, const double* part, int max_chunks,
+                          const int32_t* pos, int nh, int nkv, const int8_t* xq, const void* xds, int64_t* h, int T,
+                          void* stream);
+
 /* Batched decode attention (fp16 MFMA, fp32 softmax; the GQA group's heads as MFMA columns) + merge of the
  * page partials -> fp16 oh [T][nh*128]. Arguments and the part scratch as q355_attn_decode with fp32 = 1.
  * Replaces the batched ATTN4 + combine of scripts/qwen_batched_decode.py:156-187. */

@@ -328,3 +328,42 @@ def test_mmq_swiglu_f32_then_down_f32(cuda, T):
     qm, dm_, _ = OQ.quantize_q8_1(m.cpu().numpy())
     ref = OQ.gemv_q4_0_q8_1(bd, K, F, qm, dm_)
     assert relerr(h.cpu().numpy() / QM.FIX_SCALE - h0, ref) < REL
+
+
+@pytest.mark.parametrize("T", [3, 8, 32, 40])
+def test_attn_partials_merge_in_o_product(cuda, T):
+    """Attention without its merge launch + the O product that merges the split partials per head while
+    staging (q355_attn_decode_partials + q355_mmq_attn_o_resid) adds bit-equal residuals to attention with
+    its merge + the plain O product, for contexts of 1 to 9 splits (short ones finished by the attention)."""
+    import torch
+    c = QM.Config(L=1, V=1024)
+    mc = 36
+    rng = np.random.default_rng(T)
+    kc = dev(rng.standard_normal((T * mc, c.NKV, 64, 128)).astype(np.float16))
+    vc = dev(rng.standard_normal((T * mc, c.NKV, 64, 128)).astype(np.float16))
+    bt = dev(rng.permutation(T * mc).astype(np.int32).reshape(T, mc))
+    q = dev((rng.standard_normal((T, c.NH * 128)) * 2).astype(np.float16))
+    pos_np = rng.integers(0, mc * 64, T).astype(np.int32)
+    pos_np[0] = 100                                    # one split, finished by the attention kernel
+    pos = dev(pos_np)
+    W, _ = mat(c.H, c.NH * 128, 77)
+    h0 = np.round(rng.standard_normal((T, c.H)) * QM.FIX_SCALE).astype(np.int64)
+    out = []
+    for fused in (True, False):
+        part = torch.full((T, c.NH, mc, 130), float("nan"), dtype=torch.float64, device=cuda)
+        oq = torch.zeros(T, c.NH * 128, dtype=torch.int8, device=cuda)
+        ods = torch.zeros(T, c.NH * 4, 2, dtype=torch.float16, device=cuda)
+        h = dev(h0.copy())
+        if fused:
+            call("q355_attn_decode_partials", ptr(q), ptr(kc), ptr(vc), ptr(pos), ptr(bt), mc, c.NH, c.NKV, mc,
+                 1 / math.sqrt(128), ptr(part), ptr(oq), ptr(ods), T)
+            call("q355_mmq_attn_o_resid", ptr(W.qs), ptr(W.d), c.H, ptr(part), mc, ptr(pos), c.NH, c.NKV, ptr(oq),
+                 ptr(ods), ptr(h), T)
+        else:
+            call("q355_attn_decode", ptr(q), ptr(kc), ptr(vc), ptr(pos), ptr(bt), mc, c.NH, c.NKV, mc,
+                 1 / math.sqrt(128), ptr(part), ptr(oq), ptr(ods), None, T, 1)
+            call("q355_mmq_q4_0_q8_1", ptr(W.qs), ptr(W.d), c.H, c.NH * 128, ptr(oq), ptr(ods), T, 6, None, ptr(h),
+                 None, None, None, None)
+        sync()
+        out.append(h.cpu().numpy())
+    assert np.array_equal(out[0], out[1])
