@@ -449,10 +449,11 @@ static int launch_mmq_r_tg(const GemvArgs& a, hipStream_t s) {
     return launched("mmq");
   }
   if constexpr (EPI == EPI_QKV && !XF32) {
-    // one writer per output (no K split): 16-row workgroups of 8 waves x 6 blocks, bias + RoPE + K/V write
-    // in the epilogue (a RoPE pair sits in adjacent rows of one tile)
-    if (a.N % 16 || nb > 8 * 6) return -1;
-    hipLaunchKernelGGL((k_mmq_r<TG, 1, 8, 6, EPI, XF32>), dim3(a.N / 16), dim3(512), 0, s, a);
+    // one writer per output (no K split): 16-row workgroups of 16 waves x 3 blocks (8 waves x 6: 5.77 / 9.80 us
+    // at B = 8 / 32 against 5.20 / 8.94), bias + RoPE + K/V write in the epilogue (a RoPE pair sits in
+    // adjacent rows of one tile)
+    if (a.N % 16 || nb > 16 * 3) return -1;
+    hipLaunchKernelGGL((k_mmq_r<TG, 1, 16, 3, EPI, XF32>), dim3(a.N / 16), dim3(1024), 0, s, a);
     return launched("mmq");
   }
   if constexpr (EPI == EPI_RESID_FIX && XF32) {
@@ -613,8 +614,8 @@ template <int TG, int EPI>
 static int launch_gemm_f16r_tg(const GemvArgs& a, hipStream_t s) {
   const int nb = a.K / 32;
   if constexpr (EPI == EPI_QKV) {                    // no K split: 16-row workgroups, finish in the epilogue
-    if (a.N % 16 || nb > 8 * 6) return -1;
-    hipLaunchKernelGGL((k_gemm_f16r<TG, 1, 8, 6, EPI>), dim3(a.N / 16), dim3(512), 0, s, a);
+    if (a.N % 16 || nb > 16 * 3) return -1;
+    hipLaunchKernelGGL((k_gemm_f16r<TG, 1, 16, 3, EPI>), dim3(a.N / 16), dim3(1024), 0, s, a);
     return launched("gemm_f16");
   } else {
     if (EPI == EPI_RESID_FIX) {

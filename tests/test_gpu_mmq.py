@@ -205,22 +205,52 @@ def check_greedy(got, ref, margins, what):
 NEAR_TIE = 1e-2
 
 
+# Largest teacher-forced logit deviation from the oracle in the matching arithmetic, with margin: measured
+# 0.070 (int8 MMQ: its fp16-P attention and fp32 sums move a few Q8_1 codes per layer, each step of one code
+# moving its block by d/2) and 0.014 (fp16 mode) on this model over 10 steps.
+LOGIT_TOL = {"q8": 0.12, "f16": 0.03}
+
+
 @pytest.mark.parametrize("act", ["f16", "q8"])
 @pytest.mark.parametrize("B", [8, 32])
 def test_batched_greedy_matches_oracle(small, small_f16, B, act):
-    """B independent prompts decoded together (paged KV, scattered pages) match the oracle per sequence, in
-    both arithmetic modes (the oracle in the matching mode)."""
+    """B independent prompts decoded together (paged KV, scattered pages) against the oracle in the matching
+    arithmetic, teacher-forced: at every step each checked sequence is fed the oracle's token; its logits must
+    be within LOGIT_TOL of the oracle's, and its argmax must equal the oracle's wherever the oracle's top-2
+    margin exceeds twice that tolerance (below it, either token is a legitimate greedy choice)."""
+    import torch
     w, dm, om = small
     if act == "f16":
         om = small_f16
+    tol = LOGIT_TOL[act]
     rng = np.random.default_rng(B)
     prompts = rng.integers(0, CFG_S.V, (B, 6))
-    bd = QB.BatchedDecoder(dm, B=B, max_ctx=256, page_seed=B, act=act)
+    bd = QB.BatchedDecoder(dm, B=B, max_ctx=256, page_seed=B, act=act, keep_logits=True)
     bd.prefill_tokens(prompts)
-    got = bd.generate(10)
-    for b in ([0, 3, B - 1] if B > 8 else range(B)):
-        ref, margins = om.greedy(list(prompts[b]), 10)
-        check_greedy(got[b], ref, margins, f"B={B} seq {b}")
+    seqs = [0, 3, B - 1] if B > 8 else list(range(B))
+    ref = {}
+    for s_ in seqs:
+        cache = om.new_cache()
+        h = om.forward(list(prompts[s_]), 0, cache)
+        lgs = [om.logits(h[-1:])[0]]
+        for t in range(9):
+            h = om.forward([int(np.argmax(lgs[-1]))], 6 + t, cache)
+            lgs.append(om.logits(h)[0])
+        ref[s_] = lgs
+    for t in range(10):
+        got = bd.logits.cpu().numpy()
+        toks = got.argmax(axis=1).astype(np.int32)
+        for s_ in seqs:
+            lg = ref[s_][t]
+            dev_ = float(np.abs(got[s_] - lg).max())
+            assert dev_ < tol, f"B={B} seq {s_} step {t}: logits off by {dev_:.3g}"
+            top2 = np.partition(lg, -2)[-2:]
+            if top2[1] - top2[0] > 2 * tol:
+                assert int(toks[s_]) == int(np.argmax(lg)), f"B={B} seq {s_} step {t}"
+            toks[s_] = int(np.argmax(lg))                 # teacher forcing
+        if t < 9:
+            bd.tok.copy_(torch.from_numpy(toks))
+            bd.step()
 
 
 def test_batched_equals_single_sequence(small):
