@@ -1,9 +1,9 @@
 // Decode GQA attention over the paged fp16 KV cache, split-K over pages (flash-decoding), gfx950.
 //
-// k_attn_decode: workgroup (chunk c, KV head g, token j) = one wave per query head of the GQA group
-// (G waves). It stages one 64-position K page (row-padded against LDS bank conflicts) and V page in
-// LDS, lane p scores position p for its wave's head, the softmax numerator is a wave reduction, and
-// lane l accumulates dims 2l, 2l+1 of P.V. Output: the unnormalised partial (o[128], m, l) per
+// k_attn_decode: workgroup (chunk c, query head or heads of KV head g, token j), W waves per query head.
+// It stages one 64-position K page (row-padded against LDS bank conflicts) and V page in LDS, the lanes
+// of a position score it for their wave's head, the softmax numerator is a wave reduction, and lane l
+// accumulates dims 2l, 2l+1 of P.V. Output: the unnormalised partial (o[128], m, l) per
 // (token, query head, chunk). No atomics and no cross-workgroup waits.
 // attn_merge_*: merges the partials of one token in fixed chunk order (o = sum_c e^(m_c - M) o_c / L)
 // and quantizes the result to Q8_1 -- fused into the O-projection GEMV prologue, or standalone.
@@ -47,34 +47,36 @@ __device__ __forceinline__ float exp_t(float v) { return expf(v); }
 
 // F = double: every step in f64 (the batch-1 decode path, exact against the f64 oracle to ~1e-12);
 // F = float: fp32 scores, softmax and P.V (not launched: the batched path runs k_attn_decode_mfma below).
-// W waves per query head (1 or 2): wave W h + w takes positions (64 / W) w .. of the page; its lane
+// W waves per query head (1, 2, 4, 8 or 16): wave W h + w takes positions (64 / W) w .. of the page; its lane
 // (position (64 / W) w + lane / W, dim part lane % W) scores 128 / W dims and the W lanes of a position sum;
-// with W = 2 the two waves of a head exchange their maximum and sum through LDS, so their P.V halves
-// (lane l: dims 2l, 2l+1) share the page maximum and add into one partial (o[128], m, l) per (head, page).
-// W = 2 halves the serial f64 work of each wave (the batch-1 latency); W = 1 keeps more workgroups
-// resident (the batched throughput).
-template <int G, typename F, int W>
-__global__ void __launch_bounds__(G * W * 64) k_attn_decode(const AttnArgs a) {
-  constexpr int PPW = PAGE / W, DPL = HD / W;
+// with W > 1 the waves of a head exchange their maximum and sum through LDS, so their P.V parts
+// (lane l: dims 2l, 2l+1) share the page maximum and add, in wave order, into one partial (o[128], m, l) per
+// (head, page). HS workgroups share a page, each taking G / HS heads of the group (its K/V page staged by
+// each). More waves per head shorten the serial f64 chains of each lane (the batch-1 latency).
+template <int G, typename F, int W, int HS>
+__global__ void __launch_bounds__(G / HS * W * 64) k_attn_decode(const AttnArgs a) {
+  static_assert(G % HS == 0 && (W == 1 || W == 2 || W == 4 || W == 8 || W == 16), "k_attn_decode: head split / wave count");
+  constexpr int GH = G / HS, PPW = PAGE / W, DPL = HD / W;
   __shared__ __align__(16) __half ks[PAGE][KROW];
   __shared__ __align__(16) __half vs[PAGE][HD];
-  __shared__ __align__(16) F qf[G][HD];
-  __shared__ F xm[G][W], xl[G][W];
-  __shared__ __align__(16) F xo[W == 2 ? G : 1][HD];
+  __shared__ __align__(16) F qf[GH][HD];
+  __shared__ F xm[GH][W], xl[GH][W];
+  __shared__ __align__(16) F xo[W > 1 ? GH : 1][W > 1 ? W - 1 : 1][HD];
 
   const int j = blockIdx.y;
-  const int kvh = blockIdx.x / a.max_chunks, c = blockIdx.x % a.max_chunks;
+  const int c = blockIdx.x % a.max_chunks, r = blockIdx.x / a.max_chunks;
+  const int kvh = r / HS, hs = r % HS;
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int hh = wv / W, part = wv % W;
   const int pos = a.pos[j];
   const int pg = a.block_table[(size_t)j * a.bt_stride + c];
-  const int hq = kvh * G + hh;
+  const int hq = kvh * G + hs * GH + hh;
   if (c * PAGE > pos) return;                       // chunk beyond the context: nothing to do
   const int nvalid = min(PAGE, pos + 1 - c * PAGE);
 
   const uint4* kp = (const uint4*)(a.kcache + ((size_t)pg * a.nkv + kvh) * PAGE * HD);
   const uint4* vp = (const uint4*)(a.vcache + ((size_t)pg * a.nkv + kvh) * PAGE * HD);
-  constexpr int NT = G * W * 64, PER = (PAGE * HD / 8 + NT - 1) / NT;
+  constexpr int NT = GH * W * 64, PER = (PAGE * HD / 8 + NT - 1) / NT;
   uint4 kr[PER], vr[PER];
 #pragma unroll
   for (int i = 0; i < PER; ++i) {
@@ -117,18 +119,23 @@ __global__ void __launch_bounds__(G * W * 64) k_attn_decode(const AttnArgs a) {
       }
     }
     s = (sp[0] + sp[1]) + (sp[2] + sp[3]);
-    if (W == 2) s += dpp_t<DPP_XOR1>(s);
+    if (W >= 2) s += dpp_t<DPP_XOR1>(s);
+    if (W >= 4) s += dpp_t<DPP_XOR2>(s);
+    if (W >= 8) s += dpp_t<DPP_HALF_MIRROR>(s);   // the two quads of each 8 lanes
+    if (W == 16) s += dpp_t<DPP_MIRROR>(s);       // the two halves of each 16-lane row
   }
   s = p < nvalid ? s * (F)a.scale : (F)-INFINITY;
-  F m = wmax(s);                                    // with W = 2 each position twice: harmless
-  if (W == 2) {
+  F m = wmax(s);                                    // with W > 1 each position W times: harmless
+  if (W > 1) {
     if (lane == 0) xm[hh][part] = m;
     __syncthreads();
-    m = max_t(xm[hh][0], xm[hh][1]);
+    m = xm[hh][0];
+#pragma unroll
+    for (int w = 1; w < W; ++w) m = max_t(m, xm[hh][w]);
   }
   const F e = p < nvalid ? exp_t(s - m) : (F)0;
   const F lw = wsum(dh == 0 ? e : (F)0);
-  if (W == 2 && lane == 0) xl[hh][part] = lw;
+  if (W > 1 && lane == 0) xl[hh][part] = lw;
 
   // P.V over this wave's positions: lane owns dims 2*lane, 2*lane+1; position q's weight from lane W q
   F o[4][2] = {{0, 0}, {0, 0}, {0, 0}, {0, 0}};
@@ -142,16 +149,19 @@ __global__ void __launch_bounds__(G * W * 64) k_attn_decode(const AttnArgs a) {
   F o0 = (o[0][0] + o[1][0]) + (o[2][0] + o[3][0]);
   F o1 = (o[0][1] + o[1][1]) + (o[2][1] + o[3][1]);
   F l = lw;
-  if (W == 2) {
-    if (part == 1) {
-      xo[hh][2 * lane] = o0;
-      xo[hh][2 * lane + 1] = o1;
+  if (W > 1) {
+    if (part > 0) {
+      xo[hh][part - 1][2 * lane] = o0;
+      xo[hh][part - 1][2 * lane + 1] = o1;
     }
     __syncthreads();
-    if (part == 1) return;
-    o0 += xo[hh][2 * lane];
-    o1 += xo[hh][2 * lane + 1];
-    l = xl[hh][0] + xl[hh][1];
+    if (part > 0) return;
+#pragma unroll
+    for (int w = 1; w < W; ++w) {
+      o0 += xo[hh][w - 1][2 * lane];
+      o1 += xo[hh][w - 1][2 * lane + 1];
+      l += xl[hh][w];
+    }
   }
   double* P = a.part + (((size_t)j * a.nh + hq) * a.max_chunks + c) * (HD + 2);
   ((double2*)P)[lane] = make_double2((double)o0, (double)o1);

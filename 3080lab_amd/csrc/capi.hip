@@ -299,17 +299,19 @@ extern "C" int q355_attn_decode(const void* q, const void* kcache, const void* v
   a.max_chunks = max_chunks; a.scale = scale; a.part = part;
   a.oq = oq; a.ods = (half2*)ods; a.o32 = o32;
   hipStream_t s = (hipStream_t)stream;
-  const dim3 grid(nkv * max_chunks, T);
   if (fp32) {                                           // attention (4-page merge inside) + split merge
     hipLaunchKernelGGL(k_attn_decode_mfma<ATTN_KW>, dim3(nkv * ((max_chunks + 3) / 4), T), dim3(4 * 64 / ATTN_KW * 64), 0, s, a);
     if (int e = launched("attn_decode")) return e;
     hipLaunchKernelGGL(k_attn_merge_split, dim3(nkv, T), dim3(256), 0, s, a);
     return launched("attn_merge_split");
   } else {
+    // one query head per workgroup, 16 waves of 4 positions each (short serial f64 chains per lane); the
+    // workgroups of a KV head's group each stage its K/V page (from L2 after the first)
+    const dim3 grid(nh * max_chunks, T);
     switch (nh / nkv) {
-      case 4: hipLaunchKernelGGL((k_attn_decode<4, double, 2>), grid, dim3(512), 0, s, a); break;
-      case 6: hipLaunchKernelGGL((k_attn_decode<6, double, 2>), grid, dim3(768), 0, s, a); break;
-      default: hipLaunchKernelGGL((k_attn_decode<8, double, 2>), grid, dim3(1024), 0, s, a); break;
+      case 4: hipLaunchKernelGGL((k_attn_decode<4, double, 16, 4>), grid, dim3(1024), 0, s, a); break;
+      case 6: hipLaunchKernelGGL((k_attn_decode<6, double, 16, 6>), grid, dim3(1024), 0, s, a); break;
+      default: hipLaunchKernelGGL((k_attn_decode<8, double, 16, 8>), grid, dim3(1024), 0, s, a); break;
     }
   }
   if (int e = launched("attn_decode")) return e;

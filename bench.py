@@ -38,10 +38,10 @@ sys.path.insert(0, str(ROOT / "3080lab_amd"))
 HBM_PEAK_GBS = 8000.0
 GEMV0_BYTES = 6_881_280 + 860_160 + 1_728 + 35_840     # config 0: nibbles + scales + Q8_1 x + fp32 y
 # HBM bytes per gate_up launch from rocprofv3 PMC (FETCH_SIZE x 2.0 + WRITE_SIZE x 1.0 KiB per dispatch; the
-# factors make a 64 MiB device copy read 64 MiB and write 64 MiB): 7706.5 * 2 + 35.0 KiB. Counters cannot be
+# factors make a 64 MiB device copy read 64 MiB and write 64 MiB): 7703.5 * 2 + 35.0 KiB. Counters cannot be
 # read from inside this process, so the measured figure is recorded here and re-measured by
 #   rocprofv3 --pmc FETCH_SIZE -- python3 bench.py --quick --no-cpu --steps 4   (then WRITE_SIZE, then --copy-probe)
-GATE_UP_TRAFFIC = int((7706.5 * 2 + 35.0) * 1024)
+GATE_UP_TRAFFIC = int((7703.5 * 2 + 35.0) * 1024)
 
 
 def log(*a):
