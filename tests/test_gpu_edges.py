@@ -77,6 +77,36 @@ def test_gemv_all_zero_activation_blocks(cuda):
 
 
 @pytest.mark.parametrize("fp32", [0, 1])
+@pytest.mark.parametrize("nh,nkv", [(8, 2), (16, 2), (12, 3)])
+def test_attn_decode_gqa_groups(cuda, nh, nkv, fp32):
+    """GQA groups of 4 and 8 query heads per KV head (the model's is 6): each group size has its own
+    instantiation of the f64 kernel, one query head per workgroup. Positions cover one page, a page plus one
+    key and three full pages."""
+    import torch
+    mc = 4
+    rng = np.random.default_rng(nh * 10 + nkv + fp32)
+    pos = np.array([0, 64, 255], np.int32)
+    T = len(pos)
+    kc = rng.standard_normal((T * mc, nkv, 64, 128)).astype(np.float16)
+    vc = rng.standard_normal((T * mc, nkv, 64, 128)).astype(np.float16)
+    bt = rng.permutation(T * mc).astype(np.int32).reshape(T, mc)
+    q = (rng.standard_normal((T, nh * 128)) * 2).astype(np.float16)
+    part = torch.zeros(T, nh, mc, 130, dtype=torch.float64, device=cuda)
+    oq = torch.zeros(T, nh * 128, dtype=torch.int8, device=cuda)
+    ods = torch.zeros(T, nh * 4, 2, dtype=torch.float16, device=cuda)
+    o32 = torch.zeros(T, nh * 128, device=cuda)
+    call("q355_attn_decode", ptr(dev(q)), ptr(dev(kc)), ptr(dev(vc)), ptr(dev(pos)), ptr(dev(bt)), mc, nh, nkv, mc,
+         1 / math.sqrt(128), ptr(part), ptr(oq), ptr(ods), ptr(o32), T, fp32)
+    torch.cuda.synchronize()
+    for j in range(T):
+        K = np.concatenate([kc[bt[j, p]] for p in range(mc)], axis=1)
+        V = np.concatenate([vc[bt[j, p]] for p in range(mc)], axis=1)
+        ref = OM.attn_decode(q[j].reshape(nh, 128), K, V, int(pos[j]) + 1, nh, nkv)
+        # f64 scores/softmax/P.V rounded once to fp32 (fp32 = 0); fp16 P on the matrix cores (fp32 = 1)
+        assert relerr(o32[j].cpu().numpy(), ref) < (1e-6 if fp32 == 0 else 1e-3), (nh, nkv, j)
+
+
+@pytest.mark.parametrize("fp32", [0, 1])
 def test_attn_decode_longest_context(cuda, fp32):
     """max_chunks = 64 pages: the last position of a 4096-token cache, and position 0 beside it."""
     import torch
