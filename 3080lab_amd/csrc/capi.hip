@@ -439,15 +439,19 @@ static int launch_mmq_logits_tile(const GemvArgs& a, hipStream_t s) {
 }
 
 // Register-resident decode-batch kernel (T <= 32). SWIGLU (fp32 out) with N % 80 == 0 and K <= 1536:
-// 80-row workgroups of 8 waves x 6 blocks (224 for gate_up, one per CU). RESID_FIX from fp32 activations
-// (XF32): 64-row workgroups, K split 32 blocks per slice (8 waves x 4) or <= 16 (4 waves x 4).
+// 80-row workgroups of 16 waves x 3 blocks (8 x 6 at 32 tokens; 224 for gate_up, one per CU). RESID_FIX from fp32 activations
+// (XF32): 64-row workgroups, K split 32 blocks per slice (16 waves x 2 up to 16 tokens, else 8 x 4) or <= 16
+// (4 waves x 4).
 // Returns -1 outside these classes.
 template <int TG, int EPI, bool XF32>
 static int launch_mmq_r_tg(const GemvArgs& a, hipStream_t s) {
   const int nb = a.K / 32;
   if constexpr (EPI == EPI_SWIGLU && !XF32) {
     if (a.N % 80 || a.N / 80 > 256 || nb > 8 * 6) return -1;
-    hipLaunchKernelGGL((k_mmq_r<TG, 5, 8, 6, EPI, XF32>), dim3(a.N / 80), dim3(512), 0, s, a);
+    // up to 16 tokens 16 waves x 3 blocks (8 x 6: 9.66 against 8.34 us at B = 8); 32 tokens keep 8 waves (the
+    // 16-wave partials would need 160 KB of LDS)
+    if constexpr (TG == 1) hipLaunchKernelGGL((k_mmq_r<TG, 5, 16, 3, EPI, XF32>), dim3(a.N / 80), dim3(1024), 0, s, a);
+    else hipLaunchKernelGGL((k_mmq_r<TG, 5, 8, 6, EPI, XF32>), dim3(a.N / 80), dim3(512), 0, s, a);
     return launched("mmq");
   }
   if constexpr (EPI == EPI_QKV && !XF32) {
@@ -462,7 +466,8 @@ static int launch_mmq_r_tg(const GemvArgs& a, hipStream_t s) {
     if (a.N % 64) return -1;
     if (nb >= 64) {
       const int KS = (nb + 31) / 32;
-      hipLaunchKernelGGL((k_mmq_r<TG, 4, 8, 4, EPI, XF32>), dim3(a.N / 64, KS), dim3(512), 0, s, a);
+      if constexpr (TG == 1) hipLaunchKernelGGL((k_mmq_r<TG, 4, 16, 2, EPI, XF32>), dim3(a.N / 64, KS), dim3(1024), 0, s, a);
+      else hipLaunchKernelGGL((k_mmq_r<TG, 4, 8, 4, EPI, XF32>), dim3(a.N / 64, KS), dim3(512), 0, s, a);
       return launched("mmq");
     }
     int KS = 1;
@@ -609,8 +614,8 @@ static int launch_gemm_f16(GemvArgs a, int KS, hipStream_t s) {
 }
 
 // Register-resident variant for T <= 32: one launch per shape class. SWIGLU_F16 and the other single-slice
-// epilogues: 80-row workgroups (N % 80 == 0; 224 for gate_up, one per CU) or 64-row ones, 8 waves x 6
-// blocks over K <= 1536. RESID_FIX: 64-row workgroups of 4 waves, K split until ~256 workgroups.
+// epilogues: 80-row workgroups (N % 80 == 0; 224 for gate_up, one per CU; 16 waves x 3 blocks up to 16 tokens,
+// measured 8.4 against 9.0 us at B = 8) or 64-row ones, 8 waves x 6 blocks over K <= 1536. RESID_FIX: 64-row workgroups of 4 waves, K split until ~256 workgroups.
 // Returns -1 when the shape falls outside these classes.
 template <int TG, int EPI>
 static int launch_gemm_f16r_tg(const GemvArgs& a, hipStream_t s) {
@@ -622,9 +627,10 @@ static int launch_gemm_f16r_tg(const GemvArgs& a, hipStream_t s) {
   } else {
     if (EPI == EPI_RESID_FIX) {
       if (a.N % 64) return -1;
-      if (nb >= 64) {                                  // long K (down): 8 waves x 4 blocks per slice
+      if (nb >= 64) {                                  // long K (down): 16 waves x 2 blocks per slice (8 x 4 at 32 tokens)
         const int KS = (nb + 31) / 32;
-        hipLaunchKernelGGL((k_gemm_f16r<TG, 4, 8, 4, EPI>), dim3(a.N / 64, KS), dim3(512), 0, s, a);
+        if constexpr (TG == 1) hipLaunchKernelGGL((k_gemm_f16r<TG, 4, 16, 2, EPI>), dim3(a.N / 64, KS), dim3(1024), 0, s, a);
+        else hipLaunchKernelGGL((k_gemm_f16r<TG, 4, 8, 4, EPI>), dim3(a.N / 64, KS), dim3(512), 0, s, a);
         return launched("gemm_f16");
       }
       int KS = 1;
@@ -639,7 +645,8 @@ static int launch_gemm_f16r_tg(const GemvArgs& a, hipStream_t s) {
     }
     if (nb > 8 * 6) return -1;
     if (a.N % 80 == 0 && a.N / 80 <= 256) {
-      hipLaunchKernelGGL((k_gemm_f16r<TG, 5, 8, 6, EPI>), dim3(a.N / 80), dim3(512), 0, s, a);
+      if constexpr (TG == 1) hipLaunchKernelGGL((k_gemm_f16r<TG, 5, 16, 3, EPI>), dim3(a.N / 80), dim3(1024), 0, s, a);
+      else hipLaunchKernelGGL((k_gemm_f16r<TG, 5, 8, 6, EPI>), dim3(a.N / 80), dim3(512), 0, s, a);
     } else {
       if (a.N % 64) return -1;
       hipLaunchKernelGGL((k_gemm_f16r<TG, 4, 8, 6, EPI>), dim3(a.N / 64), dim3(512), 0, s, a);
