@@ -558,6 +558,40 @@ extern "C" int q355_attn_decode_partials(const void* q, const void* kcache, cons
   return launched("attn_decode_partials");
 }
 
+extern "C" int q355_attn_decode_partials_f16(const void* q, const void* kcache, const void* vcache, const int32_t* pos,
+                                             const int32_t* block_table, int bt_stride, int nh, int nkv, int max_chunks,
+                                             double scale, double* part, void* oh, int T, void* stream) {
+  REQUIRE(q && kcache && vcache && pos && block_table && part && oh, "attn_decode_partials_f16: null pointer");
+  REQUIRE(nh > 0 && nkv > 0 && nh % nkv == 0 && nh / nkv <= 16, "attn_decode_partials_f16: nh=%d nkv=%d", nh, nkv);
+  REQUIRE(max_chunks > 0 && max_chunks <= bt_stride && max_chunks <= 64, "attn_decode_partials_f16: max_chunks=%d",
+          max_chunks);
+  REQUIRE(T > 0 && T <= 65535, "attn_decode_partials_f16: T=%d", T);
+  AttnArgs a = {};
+  a.q = (const __half*)q; a.kcache = (const __half*)kcache; a.vcache = (const __half*)vcache;
+  a.pos = pos; a.block_table = block_table; a.bt_stride = bt_stride; a.nh = nh; a.nkv = nkv;
+  a.max_chunks = max_chunks; a.scale = scale; a.part = part; a.oh = (__half*)oh;
+  hipLaunchKernelGGL(k_attn_decode_mfma<ATTN_KW>, dim3(nkv * ((max_chunks + 3) / 4), T), dim3(4 * 64 / ATTN_KW * 64), 0,
+                     (hipStream_t)stream, a);
+  return launched("attn_decode_partials_f16");
+}
+
+extern "C" int q355_gemm_f16_attn_o_resid(const uint8_t* qs, const void* d, int N, const double* part, int max_chunks,
+                                          const int32_t* pos, int nh, int nkv, const void* oh, int64_t* h, int T,
+                                          void* stream) {
+  const int K = nh * HD;
+  if (int e = check_mat("gemm_f16_attn_o_resid", qs, d, N, K)) return e;
+  REQUIRE(part && pos && oh && h, "gemm_f16_attn_o_resid: null pointer");
+  REQUIRE(nh > 0 && nkv > 0 && nh % nkv == 0 && nh / nkv <= 16 && N % 64 == 0, "gemm_f16_attn_o_resid: N=%d nh=%d nkv=%d",
+          N, nh, nkv);
+  REQUIRE(max_chunks > 0 && max_chunks <= 64 && T >= 1 && T <= 16, "gemm_f16_attn_o_resid: max_chunks=%d T=%d (T <= 16)",
+          max_chunks, T);
+  GemvArgs a = {};
+  a.qs = qs; a.d = (const __half*)d; a.N = N; a.K = K; a.T = T; a.xh = (const __half*)oh;
+  a.attn_part = part; a.attn_max_chunks = max_chunks; a.pos = pos; a.nh = nh; a.nkv = nkv; a.yfix = (long long*)h;
+  hipLaunchKernelGGL(k_gemm_f16_attn_o, dim3(N / 64, nh), dim3(256), 0, (hipStream_t)stream, a);
+  return launched("gemm_f16_attn_o_resid");
+}
+
 extern "C" int q355_mmq_attn_o_resid(const uint8_t* qs, const void* d, int N, const double* part, int max_chunks,
                                      const int32_t* pos, int nh, int nkv, const int8_t* xq, const void* xds,
                                      int64_t* h, int T, void* stream) {

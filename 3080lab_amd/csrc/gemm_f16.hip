@@ -204,4 +204,54 @@ __global__ void __launch_bounds__(NW * 64) k_gemm_f16r(const GemvArgs a) {
   else epilogue<NW, TT, NT, EPI>(a, part, tile0);
 }
 
+// Decode-batch O product + residual in the fp16 arithmetic with the split-attention merge in its activation
+// staging (T <= 16): workgroup (4 row tiles of 16, query head h = its K slice of 4 blocks, all tokens). Thread
+// (token j, 8 dims dg) merges the head's partials (attn_merge8, then fp16 rounding: the bytes
+// k_attn_merge_split writes) or reads the fp16 output the attention kernel finished; wave w multiplies block
+// 4 h + w; partials reduce over the 4 waves into the fixed-point residual.
+__global__ void __launch_bounds__(256) k_gemm_f16_attn_o(const GemvArgs a) {
+  constexpr int NT = 4, NW = 4, TT = 16, XR = HD + 8;   // XR: padded LDS row (halves)
+  __shared__ __align__(16) _Float16 xs[TT][XR];
+  __shared__ float part[NW][NT][TT][16];
+  const int K = a.K, nb = K / 32;
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int li = lane & 15, lg = lane >> 4;
+  const int tile0 = blockIdx.x * NT, h = blockIdx.y, b = 4 * h + wv;
+  uint2 w[NT];
+  __half dsc[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    const size_t base = ((size_t)(tile0 + t) * nb + b) * 16 + li;
+    w[t] = ((const uint2*)a.qs)[base * 2 + (lg & 1)];
+    dsc[t] = a.d[base];
+  }
+  {
+    const int j = threadIdx.x >> 4, dg = threadIdx.x & 15;
+    uint4 v = make_uint4(0, 0, 0, 0);                   // tokens past T stay zero (never stored)
+    float o[8];
+    if (j < a.T && attn_merge8(a, j, h, dg, o)) {
+      unsigned pk[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const __half2 hv = __floats2half2_rn(o[2 * i], o[2 * i + 1]);
+        pk[i] = *reinterpret_cast<const unsigned*>(&hv);
+      }
+      v = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+    } else if (j < a.T) {
+      v = *(const uint4*)(a.xh + (size_t)j * K + (size_t)h * HD + 8 * dg);
+    }
+    *(uint4*)&xs[j][8 * dg] = v;
+  }
+  __syncthreads();
+  const fh8 xb = *(const fh8*)&xs[li][wv * 32 + 8 * lg];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    const ff4 acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(deq8(w[t], lg, dsc[t]), xb, ff4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+#pragma unroll
+    for (int v = 0; v < 4; ++v) part[wv][t][li][4 * lg + v] = acc[v];
+  }
+  __syncthreads();
+  epilogue<NW, TT, NT, EPI_RESID_FIX>(a, part, tile0);
+}
+
 }  // namespace q355

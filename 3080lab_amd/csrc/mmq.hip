@@ -98,49 +98,59 @@ __device__ __forceinline__ void stage_x(const GemvArgs& a, int8_t* xq, float* xd
 // [nsp][G][HD] then (M, L) [nsp][G]) and quantizing to Q8_1 -- the arithmetic of k_attn_merge_split, so the
 // same bytes -- instead of reading a merged activation. Tokens whose context fits one split were finished by
 // the attention kernel: their Q8_1 is read from xq / xds. Thread: token j = tid / 16, dims 8 (tid % 16) ..
+// Merge of one (token, query head h, 8 dims dg) over its split-attention partials (the fp32 workspace of
+// k_attn_decode_mfma): o = sum_s e^(m_s - M) o_s / sum_s e^(m_s - M) l_s in split order, the arithmetic of
+// k_attn_merge_split. Returns false when the token has one split (the attention kernel finished it itself).
+__device__ __forceinline__ bool attn_merge8(const GemvArgs& a, int tok, int h, int dg, float (&o)[8]) {
+  const int G = a.nh / a.nkv, kvh = h / G, hl = h % G;
+  const int nsp = (a.attn_max_chunks + 3) / 4;
+  const int nsplit = (a.pos[tok] / PAGE + 1 + 3) / 4;
+  if (nsplit == 1) return false;                       // uniform per token (16 threads)
+  const float* wo = (const float*)a.attn_part + ((size_t)tok * a.nkv + kvh) * ((size_t)nsp * G * (HD + 2));
+  const float* wm = wo + (size_t)nsp * G * HD;
+  float2 ml[16];
+  float4 x0[16], x1[16];
+#pragma unroll
+  for (int sp = 0; sp < 16; ++sp)
+    if (sp < nsplit) {
+      ml[sp] = *(const float2*)(wm + ((size_t)sp * G + hl) * 2);
+      x0[sp] = *(const float4*)(wo + ((size_t)sp * G + hl) * HD + 8 * dg);
+      x1[sp] = *(const float4*)(wo + ((size_t)sp * G + hl) * HD + 8 * dg + 4);
+    }
+  float M = -INFINITY;
+#pragma unroll
+  for (int sp = 0; sp < 16; ++sp)
+    if (sp < nsplit) M = fmaxf(M, ml[sp].x);
+  float L = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) o[i] = 0.f;
+#pragma unroll
+  for (int sp = 0; sp < 16; ++sp)
+    if (sp < nsplit) {
+      const float f = __builtin_amdgcn_exp2f(ml[sp].x - M);
+      L = fmaf(f, ml[sp].y, L);
+      o[0] = fmaf(f, x0[sp].x, o[0]); o[1] = fmaf(f, x0[sp].y, o[1]); o[2] = fmaf(f, x0[sp].z, o[2]);
+      o[3] = fmaf(f, x0[sp].w, o[3]); o[4] = fmaf(f, x1[sp].x, o[4]); o[5] = fmaf(f, x1[sp].y, o[5]);
+      o[6] = fmaf(f, x1[sp].z, o[6]); o[7] = fmaf(f, x1[sp].w, o[7]);
+    }
+  const float inv = 1.f / L;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) o[i] *= inv;
+  return true;
+}
+
 template <int TT, int NW>
 __device__ __forceinline__ void stage_attn(const GemvArgs& a, int8_t* xq, float* xd, int xstride, int ld, int tok0,
                                            int ntok, int b0) {
   static_assert(TT * 16 == NW * 64, "one thread per (token, 8 dims)");
   const int j = threadIdx.x >> 4, dg = threadIdx.x & 15;
-  const int G = a.nh / a.nkv, h = b0 / 4, kvh = h / G, hl = h % G;
-  const int nsp = (a.attn_max_chunks + 3) / 4;
+  const int h = b0 / 4;
   const int tok = tok0 + j;
   const bool live = j < ntok;
-  const int nsplit = live ? (a.pos[tok] / PAGE + 1 + 3) / 4 : 1;
   uint2 pk = make_uint2(0, 0);
   float dx = 0.f;
-  if (live && nsplit > 1) {                            // uniform per token (16 threads)
-    const float* wo = (const float*)a.attn_part + ((size_t)tok * a.nkv + kvh) * ((size_t)nsp * G * (HD + 2));
-    const float* wm = wo + (size_t)nsp * G * HD;
-    float2 ml[16];
-    float4 x0[16], x1[16];
-#pragma unroll
-    for (int sp = 0; sp < 16; ++sp)
-      if (sp < nsplit) {
-        ml[sp] = *(const float2*)(wm + ((size_t)sp * G + hl) * 2);
-        x0[sp] = *(const float4*)(wo + ((size_t)sp * G + hl) * HD + 8 * dg);
-        x1[sp] = *(const float4*)(wo + ((size_t)sp * G + hl) * HD + 8 * dg + 4);
-      }
-    float M = -INFINITY;
-#pragma unroll
-    for (int sp = 0; sp < 16; ++sp)
-      if (sp < nsplit) M = fmaxf(M, ml[sp].x);
-    float o[8], L = 0.f;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) o[i] = 0.f;
-#pragma unroll
-    for (int sp = 0; sp < 16; ++sp)
-      if (sp < nsplit) {
-        const float f = __builtin_amdgcn_exp2f(ml[sp].x - M);
-        L = fmaf(f, ml[sp].y, L);
-        o[0] = fmaf(f, x0[sp].x, o[0]); o[1] = fmaf(f, x0[sp].y, o[1]); o[2] = fmaf(f, x0[sp].z, o[2]);
-        o[3] = fmaf(f, x0[sp].w, o[3]); o[4] = fmaf(f, x1[sp].x, o[4]); o[5] = fmaf(f, x1[sp].y, o[5]);
-        o[6] = fmaf(f, x1[sp].z, o[6]); o[7] = fmaf(f, x1[sp].w, o[7]);
-      }
-    const float inv = 1.f / L;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) o[i] *= inv;
+  float o[8];
+  if (live && attn_merge8(a, tok, h, dg, o)) {
     float df;
     int sq;
     pk = q8_1_x8(o, df, sq);                           // the 4 threads of a quad hold one 32-value block

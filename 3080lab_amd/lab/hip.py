@@ -20,6 +20,8 @@ _P = c_void_p
 _SIGS = {
     "q355_attn_decode_partials": [_P, _P, _P, _P, _P, c_int, c_int, c_int, c_int, c_double, _P, _P, _P, c_int, _P],
     "q355_mmq_attn_o_resid": [_P, _P, c_int, _P, c_int, _P, c_int, c_int, _P, _P, _P, c_int, _P],
+    "q355_attn_decode_partials_f16": [_P, _P, _P, _P, _P, c_int, c_int, c_int, c_int, c_double, _P, _P, c_int, _P],
+    "q355_gemm_f16_attn_o_resid": [_P, _P, c_int, _P, c_int, _P, c_int, c_int, _P, _P, c_int, _P],
     "q355_quant_q8_1": [_P, _P, _P, c_int, c_int, _P],
     "q355_rmsnorm_q8_1": [_P, _P, _P, _P, c_int, c_int, c_float, _P],
     "q355_gemv_q4_0_q8_1": [_P, _P, c_int, c_int, _P, _P, c_int, _P, _P, c_int, _P],

@@ -67,7 +67,7 @@ def pack_q4_i8(W, S):
 pack_q4_mma = pack_q4_i8
 
 
-# int8 path: up to this batch the attention merge runs inside the O product's staging (saves the merge
+# up to this batch the attention merge runs inside the O product's staging (int8 and fp16 paths) (saves the merge
 # launch: B = 8 step 1.391 -> 1.329 ms); above it the separate merge measured no slower
 MERGE_IN_O_MAX_B = 16
 
@@ -151,10 +151,19 @@ class BatchedDecoder:
         call("q355_gemm_f16_qkv_rope", ptr(W.qs), ptr(W.d), W.N, W.K, ptr(self.xh), B, ptr(L["qkv_b"]), ptr(m.cos),
              ptr(m.sin), ptr(self.pos), ptr(self.block_table), self.max_chunks, 1, ptr(self.kc[i]), ptr(self.vc[i]),
              ptr(self.q), c.NH, c.NKV)
-        call("q355_attn_decode_f16", ptr(self.q), ptr(self.kc[i]), ptr(self.vc[i]), ptr(self.pos),
-             ptr(self.block_table), self.max_chunks, c.NH, c.NKV, self.max_chunks, self.scale, ptr(self.part),
-             ptr(self.ah), B)
-        self._gemm(L["o"], self.ah, 6, yfix=self.h)
+        if B <= MERGE_IN_O_MAX_B:
+            # attention leaves split partials; the O product merges them per head while staging its activations
+            call("q355_attn_decode_partials_f16", ptr(self.q), ptr(self.kc[i]), ptr(self.vc[i]), ptr(self.pos),
+                 ptr(self.block_table), self.max_chunks, c.NH, c.NKV, self.max_chunks, self.scale, ptr(self.part),
+                 ptr(self.ah), B)
+            W = L["o"]
+            call("q355_gemm_f16_attn_o_resid", ptr(W.qs), ptr(W.d), W.N, ptr(self.part), self.max_chunks,
+                 ptr(self.pos), c.NH, c.NKV, ptr(self.ah), ptr(self.h), B)
+        else:
+            call("q355_attn_decode_f16", ptr(self.q), ptr(self.kc[i]), ptr(self.vc[i]), ptr(self.pos),
+                 ptr(self.block_table), self.max_chunks, c.NH, c.NKV, self.max_chunks, self.scale, ptr(self.part),
+                 ptr(self.ah), B)
+            self._gemm(L["o"], self.ah, 6, yfix=self.h)
         self._normh(L["ln2"])
         self._gemm(L["gu"], self.xh, 8, yh=self.mh)
         self._gemm(L["down"], self.mh, 6, yfix=self.h)

@@ -185,6 +185,22 @@ int q355_attn_decode_partials(const void* q, const void* kcache, const void* vca
                               const int32_t* block_table, int bt_stride, int nh, int nkv, int max_chunks, double scale,
                               double* part, int8_t* oq, void* ods, int T, void* stream);
 
+/* The fp16 batched path's attention without its merge launch: as q355_attn_decode_f16, but tokens whose context
+ * spans several 4-page splits leave only their split partials in part (for q355_gemm_f16_attn_o_resid); tokens
+ * of <= 256 positions are finished into oh [T][nh*128] fp16.
+ * Replaces the batched ATTN4 of scripts/qwen_batched_decode.py:156-187 (its combine moves into the O product). */
+int q355_attn_decode_partials_f16(const void* q, const void* kcache, const void* vcache, const int32_t* pos,
+                                  const int32_t* block_table, int bt_stride, int nh, int nkv, int max_chunks,
+                                  double scale, double* part, void* oh, int T, void* stream);
+
+/* O projection + residual of the fp16 batched path (T <= 16) with the attention merge in its activation staging:
+ * h[T][N] += Wo . fp16(merge(part)) per head (one K slice per head), reading oh for tokens that
+ * q355_attn_decode_partials_f16 finished itself. The activations are the bytes q355_attn_decode_f16 writes;
+ * the product is the fp16-weight arithmetic of q355_gemm_q4_0_f16 (epi 6) with its own K split. K = nh * 128.
+ * Replaces the batched combine + gemv_v2_source 'resid' for o (scripts/qwen_batched_decode.py:156-187). */
+int q355_gemm_f16_attn_o_resid(const uint8_t* qs, const void* d, int N, const double* part, int max_chunks,
+                               const int32_t* pos, int nh, int nkv, const void* oh, int64_t* h, int T, void* stream);
+
 /* O projection + residual of the batched int8 path with the attention merge in its activation staging:
  * h[T][N] += Wo . Q8_1(merge(part)) per head (one K slice per head), reading xq/xds for tokens that
  * q355_attn_decode_partials finished itself. The same bytes as q355_attn_decode's merge followed by

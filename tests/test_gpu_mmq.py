@@ -7,7 +7,7 @@ import pytest
 from lab import gguf
 from lab import qwen_batched as QB
 from lab import qwen_model as QM
-from lab.hip import call, ptr
+from lab.hip import HipError, call, ptr
 from oracle import model as OM
 from oracle import quant as OQ
 
@@ -397,3 +397,47 @@ def test_attn_partials_merge_in_o_product(cuda, T):
         sync()
         out.append(h.cpu().numpy())
     assert np.array_equal(out[0], out[1])
+
+
+@pytest.mark.parametrize("T", [3, 8, 16])
+def test_attn_partials_merge_in_o_product_f16(cuda, T):
+    """fp16 path: attention without its merge launch + the fp16 O product that merges the split partials per
+    head while staging (q355_attn_decode_partials_f16 + q355_gemm_f16_attn_o_resid) against attention with its
+    merge + the plain fp16 O product (q355_attn_decode_f16 + q355_gemm_q4_0_f16 epi 6). The activations are
+    the same fp16 bytes; the products differ only in how their fp32 partial sums are grouped over K (one head
+    per slice here), so the residual deltas agree to fp32 accumulation error (1e-5 of the largest), far
+    below one fp16 activation step of the merged output."""
+    import torch
+    c = QM.Config(L=1, V=1024)
+    mc = 36
+    rng = np.random.default_rng(100 + T)
+    kc = dev(rng.standard_normal((T * mc, c.NKV, 64, 128)).astype(np.float16))
+    vc = dev(rng.standard_normal((T * mc, c.NKV, 64, 128)).astype(np.float16))
+    bt = dev(rng.permutation(T * mc).astype(np.int32).reshape(T, mc))
+    q = dev((rng.standard_normal((T, c.NH * 128)) * 2).astype(np.float16))
+    pos_np = rng.integers(0, mc * 64, T).astype(np.int32)
+    pos_np[0] = 100                                    # one split, finished by the attention kernel
+    pos = dev(pos_np)
+    W, _ = mat(c.H, c.NH * 128, 78)
+    h0 = np.round(rng.standard_normal((T, c.H)) * QM.FIX_SCALE).astype(np.int64)
+    out = []
+    for fused in (True, False):
+        part = torch.full((T, c.NH, mc, 130), float("nan"), dtype=torch.float64, device=cuda)
+        oh = torch.zeros(T, c.NH * 128, dtype=torch.float16, device=cuda)
+        h = dev(h0.copy())
+        if fused:
+            call("q355_attn_decode_partials_f16", ptr(q), ptr(kc), ptr(vc), ptr(pos), ptr(bt), mc, c.NH, c.NKV, mc,
+                 1 / math.sqrt(128), ptr(part), ptr(oh), T)
+            call("q355_gemm_f16_attn_o_resid", ptr(W.qs), ptr(W.d), c.H, ptr(part), mc, ptr(pos), c.NH, c.NKV,
+                 ptr(oh), ptr(h), T)
+        else:
+            call("q355_attn_decode_f16", ptr(q), ptr(kc), ptr(vc), ptr(pos), ptr(bt), mc, c.NH, c.NKV, mc,
+                 1 / math.sqrt(128), ptr(part), ptr(oh), T)
+            call("q355_gemm_q4_0_f16", ptr(W.qs), ptr(W.d), c.H, c.NH * 128, ptr(oh), T, 6, None, ptr(h), None,
+                 None, None)
+        sync()
+        out.append((h.cpu().numpy() - h0) / QM.FIX_SCALE)
+    assert relerr(out[0], out[1]) < 1e-5
+    with pytest.raises(HipError):
+        call("q355_gemm_f16_attn_o_resid", ptr(W.qs), ptr(W.d), c.H, ptr(part), mc, ptr(pos), c.NH, c.NKV,
+             ptr(oh), ptr(h), 17)                        # T <= 16
