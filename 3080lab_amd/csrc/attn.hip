@@ -204,12 +204,12 @@ __device__ __forceinline__ void attn_out8(const AttnArgs& a, int j, int h, int d
     }
     return;
   }
-  float df;
+  float df, d32;
   int sq;
-  const uint2 q = q8_1_x8(o, df, sq);                  // the 4 threads of a quad hold one 32-value block
+  const uint2 q = q8_1_x8(o, df, sq, d32);             // the 4 threads of a quad hold one 32-value block
   if (live) {
     *(uint2*)(a.oq + e) = q;
-    if ((dg & 3) == 0) a.ods[e / 32] = __halves2half2(__float2half_rn(df), __float2half_rn(df * (float)sq));
+    if ((dg & 3) == 0) a.ods[e / 32] = __halves2half2(__float2half_rn(d32), q8_s16(d32, sq));
   }
 }
 

@@ -10,7 +10,8 @@
 //   A operand of v_mfma_i32_16x16x32_i8 (lane = row, 8 bytes per k-group).
 //   Q8_1 activations X [T, K]:
 //     xq  int8  [T][K]
-//     xds half2 [T][K/32] = (d, s): d = fp16(amax/127), s = fp16(d * sum q) (llama.cpp block_q8_1 fields)
+//     xds half2 [T][K/32] = (d, s): d = fp16(amax/127), s = fp16(d * sum q) (llama.cpp block_q8_1 fields;
+//                                  the quantizer rule is q8_code's)
 //   Kernels use the exact integer block correction dot - 8 * sum(q) (sum recomputed from xq), not s.
 #pragma once
 #include <hip/hip_runtime.h>
@@ -111,9 +112,19 @@ __device__ __forceinline__ float wave_sum_fast(float v) {
   return v + __shfl_xor(v, 32, 64);
 }
 
-// Q8_1 of 8 consecutive values held by one lane; 4 lanes form a 32-block (lane groups aligned to 4).
-// Bit-exact with the oracle (d = fp16(amax/127), q = roundf(x / d16) clamped, 0 when d16 == 0).
-// Returns the 8 int8 packed in a uint2; d (as float) and the block's sum of q through the references.
+// Q8_1 rule of every quantizer in the library (and of the oracle): the reference's QUANT_Q8
+// (lab/qwen_batched.py:1032-1033): d = amax / 127 and q = x / d, both IEEE fp32 divisions, q rounded half to
+// even (__float2int_rn), q = 0 when d == 0. |x / d| <= 127 (1 + 2^-23), so no clamp is needed. The block is
+// stored in llama.cpp's block_q8_1 form: d as fp16 (the scale every product uses) and s = fp16(d * sum q)
+// with the fp32 d (llama.cpp quantize_row_q8_1).
+__device__ __forceinline__ float q8_scale(float amax) { return amax / 127.0f; }
+__device__ __forceinline__ int q8_code(float x, float d32) {
+  const float dv = d32 != 0.0f ? d32 : 1.0f;   // branch-free: a dead block divides by 1 and selects 0
+  const int q = (int)__builtin_rintf(x / dv);
+  return d32 != 0.0f ? q : 0;
+}
+__device__ __forceinline__ __half q8_s16(float d32, int sq) { return __float2half_rn(d32 * (float)sq); }
+
 // f64 -> fp16 with ONE round to nearest even (no intermediate fp32 rounding, which can land exactly on an
 // fp16 midpoint and then break the tie the other way).
 __device__ __forceinline__ __half half_rn(double v) {
@@ -121,29 +132,31 @@ __device__ __forceinline__ __half half_rn(double v) {
   return *reinterpret_cast<const __half*>(&h);
 }
 
-__device__ __forceinline__ uint2 q8_1_x8(const float (&x)[8], float& df, int& sq) {
+// Q8_1 of 8 consecutive values held by one lane; 4 lanes form a 32-block (lane groups aligned to 4).
+// Returns the 8 int8 packed in a uint2; df = the fp16 d as float, sq = the block's sum of q, d32 = the fp32 d.
+__device__ __forceinline__ uint2 q8_1_x8(const float (&x)[8], float& df, int& sq, float& d32) {
   float amax = 0.f;
 #pragma unroll
   for (int u = 0; u < 8; ++u) amax = fmaxf(amax, fabsf(x[u]));
   amax = quad_max(amax);
-  df = __half2float(__float2half_rn(amax / 127.0f));
-  const bool live = df != 0.0f;
-  const float dv = live ? df : 1.0f;   // branch-free: a dead block divides by 1 and selects 0
+  d32 = q8_scale(amax);
+  df = __half2float(__float2half_rn(d32));
   int q[8];
   int s = 0;
 #pragma unroll
   for (int u = 0; u < 8; ++u) {
-    int v = (int)roundf(x[u] / dv);
-    v = v > 127 ? 127 : (v < -127 ? -127 : v);
-    v = live ? v : 0;
-    q[u] = v;
-    s += v;
+    q[u] = q8_code(x[u], d32);
+    s += q[u];
   }
   sq = quad_isum(s);
   uint2 pk;
   pk.x = (q[0] & 255) | ((q[1] & 255) << 8) | ((q[2] & 255) << 16) | ((unsigned)(q[3] & 255) << 24);
   pk.y = (q[4] & 255) | ((q[5] & 255) << 8) | ((q[6] & 255) << 16) | ((unsigned)(q[7] & 255) << 24);
   return pk;
+}
+__device__ __forceinline__ uint2 q8_1_x8(const float (&x)[8], float& df, int& sq) {
+  float d32;
+  return q8_1_x8(x, df, sq, d32);
 }
 
 // f64 wave reductions (the batch-1 decode path accumulates in f64 so that every Q8_1 quantizer input
@@ -216,20 +229,13 @@ __device__ __forceinline__ int g32_isum(int v) {
   return v + __shfl_xor(v, 16, 64);
 }
 
-// Q8_1 of one value inside a group of 32 lanes that hold one block (lane group aligned to 32).
-// Returns q; writes (d, s) through `ds` from the group's first lane. Bit-exact with the oracle:
-// d = fp16(amax / 127) (IEEE fp32 divide), q = roundf(x / d16) clamped to +-127, q = 0 when d16 == 0.
+// Q8_1 of one value inside a group of 32 lanes that hold one block (lane group aligned to 32), by the rule
+// of q8_code. Returns q; writes (d, s) through `ds` from the group's first lane.
 __device__ __forceinline__ int q8_1_lane32(float x, half2* ds, bool leader) {
-  float amax = g32_max(fabsf(x));
-  __half d16 = __float2half_rn(amax / 127.0f);
-  float df = __half2float(d16);
-  int q = 0;
-  if (df != 0.0f) {
-    q = (int)roundf(x / df);
-    q = q > 127 ? 127 : (q < -127 ? -127 : q);
-  }
-  int sq = g32_isum(q);
-  if (leader) *ds = __halves2half2(d16, __float2half_rn(df * (float)sq));
+  const float d32 = q8_scale(g32_max(fabsf(x)));
+  const int q = q8_code(x, d32);
+  const int sq = g32_isum(q);
+  if (leader) *ds = __halves2half2(__float2half_rn(d32), q8_s16(d32, sq));
   return q;
 }
 

@@ -272,8 +272,7 @@ __global__ void __launch_bounds__(512) k_attn_prefill(const PrefillAttnArgs a) {
             amax = fmaxf(amax, fabsf(x[h][v]));
           }
         amax = col4_max(amax);
-        const __half d16 = __float2half_rn(amax / 127.0f);
-        const float df = __half2float(d16);
+        const float d32 = q8_scale(amax);
         int sq = 0;
         unsigned pk[2];
 #pragma unroll
@@ -281,11 +280,7 @@ __global__ void __launch_bounds__(512) k_attn_prefill(const PrefillAttnArgs a) {
           pk[h] = 0;
 #pragma unroll
           for (int v = 0; v < 4; ++v) {
-            int q = 0;
-            if (df != 0.0f) {
-              q = (int)roundf(x[h][v] / df);
-              q = q > 127 ? 127 : (q < -127 ? -127 : q);
-            }
+            const int q = q8_code(x[h][v], d32);
             sq += q;
             pk[h] |= (unsigned)(q & 255) << (8 * v);
           }
@@ -296,7 +291,7 @@ __global__ void __launch_bounds__(512) k_attn_prefill(const PrefillAttnArgs a) {
           *(unsigned*)(o + 32 * bk + 4 * lg) = pk[0];
           *(unsigned*)(o + 32 * bk + 16 + 4 * lg) = pk[1];
           if (lg == 0)
-            a.ods[((size_t)qi[cb] * nq + hq * HD) / 32 + bk] = __halves2half2(d16, __float2half_rn(df * (float)sq));
+            a.ods[((size_t)qi[cb] * nq + hq * HD) / 32 + bk] = __halves2half2(__float2half_rn(d32), q8_s16(d32, sq));
         }
       }
     } else if (qi[cb] < a.P) {

@@ -664,12 +664,12 @@ __global__ void __launch_bounds__(256) k_rmsnorm_fix_q8_1(const long long* __res
 #pragma unroll
     for (int u = 0; u < 8; ++u) x[u] = (float)(hv[u] * r * (double)wv[u]);
   }
-  float df;
+  float df, d32;
   int sq;
-  const uint2 pk = q8_1_x8(x, df, sq);              // H / 8 % 4 == 0: quads stay whole
+  const uint2 pk = q8_1_x8(x, df, sq, d32);         // H / 8 % 4 == 0: quads stay whole
   if (act) {
     *(uint2*)(xq + (size_t)tok * H + 8 * g) = pk;
-    if ((g & 3) == 0) xds[(size_t)tok * (H / 32) + (g >> 2)] = __halves2half2(__float2half_rn(df), __float2half_rn(df * (float)sq));
+    if ((g & 3) == 0) xds[(size_t)tok * (H / 32) + (g >> 2)] = __halves2half2(__float2half_rn(d32), q8_s16(d32, sq));
   }
 }
 

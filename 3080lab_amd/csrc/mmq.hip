@@ -164,20 +164,19 @@ __device__ __forceinline__ void stage_attn(const GemvArgs& a, int8_t* xq, float*
 }
 
 // Q8_1 of the 8 fp32 values this lane holds of one 32-block whose 4 quarters sit in lanes l, l ^ 16, l ^ 32,
-// l ^ 48 (the MFMA B-operand layout): d = fp16(amax / 127), q = round(x / d) (as a product with 1 / d).
+// l ^ 48 (the MFMA B-operand layout), by the rule of q8_code; df = the fp16 d as float.
 __device__ __forceinline__ long q8_1_mfma8(const float (&x)[8], float& df) {
   float amax = 0.f;
 #pragma unroll
   for (int u = 0; u < 8; ++u) amax = fmaxf(amax, fabsf(x[u]));
   amax = fmaxf(amax, __shfl_xor(amax, 16));
   amax = fmaxf(amax, __shfl_xor(amax, 32));
-  df = __half2float(__float2half_rn(amax / 127.0f));
-  const float inv = df != 0.0f ? 1.0f / df : 0.0f;
+  const float d32 = q8_scale(amax);
+  df = __half2float(__float2half_rn(d32));
   unsigned lo = 0, hi = 0;
 #pragma unroll
   for (int u = 0; u < 8; ++u) {
-    int v = (int)roundf(x[u] * inv);
-    v = v > 127 ? 127 : (v < -127 ? -127 : v);
+    const int v = q8_code(x[u], d32);
     if (u < 4) lo |= (unsigned)(v & 255) << (8 * u);
     else hi |= (unsigned)(v & 255) << (8 * (u - 4));
   }
@@ -714,20 +713,12 @@ __global__ void __launch_bounds__(256) k_mmq_tile(const GemvArgs a) {
       }
       amax = fmaxf(amax, __shfl_xor(amax, 16));
       amax = fmaxf(amax, __shfl_xor(amax, 32));
-      const __half d16 = __float2half_rn(amax / 127.0f);
-      const float df = __half2float(d16);
-      const float inv = df != 0.0f ? 1.0f / df : 0.0f;   // one division per token; x * (1 / d) per value
+      const float d32 = q8_scale(amax);
       int sq = 0;
       unsigned short pk[4];
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
-        int q0 = 0, q1 = 0;
-        if (df != 0.0f) {
-          q0 = (int)roundf(o[t][0] * inv);
-          q1 = (int)roundf(o[t][1] * inv);
-          q0 = q0 > 127 ? 127 : (q0 < -127 ? -127 : q0);
-          q1 = q1 > 127 ? 127 : (q1 < -127 ? -127 : q1);
-        }
+        const int q0 = q8_code(o[t][0], d32), q1 = q8_code(o[t][1], d32);
         sq += q0 + q1;
         pk[t] = (unsigned short)((q0 & 255) | ((q1 & 255) << 8));
       }
@@ -738,7 +729,7 @@ __global__ void __launch_bounds__(256) k_mmq_tile(const GemvArgs a) {
         int8_t* dst = a.oq + (size_t)tok * Nout + ob * 32 + 2 * lg;
 #pragma unroll
         for (int t = 0; t < 4; ++t) *(unsigned short*)(dst + 8 * t) = pk[t];
-        if (lg == 0) a.ods[(size_t)tok * (Nout / 32) + ob] = __halves2half2(d16, __float2half_rn(df * (float)sq));
+        if (lg == 0) a.ods[(size_t)tok * (Nout / 32) + ob] = __halves2half2(__float2half_rn(d32), q8_s16(d32, sq));
       }
     }
   }

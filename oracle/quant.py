@@ -6,10 +6,10 @@ Restates:
   * the Q4_0 quantizer of BASELINE config 0 (llama.cpp quantize_row_q4_0_ref semantics, not in
     the reference tree): m = the signed value of max |x| (first on ties), d = m / -8 in fp32,
     stored fp16, q = clamp(round(x / d) + 8, 0, 15) with round = half away from zero, q = 8 when d = 0;
-  * the Q8_1 activation quantizer (the reference's int8 quantizer QUANT_Q8,
-    lab/qwen_batched.py:1016-1041, with fp16 d as llama.cpp block_q8_1): d = amax / 127 in fp32,
-    stored fp16; q = round(x / d16) half away from zero, clamped to [-127, 127], 0 when d16 = 0;
-    s = fp16(d16 * sum(q)) (llama.cpp's block sum field);
+  * the Q8_1 activation quantizer: the rule is the reference's QUANT_Q8 (lab/qwen_batched.py:1032-1033):
+    d = amax / 127 and r = x / d, both IEEE fp32 divisions, q = r rounded half to even (__float2int_rn),
+    q = 0 when d = 0. The block is stored as BASELINE config 0 and llama.cpp's block_q8_1 store it
+    (quantize_row_q8_1): d as fp16 (the scale every product uses), s = fp16(d * sum(q)) with the fp32 d;
   * the per-block int32 dot and the Q4_0 offset correction of the reference's int8 MMQ
     (lab/qwen_batched.py:1099-1101, 1237-1243): per 32-block b,
     dot_b = sum_i q_w,i (0..15) * q_x,i (exact int32), y += d_w * d_x * (dot_b - 8 * sum_i q_x,i).
@@ -63,22 +63,30 @@ def dequant_q4_0(b: np.ndarray, shape) -> np.ndarray:
     return (d[:, None] * (q.astype(np.float32) - 8)).reshape(shape)
 
 
+def round_half_even(v: np.ndarray) -> np.ndarray:
+    """CUDA __float2int_rn / rintf: nearest integer, halves to the even neighbour (numpy rint).
+    pinned by: tests/test_oracle.py::test_round_half_even (hand cases 0.5, 1.5, 2.5, -0.5, -2.5)."""
+    return np.rint(np.asarray(v, dtype=np.float32))
+
+
 def quantize_q8_1(x: np.ndarray):
-    """fp32 [T, K] -> (qs int8 [T, K], d fp16 [T, K/32], s fp16 [T, K/32]).
-    pinned by: known-answer blocks (amax element -> +-127, all-zero block -> q = 0, d = 0), the bound
-    |x - d q| <= d/2 for every element, and brute-force per-element loops on tiny inputs."""
+    """fp32 [T, K] -> (qs int8 [T, K], d fp16 [T, K/32], s fp16 [T, K/32]) by the rule above
+    (lab/qwen_batched.py:1032-1033 for d and q; llama.cpp block_q8_1 for the stored d and s).
+    pinned by: hand blocks where the rules differ (a half-integer x / d rounds to even; a value whose fp32
+    quotient x / d and x / fp16(d) round to different codes), the amax element -> +-127, an all-zero block
+    -> q = 0, d = 0, the bound |x - d q| <= d/2, and per-element brute-force loops in Python floats
+    (tests/test_oracle.py)."""
     x = np.asarray(x, dtype=np.float32)
     T, K = x.shape
     xb = x.reshape(T, K // QK, QK)
     amax = np.abs(xb).max(axis=2)
-    d16 = (amax / np.float32(127.0)).astype(np.float32).astype(np.float16)
-    df = d16.astype(np.float32)
+    d32 = (amax / np.float32(127.0)).astype(np.float32)
     with np.errstate(divide="ignore", invalid="ignore"):
-        r = np.where(df[..., None] != 0, xb / df[..., None], np.float32(0.0)).astype(np.float32)
-    q = np.clip(round_half_away(r), -127, 127).astype(np.int8)
+        r = np.where(d32[..., None] != 0, xb / d32[..., None], np.float32(0.0)).astype(np.float32)
+    q = round_half_even(r).astype(np.int8)
     sq = q.astype(np.int32).sum(axis=2)
-    s = (df * sq.astype(np.float32)).astype(np.float16)
-    return q.reshape(T, K), d16, s
+    s = (d32 * sq.astype(np.float32)).astype(np.float16)
+    return q.reshape(T, K), d32.astype(np.float16), s
 
 
 def dequant_q8_1(q: np.ndarray, d: np.ndarray) -> np.ndarray:

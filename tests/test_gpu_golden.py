@@ -2,9 +2,9 @@
 
 Covers BASELINE config 0 (the 8960 x 1536 GEMV: per-block int32 dots bit-exact, y within 1e-3) and
 config 2 (the full 28-layer model, 128-token prompt, 256 greedy tokens). Greedy parity is checked
-teacher-forced: at every step the GPU is fed the oracle's token, and its argmax must equal the oracle's
-wherever the oracle's top-2 logit margin is not a near-tie (< NEAR_TIE); free-running agreement is
-reported as well.
+free-running over all 256 steps (the reference's check), and teacher-forced: at every step the GPU is fed the
+oracle's token, and its argmax must equal the oracle's wherever the oracle's top-2 logit margin is not a
+near-tie (< NEAR_TIE).
 """
 import hashlib
 import json
@@ -21,6 +21,7 @@ pytestmark = pytest.mark.gpu
 GOLD = Path(__file__).resolve().parent / "golden"
 META = json.loads((GOLD / "golden.json").read_text())
 NEAR_TIE = 1e-2
+FREE_TIE = 1e-6
 
 
 def sha(a):
@@ -112,11 +113,15 @@ def test_config2_greedy_256(cuda):
     pos0 = dec.pos.clone()
     forced = _teacher_forced(dec, m["prompt"][-1], m["tokens"])
     _check(forced, m["tokens"], m["margins"], "config 2")
-    # free running from the same state: count the agreeing prefix (reported, not asserted)
+    # free running from the same state (the reference's own check, scripts/qwen_e2e.py:240-243): the batch-1
+    # path reproduces the oracle's f64 logits to ~1e-12, so every one of the 256 tokens must agree unless the
+    # oracle's top-2 margin at the first difference is below FREE_TIE (far above that error, far below any
+    # margin of this run, whose smallest is ~4e-4)
     dec.pos.copy_(pos0)
     dec.tok.fill_(int(m["prompt"][-1]))
     dec.graph.replay()
     free = dec.generate(256)[0].tolist()
     agree = next((i for i, (x, y) in enumerate(zip(free, m["tokens"])) if x != y), 256)
-    print(f"config 2: teacher-forced argmax agrees at every non-tie step; free-running agreement {agree}/256 "
-          f"(first oracle near-tie at step {next((i for i, x in enumerate(m['margins']) if x < NEAR_TIE), 256)})")
+    print(f"config 2: free-running agreement {agree}/256 (smallest oracle margin {min(m['margins']):.3g})")
+    assert agree == 256 or m["margins"][agree] < FREE_TIE, \
+        f"config 2 free-running: step {agree} differs at oracle margin {m['margins'][agree]:.3g}"

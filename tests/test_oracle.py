@@ -76,29 +76,70 @@ def test_q4_0_decoder_known_bytes():
     assert OQ.dequant_q4_0(b, (32,)).tolist() == [0.5 * (v - 8) for v in q[0].tolist()]
 
 
+def test_round_half_even():
+    v = np.array([0.5, 1.5, 2.5, -0.5, -1.5, -2.5, 0.49999997, 126.5, -124.5], np.float32)
+    assert OQ.round_half_even(v).tolist() == [0, 2, 2, -0, -2, -2, 0, 126, -124]
+
+
+def _rn32(fr: Fraction) -> Fraction:
+    """Exact rational -> the nearest float32 (ties to even significand), decided by exact comparisons."""
+    f = np.float32(float(fr))
+    cands = [f, np.nextafter(f, np.float32(np.inf)), np.nextafter(f, np.float32(-np.inf))]
+    best = min(cands, key=lambda c: (abs(Fraction(float(c)) - fr), int(np.array(c).view(np.uint32)) & 1))
+    return Fraction(float(best))
+
+
+def _q8_expect(block):
+    """Q8_1 of one 32-value block from its definition (lab/qwen_batched.py:1032-1033): d = RN32(amax / 127),
+    q = round-half-even(RN32(x / d)), 0 when d = 0; computed with exact rationals."""
+    amax = max(abs(Fraction(float(v))) for v in block)
+    d = _rn32(amax / 127)
+    if d == 0:
+        return [0] * 32, d
+    return [round(_rn32(Fraction(float(v)) / d)) for v in block], d   # round() on a Fraction: half to even
+
+
 def test_q8_1_known_blocks():
-    x = np.zeros((1, 96), np.float32)
+    x = np.zeros((1, 160), np.float32)
     x[0, :32] = np.linspace(-1.0, 2.0, 32, dtype=np.float32)    # amax 2 at the last element
-    x[0, 64:96] = -1e-9                                           # d underflows to fp16 zero
+    x[0, 64:96] = -1e-9                                           # d underflows to fp16 zero (fp32 d does not)
+    x[0, 96:128] = np.float32(127.0)                              # d = 1 exactly: half-integers round to even
+    x[0, 96:105] = [2.5, -2.5, 0.5, -0.5, 1.5, 126.5, -3.5, 4.5, 0.0]
+    x[0, 128:160] = np.float32(1.0)                               # d = fp32(1/127): fp16(d) differs from it
+    x[0, 128] = np.float32(-0.9803)
     q, d, s = OQ.quantize_q8_1(x)
-    d16 = np.float16(np.float32(2.0) / np.float32(127))
-    assert d[0, 0] == d16 and q[0, 31] == 127
+    assert q[0, 31] == 127 and d[0, 0] == np.float16(np.float32(2.0) / np.float32(127))
     assert d[0, 1] == 0 and (q[0, 32:64] == 0).all() and s[0, 1] == 0
-    assert d[0, 2] == 0 and (q[0, 64:96] == 0).all()
-    # exact rational check of q for every element of block 0
-    for i in range(32):
-        r = Fraction(float(x[0, i])) / Fraction(float(d16))
-        want = math.floor(r + Fraction(1, 2)) if r >= 0 else -math.floor(-r + Fraction(1, 2))
-        assert q[0, i] == max(-127, min(127, want))
-    assert s[0, 0] == np.float16(np.float32(d16) * np.float32(q[0, :32].astype(np.int32).sum()))
+    assert d[0, 2] == 0 and (q[0, 64:96] == -127).all()        # the rule divides by the fp32 d (nonzero)
+    assert q[0, 96:105].tolist() == [2, -2, 0, 0, 2, 126, -4, 4, 0]   # half away from zero would give 3, -3, 1, ...
+    # x / fp32 d = -124.498 -> -124; x / fp16 d = -124.506 would give -125: the divisor is the fp32 d
+    assert q[0, 128] == -124
+    for b in range(5):
+        want, d32 = _q8_expect(x[0, 32 * b:32 * b + 32])
+        assert q[0, 32 * b:32 * b + 32].tolist() == want
+        assert d[0, b] == np.float16(float(d32))
+        # llama.cpp block_q8_1: s = fp16(d * sum q) with the fp32 d
+        assert s[0, b] == np.float16(np.float32(float(d32)) * np.float32(sum(want)))
+
+
+def test_q8_1_bruteforce_random():
+    rng = np.random.default_rng(5)
+    x = (rng.standard_normal((3, 96)) * rng.choice([1e-3, 1.0, 40.0], (3, 1))).astype(np.float32)
+    q, d, _ = OQ.quantize_q8_1(x)
+    for t in range(3):
+        for b in range(3):
+            want, d32 = _q8_expect(x[t, 32 * b:32 * b + 32])
+            assert q[t, 32 * b:32 * b + 32].tolist() == want
+            assert d[t, b] == np.float16(float(d32))
 
 
 def test_q8_1_error_bound():
     x = np.random.default_rng(1).standard_normal((8, 1536)).astype(np.float32)
     q, d, _ = OQ.quantize_q8_1(x)
-    back = OQ.dequant_q8_1(q, d)
-    dd = np.repeat(d.astype(np.float32), 32, axis=1)
-    assert (np.abs(back - x) <= 0.5 * dd * (1 + 1e-3) + 1e-12).all()
+    d32 = np.abs(x.reshape(8, -1, 32)).max(axis=2).astype(np.float64) / 127    # the divisor (fp32 d, ~1 ulp)
+    back = q.astype(np.float64) * np.repeat(d32, 32, axis=1)
+    assert (np.abs(back - x) <= 0.5 * np.repeat(d32, 32, axis=1) * (1 + 1e-5)).all()
+    assert (np.abs(d.astype(np.float64) - d32) <= d32 * 2.0 ** -11).all()        # stored d = fp16 of it
     assert np.abs(q).max() == 127
 
 
