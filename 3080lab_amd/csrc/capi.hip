@@ -2,6 +2,7 @@
 #include <cstdio>
 #include <cstring>
 #include <cstdarg>
+#include <mutex>
 
 #include "../../include/qwen355.h"
 #include "common.h"
@@ -318,6 +319,66 @@ extern "C" int q355_attn_decode(const void* q, const void* kcache, const void* v
   if (!oq) return Q355_OK;
   hipLaunchKernelGGL(k_attn_merge, dim3(T, nh), dim3(64), 0, s, a);
   return launched("attn_merge");
+}
+
+// ------------------------------------------------------------------------------------------------
+// Allocation-free batched decode attention (q355_attn_decode with fp32 = 1): the split partials live in a
+// file-scope device array. Each GPU holds its own copy at its own address, looked up once per device with
+// hipGetSymbolAddress; host code uses only that address, never the array's name. Calls that overlap on one
+// GPU share the array and race; the kernels need no initial contents (each token's merge reads only the
+// splits its own attention workgroups wrote in the same call).
+static constexpr size_t NOALLOC_SCRATCH_BYTES = (size_t)4 << 20;
+static __device__ __align__(256) float scratch[NOALLOC_SCRATCH_BYTES / sizeof(float)];
+static constexpr int NOALLOC_MAX_DEVICES = 64;
+static float* g_scratch[NOALLOC_MAX_DEVICES];
+static std::mutex g_scratch_mu;
+
+static int scratch_for_current_device(float** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail((int)e, "attn_decode_noalloc: hipGetDevice: %s", hipGetErrorString(e));
+  REQUIRE(dev >= 0 && dev < NOALLOC_MAX_DEVICES, "attn_decode_noalloc: device %d >= %d", dev, NOALLOC_MAX_DEVICES);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return fail(e != hipSuccess ? (int)e : Q355_EINVAL, "attn_decode_noalloc: hipGetSymbolAddress: %s",
+                  hipGetErrorString(e));
+    g_scratch[dev] = (float*)p;
+  }
+  *out = g_scratch[dev];
+  return Q355_OK;
+}
+
+extern "C" int64_t q355_attn_decode_noalloc_max_bytes(void) { return (int64_t)NOALLOC_SCRATCH_BYTES; }
+
+extern "C" int q355_attn_decode_noalloc(const void* q, const void* kcache, const void* vcache, const int32_t* pos,
+                                        const int32_t* block_table, int bt_stride, int nh, int nkv, int max_chunks,
+                                        double scale, int8_t* oq, void* ods, float* o32, int T, void* stream) {
+  REQUIRE(q && kcache && vcache && pos && block_table && oq && ods, "attn_decode_noalloc: null pointer");
+  REQUIRE(nh > 0 && nkv > 0 && nh % nkv == 0 && nh / nkv <= 16, "attn_decode_noalloc: nh=%d nkv=%d", nh, nkv);
+  REQUIRE(max_chunks > 0 && max_chunks <= bt_stride && max_chunks <= 64,
+          "attn_decode_noalloc: max_chunks=%d bt_stride=%d", max_chunks, bt_stride);
+  REQUIRE(T > 0 && T <= 65535, "attn_decode_noalloc: T=%d", T);
+  // split partials: [T][nkv][ceil(max_chunks / 4)][G] (o[128], M, L) fp32
+  const size_t need = (size_t)T * nh * ((max_chunks + 3) / 4) * (HD + 2) * sizeof(float);
+  REQUIRE(need <= NOALLOC_SCRATCH_BYTES,
+          "attn_decode_noalloc: T=%d nh=%d max_chunks=%d need %zu bytes of split partials, the fixed scratch holds %zu",
+          T, nh, max_chunks, need, NOALLOC_SCRATCH_BYTES);
+  float* ws = nullptr;
+  if (int e = scratch_for_current_device(&ws)) return e;
+  AttnArgs a = {};
+  a.q = (const __half*)q; a.kcache = (const __half*)kcache; a.vcache = (const __half*)vcache;
+  a.pos = pos; a.block_table = block_table; a.bt_stride = bt_stride; a.nh = nh; a.nkv = nkv;
+  a.max_chunks = max_chunks; a.scale = scale; a.part = (double*)ws;
+  a.oq = oq; a.ods = (half2*)ods; a.o32 = o32;
+  hipStream_t s = (hipStream_t)stream;
+  hipLaunchKernelGGL(k_attn_decode_mfma<ATTN_KW>, dim3(nkv * ((max_chunks + 3) / 4), T), dim3(4 * 64 / ATTN_KW * 64), 0,
+                     s, a);
+  if (int e = launched("attn_decode_noalloc")) return e;
+  hipLaunchKernelGGL(k_attn_merge_split, dim3(nkv, T), dim3(256), 0, s, a);
+  return launched("attn_decode_noalloc merge");
 }
 
 extern "C" int q355_attn_decode_f16(const void* q, const void* kcache, const void* vcache, const int32_t* pos,

@@ -20,6 +20,8 @@ _P = c_void_p
 _SIGS = {
     "q355_attn_decode_partials": [_P, _P, _P, _P, _P, c_int, c_int, c_int, c_int, c_double, _P, _P, _P, c_int, _P],
     "q355_mmq_attn_o_resid": [_P, _P, c_int, _P, c_int, _P, c_int, c_int, _P, _P, _P, c_int, _P],
+    "q355_attn_decode_noalloc": [_P, _P, _P, _P, _P, c_int, c_int, c_int, c_int, c_double, _P, _P, _P, c_int, _P],
+    "q355_attn_decode_noalloc_max_bytes": [],
     "q355_attn_decode_partials_f16": [_P, _P, _P, _P, _P, c_int, c_int, c_int, c_int, c_double, _P, _P, c_int, _P],
     "q355_gemm_f16_attn_o_resid": [_P, _P, c_int, _P, c_int, _P, c_int, c_int, _P, _P, c_int, _P],
     "q355_quant_q8_1": [_P, _P, _P, c_int, c_int, _P],
@@ -60,7 +62,7 @@ _SIGS = {
                                c_int, c_int, _P],
 }
 # entry points returning something other than an int status
-_VALUE_FUNCS = {"q355_head_nparts", "q355_mmq_nparts", "q355_mega_ws_bytes", "q355_mega_layer_bytes",
+_VALUE_FUNCS = {"q355_attn_decode_noalloc_max_bytes", "q355_head_nparts", "q355_mmq_nparts", "q355_mega_ws_bytes", "q355_mega_layer_bytes",
                 "q355_attn_prefill_ws_bytes"}
 
 _lib = None
@@ -84,7 +86,7 @@ def lib():
         for name, args in _SIGS.items():
             f = getattr(L, name)
             f.argtypes = args
-            f.restype = ctypes.c_int64 if name.endswith("_ws_bytes") else c_int
+            f.restype = ctypes.c_int64 if name.endswith(("_ws_bytes", "_max_bytes")) else c_int
         _lib = L
     return _lib
 

@@ -128,6 +128,18 @@ int q355_attn_decode(const void* q, const void* kcache, const void* vcache, cons
                      const int32_t* block_table, int bt_stride, int nh, int nkv, int max_chunks, double scale,
                      double* part, int8_t* oq, void* ods, float* o32, int T, int fp32, void* stream);
 
+/* Allocation-free form of q355_attn_decode with fp32 = 1, for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). No counterpart in the
+ * reference. The fp32 split partials go to a fixed device array inside the library (one per GPU, held until the
+ * process ends) instead of a caller buffer; it calls no hipMalloc/hipFree. Limit:
+ * T * nh * ceil(max_chunks / 4) * 130 * 4 bytes <= q355_attn_decode_noalloc_max_bytes() (4 MiB), else
+ * Q355_EINVAL. Calls that overlap on one GPU share the array and race. Outputs and the other arguments as
+ * q355_attn_decode; GQA group nh/nkv <= 16. */
+int64_t q355_attn_decode_noalloc_max_bytes(void);
+int q355_attn_decode_noalloc(const void* q, const void* kcache, const void* vcache, const int32_t* pos,
+                             const int32_t* block_table, int bt_stride, int nh, int nkv, int max_chunks,
+                             double scale, int8_t* oq, void* ods, float* o32, int T, void* stream);
+
 /* Fused attention merge + Q8_1 + O-projection GEMV + residual: h[T][N] += Wo . Q8_1(merge(part))
  * (3 K slices of nh/3 heads, fixed-point atomics). part / max_chunks / pos as written by
  * q355_attn_decode; nh % 3 == 0, K = nh * 128 <= 1536.
