@@ -11,97 +11,130 @@ Added for this build:
 """
 from __future__ import annotations
 
-import struct
 from dataclasses import dataclass
 from pathlib import Path
 
 import numpy as np
 
-# ggml type id -> (name, block size in elements, bytes per block)
-GGML = {0: ("F32", 1, 4), 1: ("F16", 1, 2), 2: ("Q4_0", 32, 18), 8: ("Q8_0", 32, 34), 14: ("Q6_K", 256, 210)}
-# GGUF metadata scalar type id -> struct format
-_FMT = {0: "<B", 1: "<b", 2: "<H", 3: "<h", 4: "<I", 5: "<i", 6: "<f", 7: "<?", 10: "<Q", 11: "<q", 12: "<d"}
-_T_STRING, _T_ARRAY = 8, 9
+# ------------------------------------------------------------------------------------------------
+# GGUF container (format as published with ggml: little-endian header "GGUF", u32 version, u64 tensor
+# count, u64 key/value count; key/value pairs; tensor infos; padding to general.alignment; tensor data).
+# The whole file is memory-mapped once and parsed with a byte cursor.
+
+# tensor element types this build decodes: type id -> (element count per block, bytes per block)
+_BLOCK = {0: (1, 4), 1: (1, 2), 2: (32, 18), 14: (256, 210)}
+_TYPE_NAME = {0: "F32", 1: "F16", 2: "Q4_0", 14: "Q6_K"}
+# metadata value types with a fixed width: id -> numpy dtype
+_META_SCALAR = {0: np.uint8, 1: np.int8, 2: np.uint16, 3: np.int16, 4: np.uint32, 5: np.int32,
+                6: np.float32, 7: np.bool_, 10: np.uint64, 11: np.int64, 12: np.float64}
+_META_STRING, _META_ARRAY = 8, 9
 
 
 @dataclass
 class Tensor:
+    """One entry of the tensor directory. dims are in GGUF order: dims[0] varies fastest (the K axis of a
+    row-major [N, K] matrix); offset is relative to the start of the data section."""
     name: str
-    dims: tuple      # ggml order: dims[0] is the contiguous (K) axis
+    dims: tuple
     type: int
     offset: int
 
 
-class _Reader:
-    def __init__(self, f):
-        self.f = f
+class _Cursor:
+    """Sequential little-endian decoding over a uint8 buffer."""
 
-    def unpack(self, fmt):
-        return struct.unpack(fmt, self.f.read(struct.calcsize(fmt)))
+    def __init__(self, buf: np.ndarray):
+        self.buf, self.pos = buf, 0
 
-    def string(self):
-        (n,) = self.unpack("<Q")
-        return self.f.read(n).decode("utf-8", "replace")
+    def take(self, n: int) -> np.ndarray:
+        if self.pos + n > self.buf.size:
+            raise ValueError("GGUF: truncated file")
+        out = self.buf[self.pos:self.pos + n]
+        self.pos += n
+        return out
 
-    def value(self, typ):
-        if typ == _T_STRING:
-            return self.string()
-        if typ == _T_ARRAY:
-            sub, n = self.unpack("<IQ")
-            return [self.value(sub) for _ in range(n)]
-        return self.unpack(_FMT[typ])[0]
+    def scalar(self, dtype):
+        dt = np.dtype(dtype).newbyteorder("<")
+        v = self.take(dt.itemsize).view(dt)[0]
+        return v.item()
+
+    def u32(self) -> int:
+        return self.scalar(np.uint32)
+
+    def u64(self) -> int:
+        return self.scalar(np.uint64)
+
+    def text(self) -> str:
+        return bytes(self.take(self.u64())).decode("utf-8", "replace")
+
+    def meta_value(self, kind: int):
+        if kind == _META_STRING:
+            return self.text()
+        if kind == _META_ARRAY:
+            elem, count = self.u32(), self.u64()
+            if elem in _META_SCALAR:                # fixed-width arrays decode in one step
+                dt = np.dtype(_META_SCALAR[elem]).newbyteorder("<")
+                return self.take(count * dt.itemsize).view(dt).tolist()
+            return [self.meta_value(elem) for _ in range(count)]
+        if kind not in _META_SCALAR:
+            raise ValueError(f"GGUF: unknown metadata value type {kind}")
+        return self.scalar(_META_SCALAR[kind])
 
 
 class GGUF:
-    """GGUF v2/v3 file: metadata dict, tensor directory, memory-mapped data."""
+    """A GGUF (v2/v3) file: `meta` (key -> value), `tensors` (name -> Tensor), tensor bytes by `raw`."""
 
     def __init__(self, path: str | Path):
         self.path = Path(path)
-        self.meta, self.tensors = {}, {}
-        with open(self.path, "rb") as f:
-            r = _Reader(f)
-            magic, self.version, n_tensors, n_kv = r.unpack("<4sIQQ")
-            if magic != b"GGUF":
-                raise ValueError(f"{path}: not a GGUF file (magic {magic!r})")
-            for _ in range(n_kv):
-                key = r.string()
-                (typ,) = r.unpack("<I")
-                self.meta[key] = r.value(typ)
-            for _ in range(n_tensors):
-                name = r.string()
-                (nd,) = r.unpack("<I")
-                dims = r.unpack(f"<{nd}Q")
-                typ, off = r.unpack("<IQ")
-                self.tensors[name] = Tensor(name, tuple(dims), typ, off)
-            align = int(self.meta.get("general.alignment", 32))
-            self.data_start = -(-f.tell() // align) * align
         self.mm = np.memmap(self.path, dtype=np.uint8, mode="r")
+        cur = _Cursor(self.mm)
+        if bytes(cur.take(4)) != b"GGUF":
+            raise ValueError(f"{path}: not a GGUF file")
+        self.version = cur.u32()
+        n_tensors, n_meta = cur.u64(), cur.u64()
+        self.meta = {}
+        for _ in range(n_meta):
+            key = cur.text()
+            self.meta[key] = cur.meta_value(cur.u32())
+        self.tensors = {}
+        for _ in range(n_tensors):
+            name = cur.text()
+            dims = tuple(cur.u64() for _ in range(cur.u32()))
+            kind, offset = cur.u32(), cur.u64()
+            self.tensors[name] = Tensor(name, dims, kind, offset)
+        align = int(self.meta.get("general.alignment", 32))
+        self.data_start = (cur.pos + align - 1) // align * align
 
     def raw(self, name: str):
         """-> (uint8 bytes of the tensor, Tensor)."""
         t = self.tensors[name]
-        _, blk, bsz = GGML[t.type]
-        n = int(np.prod(t.dims))
-        start = self.data_start + t.offset
-        return np.asarray(self.mm[start:start + n // blk * bsz]), t
+        if t.type not in _BLOCK:
+            raise NotImplementedError(f"{name}: ggml type {t.type}")
+        per, nbytes = _BLOCK[t.type]
+        count = 1
+        for d in t.dims:
+            count *= d
+        begin = self.data_start + t.offset
+        return np.asarray(self.mm[begin:begin + count // per * nbytes]), t
 
     def f32(self, name: str) -> np.ndarray:
-        """Decoded float32 array, shape reversed from ggml dims (row-major [N, K])."""
+        """The tensor decoded to float32, shaped row-major (reverse of the GGUF dims)."""
         b, t = self.raw(name)
-        kind = GGML[t.type][0]
-        if kind == "F32":
-            a = b.view(np.float32)
-        elif kind == "F16":
-            a = b.view(np.float16).astype(np.float32)
-        elif kind == "Q4_0":
-            d, q = q4_0_blocks(b)
-            a = (d[:, None] * (q.astype(np.float32) - 8)).reshape(-1)
-        elif kind == "Q6_K":
-            q, s = q6_k_blocks(b)
-            a = (q.astype(np.float32) * np.repeat(s, 16, axis=1)).reshape(-1)
-        else:
-            raise NotImplementedError(kind)
-        return a.reshape(tuple(reversed(t.dims)))
+        return _DECODE[_TYPE_NAME[t.type]](b).reshape(t.dims[::-1])
+
+
+def _decode_q4_0(b):
+    d, q = q4_0_blocks(b)
+    return (q.astype(np.float32) - 8) * d[:, None]
+
+
+def _decode_q6_k(b):
+    q, s = q6_k_blocks(b)
+    return q.reshape(-1, 16, 16).astype(np.float32) * s[:, :, None]
+
+
+_DECODE = {"F32": lambda b: b.view(np.float32), "F16": lambda b: b.view(np.float16).astype(np.float32),
+           "Q4_0": _decode_q4_0, "Q6_K": _decode_q6_k}
 
 
 def q4_0_blocks(b: np.ndarray):

@@ -7,7 +7,7 @@ import numpy as np
 
 def write_gguf(path, tensors, meta):
     """tensors = {name: (ggml_type, dims, raw bytes)} (dims in ggml order, dims[0] contiguous);
-    meta values: int -> uint32, float -> float32."""
+    meta values: int -> uint32, float -> float32, str -> string, [str] / [int] -> array of string / int32."""
     def s(x):
         e = x.encode()
         return struct.pack("<Q", len(e)) + e
@@ -15,6 +15,12 @@ def write_gguf(path, tensors, meta):
     for k, v in meta.items():
         if isinstance(v, float):
             out += s(k) + struct.pack("<I", 6) + struct.pack("<f", v)
+        elif isinstance(v, str):
+            out += s(k) + struct.pack("<I", 8) + s(v)
+        elif isinstance(v, list) and v and isinstance(v[0], str):
+            out += s(k) + struct.pack("<IIQ", 9, 8, len(v)) + b"".join(s(x) for x in v)
+        elif isinstance(v, list):
+            out += s(k) + struct.pack("<IIQ", 9, 5, len(v)) + struct.pack(f"<{len(v)}i", *v)
         else:
             out += s(k) + struct.pack("<I", 4) + struct.pack("<I", v)
     off = 0

@@ -75,9 +75,14 @@ def test_gguf_reader_and_decoders(tmp_path):
     tensors = {"a.weight": (2, (64, 4), q4.tobytes()), "b": (0, (4, 64), w.tobytes()),
                "c": (1, (8,), f16.tobytes()), "h": (14, (256, 2), q6.tobytes())}
     p = tmp_path / "t.gguf"
-    write_gguf(p, tensors, {"qwen2.block_count": 28})
+    write_gguf(p, tensors, {"qwen2.block_count": 28, "general.architecture": "qwen2",
+                            "tokenizer.ggml.tokens": ["a", "bc", ""], "tokenizer.ggml.token_type": [1, -2, 3],
+                            "qwen2.rope.freq_base": 1e6})
     g = gguf.GGUF(p)
-    assert g.meta["qwen2.block_count"] == 28
+    assert g.meta["qwen2.block_count"] == 28 and g.meta["general.architecture"] == "qwen2"
+    assert g.meta["tokenizer.ggml.tokens"] == ["a", "bc", ""] and g.meta["tokenizer.ggml.token_type"] == [1, -2, 3]
+    assert g.meta["qwen2.rope.freq_base"] == 1e6 and g.version == 3
+    assert g.tensors["h"].dims == (256, 2) and g.tensors["h"].type == 14
     assert g.f32("a.weight").shape == (4, 64)
     assert np.array_equal(g.f32("a.weight"), OQ.dequant_q4_0(q4, (4, 64)))
     assert np.array_equal(g.f32("b").reshape(-1), w.reshape(-1).view(np.float32))
