@@ -122,21 +122,25 @@ def call(name: str, *args):
 
 class Kern:
     """Reference-compatible launcher (scripts/qwen_fused.py:30-42): Kern(spec).launch(grid, block, args).
-    `spec` is a KernelSpec from lab.qwen_kernels / lab.qwen_batched naming a C-ABI entry point; the
-    launch geometry is chosen by the library for gfx950, so grid/block are accepted for signature
-    compatibility and ignored. `args` are the entry point's arguments in declaration order (device
-    pointers as ints or tensors, scalars as Python numbers or ctypes values)."""
+    `spec` is a KernelSpec from lab.qwen_kernels / lab.qwen_batched / lab.qwen_mega naming a C-ABI entry point.
+    If the spec names a reference kernel (spec.ref), `args` is that kernel's own argument list in the reference's
+    order, mapped onto the fused entry points by lab/refcall.py (spec.params carries the generator's choices,
+    e.g. the GEMV epilogue). Otherwise `args` are the entry point's arguments in declaration order. The library
+    picks the gfx950 launch geometry, so grid and block are accepted for signature compatibility and ignored."""
 
     def __init__(self, spec):
         self.spec = spec
         lib()
 
     def launch(self, grid=None, block=None, args=()):
+        if getattr(self.spec, "ref", ""):
+            from .refcall import LAUNCHERS
+            return LAUNCHERS[self.spec.ref](self.spec, list(args))
         conv = []
         for a in args:
             if hasattr(a, "data_ptr"):
                 conv.append(a.data_ptr())
-            elif isinstance(a, (ctypes.c_uint64, ctypes.c_int32, ctypes.c_float)):
+            elif isinstance(a, (ctypes.c_uint64, ctypes.c_int32, ctypes.c_int64, ctypes.c_float, ctypes.c_double)):
                 conv.append(a.value)
             else:
                 conv.append(a)

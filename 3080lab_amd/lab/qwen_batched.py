@@ -23,13 +23,8 @@ from dataclasses import dataclass, field
 import numpy as np
 
 from .hip import call, ptr
+from .qwen_kernels import KernelSpec
 from .qwen_model import FIX_SCALE, PAGE, Config, DeviceModel
-
-
-@dataclass(frozen=True)
-class KernelSpec:
-    symbol: str
-    params: dict = field(default_factory=dict)
 
 
 # reference generator names (lab/qwen_batched.py) -> the C-ABI entry points that replace them

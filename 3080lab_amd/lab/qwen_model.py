@@ -112,10 +112,16 @@ class Q4Mat:
         self.N, self.K = N, K
         self.qs = torch.from_numpy(qs.reshape(-1)).to(device)
         self.d = torch.from_numpy(d.reshape(-1).view(np.int16)).to(device)
+        from .refcall import register
+        register(self.qs, self)           # W / E pointers of reference-order launches resolve to this matrix
 
     @property
     def nbytes(self):
         return self.qs.numel() + 2 * self.d.numel()
+
+    def data_ptr(self):
+        """The matrix's handle in reference-order launches (its qs plane's address)."""
+        return self.qs.data_ptr()
 
 
 class Q6KMat:

@@ -1,0 +1,136 @@
+"""Reference-order launches (lab/refcall.py): a decode step written the way the reference's host code writes it.
+
+RefStep below mirrors FusedQwen.gemv / rms / step (scripts/qwen_fused.py:104-145) line for line: the same kernel
+names (gemv_source(epi), RMSNORM_F32W_1P, EMBED_F32, ATTN4 % {...}, FINISH_MB), the same launch argument lists
+(W, S, X, Y, AUX, N, K etc.) built from tensor.data_ptr() and ctypes scalars. The CPU test checks which library
+calls those launches become (the call layer is replaced by a recorder); the GPU test runs the step and requires
+bit-equal residual streams and equal tokens against lab.qwen_model.Decoder.step.
+"""
+import ctypes
+import math
+
+import numpy as np
+import pytest
+
+from lab import qwen_kernels as KS
+from lab import qwen_model as QM
+from lab import refcall
+from lab.hip import Kern
+
+SPLIT = {"qkv": 2, "o": 2, "gu": 4, "down": 8, "head": 4}
+
+
+class RefStep:
+    """FusedQwen's step over this build's buffers (device-resident model `dm`, decode state of `dec`)."""
+
+    def __init__(self, dm, dec):
+        c = dm.cfg
+        self.H, self.nh, self.nkv, self.hd, self.inter, self.V, self.eps = c.H, c.NH, c.NKV, c.HD, c.FFN, c.V, c.eps
+        self.L = [{"ln1": L["ln1"], "ln2": L["ln2"], "qkv_b": L["qkv_b"], "qkv": (L["qkv"].qs, L["qkv"].d),
+                   "o": (L["o"].qs, L["o"].d), "gu": (L["gu"].qs, L["gu"].d), "down": (L["down"].qs, L["down"].d)}
+                  for L in dm.layers]
+        self.embed, self.norm, self.head = dm.embed, dm.norm, (dm.embed.qs, dm.embed.d)
+        self.cos, self.sin = dm.cos, dm.sin
+        self.kc, self.vc = dec.kc, dec.vc
+        dev = dec.h.device
+        self.h, self.tok, self.pos = dec.h, dec.tok, dec.pos
+        self.x = refcall.NormedAct(1, self.H, dev)
+        self.xm = dec.mlp
+        self.qkv = refcall.QKVOut(1, self.nh, self.hd, dec.block_table, dev)
+        self.att = refcall.AttnOut(1, self.nh, self.hd, dec.max_chunks, dev)
+        self.logits = refcall.Logits(1, self.V, dev)
+        self.k = {name: Kern(KS.gemv_source(SPLIT[name], epi)) for name, epi in
+                  (("qkv", "bias"), ("o", "resid"), ("gu", "swiglu"), ("down", "resid"), ("head", "logits"))}
+        self.k_rms, self.k_emb = Kern(KS.RMSNORM_F32W_1P), Kern(KS.EMBED_F32)
+        self.k_attn, self.k_fin = Kern(KS.ATTN4 % {"maxlen": 2048}), Kern(KS.FINISH_MB)
+
+    def gemv(self, name, wsplit, X, Y, aux, N, K):
+        W, S = wsplit
+        self.k[name].launch((N + 3) // 4, 32 * SPLIT[name],
+                            [W.data_ptr(), S.data_ptr(), X.data_ptr(), Y.data_ptr(), aux, ctypes.c_int32(N),
+                             ctypes.c_int32(K)])
+
+    def rms(self, w, out):
+        self.k_rms.launch(1, 512, [self.h.data_ptr(), w.data_ptr(), out.data_ptr(), ctypes.c_int32(self.H),
+                                   ctypes.c_float(self.eps)])
+
+    def step(self):
+        H, nq = self.H, (self.nh + 2 * self.nkv) * self.hd
+        self.k_emb.launch(4, 512, [self.embed.data_ptr(), self.tok.data_ptr(), self.h.data_ptr(), ctypes.c_int32(H)])
+        scale = ctypes.c_float(1.0 / math.sqrt(self.hd))
+        for i, L in enumerate(self.L):
+            self.rms(L["ln1"], self.x)
+            self.gemv("qkv", L["qkv"], self.x, self.qkv, L["qkv_b"].data_ptr(), nq, H)
+            aargs = [self.qkv.data_ptr(), self.cos.data_ptr(), self.sin.data_ptr(), self.pos.data_ptr(),
+                     self.kc[i].data_ptr(), self.vc[i].data_ptr(), self.att.data_ptr(), ctypes.c_int32(self.nh),
+                     ctypes.c_int32(self.nkv), scale]
+            self.k_attn.launch(self.nh, 128, aargs)
+            self.gemv("o", L["o"], self.att, self.h, 0, H, self.nh * self.hd)
+            self.rms(L["ln2"], self.x)
+            self.gemv("gu", L["gu"], self.x, self.xm, 0, 2 * self.inter, H)
+            self.gemv("down", L["down"], self.xm, self.h, 0, H, self.inter)
+        self.rms(self.norm, self.x)
+        self.gemv("head", self.head, self.x, self.logits, 0, self.V, H)
+        nb = 8
+        self.k_fin.launch(nb, 256, [self.logits.data_ptr(), ctypes.c_int32(self.V), self.tok.data_ptr(),
+                                    self.pos.data_ptr(), 0, 0, 0])
+
+
+CFG = QM.Config(L=2, V=4096)
+
+
+def _model(device):
+    w = QM.random_weights(CFG, seed=23)
+    return QM.DeviceModel(w, CFG, maxlen=128, device=device)
+
+
+def test_reference_order_launches_map_to_fused_calls(monkeypatch):
+    """CPU: the reference-shaped step issues exactly the fused entry points Decoder.step issues, in order, with the
+    epilogue the generator chose."""
+    import torch
+    calls = []
+    monkeypatch.setattr(refcall, "call", lambda name, *a: calls.append((name, a)) or (8 if name.endswith("nparts") else 0))
+    monkeypatch.setattr(QM, "call", lambda name, *a: 8 if name.endswith("nparts") else 0)
+    dm = _model("cpu")
+    dec = QM.Decoder(dm, T=1, max_ctx=128)
+    RefStep(dm, dec).step()
+    names = [n for n, _ in calls]
+    layer = ["q355_qkv_rope_kv", "q355_attn_decode", "q355_attn_o_resid", "q355_ffn_gate_up", "q355_ffn_down"]
+    assert names == ["q355_head_nparts", "q355_embed_q4_0"] + layer * CFG.L + ["q355_head_logits", "q355_finish"]
+    qkv = calls[2][1]
+    L0 = dm.layers[0]
+    # q355_qkv_rope_kv(qs, d, K, h, ln1, eps, bias, cos, sin, pos, block_table, bt_stride, 1, kc, vc, q, nh, nkv, T)
+    assert qkv[0] == L0["qkv"].qs.data_ptr() and qkv[2] == CFG.H and qkv[3] == dec.h.data_ptr()
+    assert qkv[4] == L0["ln1"].data_ptr() and qkv[6] == L0["qkv_b"].data_ptr() and qkv[16:19] == (CFG.NH, CFG.NKV, 1)
+    down = calls[6][1]
+    assert down[:4] == (L0["down"].qs.data_ptr(), L0["down"].d.data_ptr(), CFG.H, CFG.FFN)
+    assert down[4] == dec.mlp.data_ptr() and down[5] == dec.h.data_ptr()
+
+
+def test_reference_order_errors():
+    """Wrong shapes and missing producers are reported, not launched."""
+    spec = KS.gemv_source(2, "resid")
+    assert spec.params["epi_name"] == "resid" and spec.ref == "gemv"
+    assert KS.ATTN4 % {"maxlen": 4096} is KS.ATTN4
+    with pytest.raises(ValueError):
+        KS.gemv_source(2, "bogus")
+
+
+@pytest.mark.gpu
+def test_reference_order_step_equals_decoder(cuda):
+    """GPU: prompt + greedy steps through RefStep and through Decoder.step give bit-equal h and equal tokens."""
+    import torch
+    dm = _model("cuda")
+    a = QM.Decoder(dm, T=1, max_ctx=128)
+    b = QM.Decoder(dm, T=1, max_ctx=128)
+    ref = RefStep(dm, b)
+    prompt = [7, 4000, 123, 9, 3071]
+    for t in prompt + [None] * 6:
+        if t is not None:
+            a.tok.fill_(t)
+            b.tok.fill_(t)
+        a.step()
+        ref.step()
+        torch.cuda.synchronize()
+        assert torch.equal(a.h, b.h)
+        assert int(a.tok.item()) == int(b.tok.item()) and int(a.pos.item()) == int(b.pos.item())
