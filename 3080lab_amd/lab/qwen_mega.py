@@ -11,7 +11,7 @@ from __future__ import annotations
 
 import ctypes
 
-from .hip import call, ptr
+from .hip import HipError, call, ptr
 from .qwen_kernels import KernelSpec
 from .qwen_model import Decoder, DeviceModel
 
@@ -65,6 +65,21 @@ class MegaDecoder(Decoder):
         call("q355_mega_decode", ptr(self.layer_table), c.L, ptr(e.qs), ptr(e.d), ptr(m.norm), c.V, ptr(m.cos),
              ptr(m.sin), ptr(self.block_table), self.max_chunks, c.eps, ptr(self.tok), ptr(self.pos), ptr(self.h),
              ptr(self.logits), ptr(self.ws), self.SPIN_LIMIT_US)
+        import torch
+        if not torch.cuda.is_current_stream_capturing():
+            self.check()
+
+    def check(self):
+        """Raise HipError if the kernel's error word is set (a bounded wait expired, or a bad pos/tok): the tokens
+        of that launch and every later one are invalid. Synchronises with the device."""
+        e = self.error()
+        if e:
+            raise HipError(f"q355_mega_decode: error word {e:#x} (bounded wait expired or invalid pos/tok)")
+
+    def generate(self, n: int, use_graph: bool = True):
+        out = super().generate(n, use_graph)
+        self.check()
+        return out
 
     def error(self) -> int:
         """The kernel's error word (non-zero after a bounded wait expired or a bad pos/tok)."""

@@ -37,11 +37,39 @@ sys.path.insert(0, str(ROOT / "3080lab_amd"))
 
 HBM_PEAK_GBS = 8000.0
 GEMV0_BYTES = 6_881_280 + 860_160 + 1_728 + 35_840     # config 0: nibbles + scales + Q8_1 x + fp32 y
-# HBM bytes per gate_up launch from rocprofv3 PMC (FETCH_SIZE x 2.0 + WRITE_SIZE x 1.0 KiB per dispatch; the
-# factors make a 64 MiB device copy read 64 MiB and write 64 MiB): 7703.5 * 2 + 35.0 KiB. Counters cannot be
-# read from inside this process, so the measured figure is recorded here and re-measured by
-#   rocprofv3 --pmc FETCH_SIZE -- python3 bench.py --quick --no-cpu --steps 4   (then WRITE_SIZE, then --copy-probe)
-GATE_UP_TRAFFIC = int((7703.5 * 2 + 35.0) * 1024)
+# HBM bytes per launch of the roofline kernel come from the committed rocprofv3 PMC summary (counters cannot be
+# read from inside this process): FETCH_SIZE and WRITE_SIZE KiB per dispatch, each scaled by what the same counter
+# reads for a 64 MiB device-to-device copy (see the command lines at the top of that file).
+TRAFFIC_PROFILE = ROOT / "profiles" / "decode_gemv_hbm_traffic_pmc.txt"
+ROOFLINE_KERNEL = "k_gemv<1, 5, 4, 3, 1, 4, 0>"       # q355_ffn_gate_up
+
+
+def traffic_from_profile(kernel: str = ROOFLINE_KERNEL, path: Path = TRAFFIC_PROFILE):
+    """HBM bytes per dispatch of `kernel` from the PMC summary: FETCH_SIZE * (64 MiB / copy FETCH_SIZE) +
+    WRITE_SIZE * (64 MiB / copy WRITE_SIZE). None if the summary does not hold the kernel."""
+    if not path.exists():
+        return None
+    vals, section = {}, None
+    for line in path.read_text().splitlines():
+        if line.startswith("pmc_"):
+            section = line.split("/")[0]                 # pmc_dec_FETCH_SIZE, pmc_copy_WRITE_SIZE, ...
+            continue
+        parts = line.split()
+        if section and len(parts) >= 6 and parts[0] in ("FETCH_SIZE", "WRITE_SIZE") and "mean" in parts:
+            kib = float(parts[parts.index("mean") + 1])
+            name = line.split("KiB", 1)[1].strip()
+            if section.startswith("pmc_copy") and "copyBuffer" in name:
+                vals[(section, "copy")] = kib
+            elif section.startswith("pmc_dec") and kernel in name:
+                vals[(section, "kernel")] = kib
+    need = [("pmc_dec_FETCH_SIZE", "kernel"), ("pmc_dec_WRITE_SIZE", "kernel"),
+            ("pmc_copy_FETCH_SIZE", "copy"), ("pmc_copy_WRITE_SIZE", "copy")]
+    if any(k not in vals for k in need):
+        return None
+    mib64 = 64.0 * 1024
+    fetch = vals[need[0]] * mib64 / vals[need[2]]
+    write = vals[need[1]] * mib64 / vals[need[3]]
+    return int(round((fetch + write) * 1024))
 
 
 def log(*a):
@@ -85,7 +113,8 @@ def gate_up_roofline(dm, dec) -> dict:
     ach = algo / (ms * 1e-3) / 1e9
     return {"kernel": "q355_ffn_gate_up (k_gemv<1,5,4,3,PRO_RMS,EPI_SWIGLU>)", "bound": "hbm",
             "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4),
-            "traffic": GATE_UP_TRAFFIC, "algorithmic_bytes": int(algo), "avg_us": round(ms * 1e3, 3)}
+            "traffic": traffic_from_profile(), "traffic_source": str(TRAFFIC_PROFILE.relative_to(ROOT)),
+            "algorithmic_bytes": int(algo), "avg_us": round(ms * 1e3, 3)}
 
 
 def gemv_config0(copies: int = 64) -> dict:
@@ -185,26 +214,58 @@ def prefill(dm, P: int = 2048, reps: int = 3) -> dict:
     return out
 
 
-def cpu_baseline(w, cfg, prompt, n_steps: int = 6) -> dict:
-    """The oracle (exact int32 block dots, numpy, single core) decoding n_steps tokens of the same model
-    after a short context; tok/s = n_steps / wall time."""
+def cpu_baseline(w, cfg, prompt, n_steps: int = 4) -> dict:
+    """The oracle (oracle/model.py, exact int32 block-dot mode, numpy, one core) on the same workload as the GPU
+    line: the 128-token prompt is run through the oracle's float64 form (untimed; it fills the same K/V cache),
+    then n_steps greedy decode steps at positions 128.. are timed in int32 block-dot mode; tok/s =
+    n_steps / wall time. Also times BASELINE config 0 (one 8960 x 1536 GEMV) and config 1 (one decoder layer
+    at 512 past positions) in the same mode, median of 3 after one warm-up."""
     sys.path.insert(0, str(ROOT))
     from oracle import model as OM
+    from oracle import quant as OQ
     ocfg = OM.Config(**{k: getattr(cfg, k) for k in ("H", "NH", "NKV", "HD", "FFN", "L", "V", "eps", "theta")})
-    m = OM.Model(ocfg, w, maxlen=256, mode="int")
-    cache = m.new_cache()
-    ctx = list(prompt[:4])
-    h = m.forward(ctx, 0, cache)                       # untimed warm-up over a 4-token context
-    tok = int(np.argmax(m.logits(h[-1:])[0]))
+    P = len(prompt)
+    m64 = OM.Model(ocfg, w, maxlen=P + n_steps + 8, mode="f64")
+    cache = m64.new_cache()
+    h = m64.forward([int(t) for t in prompt], 0, cache)
+    tok = int(np.argmax(m64.logits(h[-1:])[0]))
+    del m64
+    m = OM.Model(ocfg, w, maxlen=P + n_steps + 8, mode="int")
     t0 = time.perf_counter()
     for s in range(n_steps):
-        h = m.forward([tok], len(ctx) + s, cache)
+        h = m.forward([tok], P + s, cache)
         tok = int(np.argmax(m.logits(h)[0]))
     dt = time.perf_counter() - t0
+
+    def med(fn, n=3):
+        fn()
+        ts = []
+        for _ in range(n):
+            t = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t)
+        return float(np.median(ts))
+    # config 0: one GEMV, int32 block-dot form
+    rng = np.random.default_rng(0)
+    w0 = rng.standard_normal((8960, 1536), dtype=np.float32) * np.float32(0.02)
+    wb0 = OQ.quantize_q4_0(w0)
+    qx, dx, _ = OQ.quantize_q8_1(rng.standard_normal((1, 1536), dtype=np.float32))
+    t_gemv = med(lambda: OQ.gemv_q4_0_q8_1(wb0, 8960, 1536, qx, dx))
+    # config 1: one layer at 512 past positions (K/V filled with N(0, 1))
+    m1 = OM.Model(OM.Config(L=1, V=cfg.V), {"embed": w["embed"], "norm": w["norm"], "layers": w["layers"][:1]},
+                  maxlen=520, mode="int")
+    c1 = m1.new_cache()
+    kv = np.random.default_rng(5).standard_normal((2, 1, cfg.NKV, 512, cfg.HD)).astype(np.float16)
+    c1["K"][:, :, :512], c1["V"][:, :, :512] = kv[0], kv[1]
+    h1 = np.random.default_rng(6).standard_normal((1, cfg.H))
+    t_layer = med(lambda: m1.layer(0, h1, 512, c1))
     return {"value": round(n_steps / dt, 4), "unit": "tok/s", "cores": 1, "kind": "port",
-            "sample": f"{n_steps} greedy decode steps of the config-2 model (28 layers + tied head, "
-                      f"positions 4..{3 + n_steps}) through oracle/model.py in int32 block-dot mode, "
-                      f"single-threaded numpy, {dt:.1f} s; host os.cpu_count()={os.cpu_count()}"}
+            "sample": f"{n_steps} greedy decode steps of the config-2 model (28 layers + tied head) at positions "
+                      f"{P}..{P + n_steps - 1} after the same {P}-token prompt, oracle/model.py in int32 block-dot "
+                      f"mode, single-threaded numpy, {dt:.1f} s; host os.cpu_count()={os.cpu_count()}",
+            "config0_gemv": {"us": round(t_gemv * 1e6, 1),
+                             "GBps": round(GEMV0_BYTES / t_gemv / 1e9, 3), "cores": 1},
+            "config1_layer": {"us": round(t_layer * 1e6, 1), "past_positions": 512, "cores": 1}}
 
 
 def paired(args):
