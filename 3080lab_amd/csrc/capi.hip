@@ -676,6 +676,25 @@ extern "C" int q355_mmq_attn_o_resid(const uint8_t* qs, const void* d, int N, co
 
 extern "C" int q355_mmq_nparts(int N) { return N / 64; }
 
+extern "C" int q355_mmq_q6k_logits(const uint8_t* lo, const uint8_t* hi, const int8_t* sc, const void* d, int V, int K,
+                                   const int8_t* xq, const void* xds, int T, float* y, float* pmax, int32_t* pidx,
+                                   void* stream) {
+  REQUIRE(lo && hi && sc && d && xq && xds && pmax && pidx, "mmq_q6k_logits: null pointer");
+  REQUIRE(V > 0 && V % 64 == 0, "mmq_q6k_logits: V=%d must be a positive multiple of 64", V);
+  REQUIRE(K > 0 && K % 256 == 0 && K <= 1536, "mmq_q6k_logits: K=%d must be a multiple of 256 and <= 1536", K);
+  REQUIRE(T >= 1 && T <= 32, "mmq_q6k_logits: T=%d outside 1..32", T);
+  GemvArgs a = {};
+  a.qs = lo; a.qhi = hi; a.qsc = (const uint8_t*)sc; a.d = (const __half*)d; a.N = V; a.K = K; a.T = T;
+  a.xq = xq; a.xds = (const half2*)xds; a.y = y; a.pmax = pmax; a.pidx = pidx;
+  const int TT = T <= 16 ? 16 : 32;
+  const size_t lds = (size_t)TT * (K + Q6M_XPAD) + (size_t)TT * (K / 32) * sizeof(float);
+  if (T <= 16)
+    hipLaunchKernelGGL(k_mmq_q6k_logits<1>, dim3(V / 64), dim3(Q6M_WAVES * 64), lds, (hipStream_t)stream, a);
+  else
+    hipLaunchKernelGGL(k_mmq_q6k_logits<2>, dim3(V / 64), dim3(Q6M_WAVES * 64), lds, (hipStream_t)stream, a);
+  return launched("mmq_q6k_logits");
+}
+
 extern "C" int q355_mmq_q4_0_f32(const uint8_t* qs, const void* d, int N, int K, const float* xf, int T,
                                  int64_t* yfix, void* stream) {
   if (int e = check_mat("mmq_q4_0_f32", qs, d, N, K)) return e;

@@ -546,7 +546,9 @@ __global__ void __launch_bounds__(MG_NTH) k_mega_decode(const MegaArgs a) {
       if (w == 0 && layer > 0) mg_wload(Wq, Ly.qkv_qs, Ly.qkv_d, MG_H / 32, qkv_tl, qkv_b0, qkv_b1);
       if (layer == 0) mg_rms_stage(emb, Ly.ln1, a.eps, x, red);
       else mg_rms_stage(prev, Ly.ln1, a.eps, x, red);
+      Q355_MEGA_MARK(layer, 9);
       mg_dots(Wq, x, qkv_b0, qkv_b1, reinterpret_cast<double(*)[1][16]>(part_s), rv);
+      Q355_MEGA_MARK(layer, 10);
       if (threadIdx.x < 16) {
         const int r = threadIdx.x, row = w * 16 + r;
         const double v = rv[0][r] + (double)Ly.qkv_b[row];
@@ -643,7 +645,9 @@ __global__ void __launch_bounds__(MG_NTH) k_mega_decode(const MegaArgs a) {
         stc(ws.accD + (size_t)(layer - 1) * MG_H + i, 0LL);
       }
       mg_rms_stage(HSum2{R, accO}, Ly.ln2, a.eps, x, red);
+      Q355_MEGA_MARK(layer, 11);
       mg_dots(Wg, x, gb0, gb1, reinterpret_cast<double(*)[5][16]>(part_s), rv);
+      Q355_MEGA_MARK(layer, 12);
       for (int e = threadIdx.x; e < nt * 8; e += MG_NTH) {
         const int t = e >> 3, k = e & 7;
         const double gg = rv[t][2 * k], uu = rv[t][2 * k + 1];
@@ -682,7 +686,9 @@ __global__ void __launch_bounds__(MG_NTH) k_mega_decode(const MegaArgs a) {
         mg_stage8(x, g, v);
       }
       __syncthreads();
+      Q355_MEGA_MARK(layer, 13);
       mg_dots(W, x, b0, b1, reinterpret_cast<double(*)[3][16]>(part_s), rv);
+      Q355_MEGA_MARK(layer, 14);
       if (threadIdx.x < 48) {
         const int k = threadIdx.x >> 4, r = threadIdx.x & 15;
         const int tile = (w + MG_NWG * k) % 96;

@@ -10,10 +10,12 @@ There is no CPU fallback: if the library is missing or fails to load, `lib()` ra
 from __future__ import annotations
 
 import ctypes
+import os
 from ctypes import c_char_p, c_double, c_float, c_int, c_void_p
 from pathlib import Path
 
-LIB_PATH = Path(__file__).resolve().parents[1] / "lib" / "libqwen355.so"
+# Q355_LIB selects another build of the same ABI (e.g. an instrumented one); default: the in-tree library
+LIB_PATH = Path(os.environ.get("Q355_LIB") or Path(__file__).resolve().parents[1] / "lib" / "libqwen355.so")
 
 _P = c_void_p
 # name -> argtypes (all return int status)
@@ -48,6 +50,7 @@ _SIGS = {
     "q355_gemm_q4_0_f16": [_P, _P, c_int, c_int, _P, c_int, c_int, _P, _P, _P, _P, _P, _P],
     "q355_attn_decode_f16": [_P, _P, _P, _P, _P, c_int, c_int, c_int, c_int, c_double, _P, _P, c_int, _P],
     "q355_mmq_nparts": [c_int],
+    "q355_mmq_q6k_logits": [_P, _P, _P, _P, c_int, c_int, _P, _P, c_int, _P, _P, _P, _P],
     "q355_attn_prefill": [_P, _P, _P, _P, c_int, c_int, c_int, c_int, c_float, _P, _P, ctypes.c_int64, _P],
     "q355_attn_prefill_q8_1": [_P, _P, _P, _P, c_int, c_int, c_int, c_int, c_float, _P, _P, _P, ctypes.c_int64, _P],
     "q355_attn_prefill_ws_bytes": [c_int, c_int, c_int, c_int],

@@ -84,8 +84,6 @@ class BatchedDecoder:
         self.keep_logits = keep_logits
         import torch
         c = m.cfg
-        if m.head_q6k is not None:
-            raise ValueError("the batched step implements the tied Q4_0 head only")
         if act not in ("f16", "q8"):
             raise ValueError(f"act={act!r}: 'f16' or 'q8'")
         self.m, self.cfg, self.B, self.act = m, c, B, act
@@ -205,8 +203,17 @@ class BatchedDecoder:
             self.layer(i)
         # the LM head runs on Q8_1 activations in both modes (the int8 LDS-tiled kernel reads its 131 MB once)
         self._norm(m.norm)
-        self._mmq(e, self.xq, self.xds, 5, y=self.logits if self.keep_logits else None, pmax=self.pmax,
-                  pidx=self.pidx)
+        if m.head_q6k is not None:           # llama.cpp's Q6_K output.weight, 32 tokens per launch
+            q6 = m.head_q6k
+            for j in range(0, self.B, 32):
+                n = min(32, self.B - j)
+                # the normalized activations are packed [B][H] (int8) and [B][H/32] (half2) from the buffer start
+                call("q355_mmq_q6k_logits", ptr(q6.lo), ptr(q6.hi), ptr(q6.sc), ptr(q6.d), q6.N, q6.K,
+                     ptr(self.xq) + j * c.H, ptr(self.xds) + j * (c.H // 32) * 4, n,
+                     ptr(self.logits[j]) if self.keep_logits else None, ptr(self.pmax[j]), ptr(self.pidx[j]))
+        else:
+            self._mmq(e, self.xq, self.xds, 5, y=self.logits if self.keep_logits else None, pmax=self.pmax,
+                      pidx=self.pidx)
         call("q355_finish", ptr(self.pmax), ptr(self.pidx), self.nparts, ptr(self.tok), ptr(self.pos), self.B)
 
     def capture(self):

@@ -166,6 +166,14 @@ int q355_mmq_q4_0_q8_1(const uint8_t* qs, const void* d, int N, int K, const int
                        void* stream);
 int q355_mmq_nparts(int N);
 
+/* Q6_K x Q8_1 LM head for decode batches on int8 MFMA: logits y fp32 [T][V] (optional, y may be NULL) and the
+ * argmax partials pmax/pidx [T][V/64] (max, lowest row of every 64 rows; q355_finish reduces them), from
+ * llama.cpp's Q6_K output.weight in the library's Q6_K planes (as q355_head_logits_q6k) and Q8_1 activations
+ * xq/xds [T][K]. Each 16-weight sub-block is an exact int32 dot. V % 64 == 0, K % 256 == 0, K <= 1536, T <= 32.
+ * Replaces head_v2_source (lab/qwen_batched.py:681-833). */
+int q355_mmq_q6k_logits(const uint8_t* lo, const uint8_t* hi, const int8_t* sc, const void* d, int V, int K,
+                        const int8_t* xq, const void* xds, int T, float* y, float* pmax, int32_t* pidx, void* stream);
+
 /* Decode batches (T <= 32): yfix [T][N] += W Q8_1(xf), the fp32 activations xf [T][K] (e.g. the SwiGLU output
  * of epi 4) quantized to Q8_1 inside the kernel (d = fp16(amax / 127) per 32-block, q = round(x / d)), then
  * the int8 MFMA product of q355_mmq_q4_0_q8_1 epi 6. N % 64 == 0.

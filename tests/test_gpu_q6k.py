@@ -63,3 +63,69 @@ def test_gguf_model_with_q6k_head_greedy(cuda, tmp_path):
         if margins[i] < NEAR_TIE:
             break
         assert a == b, f"token {i}: {a} vs {b} (margin {margins[i]:.3g})"
+
+
+@pytest.mark.parametrize("N,K,T", [(8192, 1536, 8), (151936, 1536, 32), (4096, 1536, 5), (1024, 256, 17)])
+def test_mmq_q6k_logits(cuda, N, K, T):
+    """The batched Q6_K head on int8 MFMA (exact int32 sub-block dots, fp32 accumulation) against the oracle's
+    f64 dequantized product (oracle.quant.gemv_q6_k_q8_1, the arithmetic of oracle.model.LinearQ6K): logits
+    within 1e-5 relative, argmax partials of every 64 rows consistent with the logits."""
+    import torch
+    rng = np.random.default_rng(N + T)
+    b = random_q6_k(N * K // 256, rng, d=0.0005)
+    W = QM.Q6KMat(b, N, K, "cuda")
+    x = rng.standard_normal((T, K), dtype=np.float32)
+    q, d, s = OQ.quantize_q8_1(x)
+    xq = torch.from_numpy(q).cuda()
+    xds = torch.from_numpy(np.stack([d, s], -1)).cuda()
+    y = torch.full((T, N), float("nan"), device=cuda)
+    pmax = torch.zeros(T, N // 64, device=cuda)
+    pidx = torch.zeros(T, N // 64, dtype=torch.int32, device=cuda)
+    call("q355_mmq_q6k_logits", ptr(W.lo), ptr(W.hi), ptr(W.sc), ptr(W.d), N, K, ptr(xq), ptr(xds), T, ptr(y),
+         ptr(pmax), ptr(pidx))
+    torch.cuda.synchronize()
+    got = y.cpu().numpy()
+    ref = OQ.gemv_q6_k_q8_1(b, N, K, q, d)
+    assert relerr(got, ref) < 1e-5
+    parts = got.reshape(T, N // 64, 64)
+    assert np.array_equal(pmax.cpu().numpy(), parts.max(axis=2))
+    assert np.array_equal(pidx.cpu().numpy(), parts.argmax(axis=2) + 64 * np.arange(N // 64)[None])
+
+
+@pytest.mark.parametrize("B", [8, 32])
+def test_batched_decode_with_q6k_head(cuda, B):
+    """BatchedDecoder with llama.cpp's Q6_K output.weight (int8 MMQ layers, Q6_K MFMA head), teacher-forced
+    against the oracle (oracle.model.LinearQ6K head): logits within the batched int8 mode's tolerance (0.12),
+    argmax equal wherever the oracle's margin exceeds twice that."""
+    import torch
+    from lab import qwen_batched as QB
+    cfg = QM.Config(L=2, V=4096)
+    w = QM.random_weights(cfg, seed=31)
+    # d = 2e-5: weights of std ~0.02 like the Q4_0 layers, so the logits have the magnitude the 0.12 bound
+    # (measured on the tied Q4_0 head) was calibrated for
+    w["head_q6k"] = random_q6_k(cfg.V * cfg.H // 256, np.random.default_rng(32), d=0.00002)
+    dm = QM.DeviceModel(w, cfg, maxlen=256)
+    om = OM.Model(OM.Config(L=2, V=4096), w, maxlen=256)
+    rng = np.random.default_rng(B + 40)
+    prompts = rng.integers(0, cfg.V, (B, 5))
+    bd = QB.BatchedDecoder(dm, B=B, max_ctx=128, page_seed=B, keep_logits=True)
+    bd.prefill_tokens(prompts)
+    seqs = [0, B // 2, B - 1]
+    caches, lgs = {}, {}
+    for s_ in seqs:
+        caches[s_] = om.new_cache()
+        lgs[s_] = om.logits(om.forward(list(prompts[s_]), 0, caches[s_])[-1:])[0]
+    for t in range(4):
+        got = bd.logits.cpu().numpy()
+        toks = got.argmax(axis=1).astype(np.int32)
+        for s_ in seqs:
+            lg = lgs[s_]
+            dev = float(np.abs(got[s_] - lg).max())
+            assert dev < 0.12, f"B={B} seq {s_} step {t}: logits off by {dev:.3g}"
+            top2 = np.partition(lg, -2)[-2:]
+            if top2[1] - top2[0] > 0.24:
+                assert int(toks[s_]) == int(np.argmax(lg))
+            toks[s_] = int(np.argmax(lg))
+            lgs[s_] = om.logits(om.forward([int(toks[s_])], 5 + t, caches[s_]))[0]
+        bd.tok.copy_(torch.from_numpy(toks))
+        bd.step()
