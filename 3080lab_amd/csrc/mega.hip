@@ -63,9 +63,8 @@ struct MegaWs {
   float* m;          // [FFN]
   float* amax;       // [MG_NWG]
   int* aidx;         // [MG_NWG]
-  long long* R;      // [L][H] residual at the start of layer i (materialised by that layer's O phase)
-  long long* accO;   // [L][H] O-projection sums of layer i (int64 atomics; zero between launches)
-  long long* accD;   // [L][H] down-projection sums of layer i
+  long long* accD;   // [2][H] down-projection sums of layer i in slot i % 2 (int64 atomics); folded into the
+                     // residual by the O phase of layer i + 1 (or at the end of the launch) and cleared there
 };
 
 struct MegaArgs {
@@ -80,7 +79,7 @@ struct MegaArgs {
 };
 
 __host__ __device__ inline size_t mega_ws_bytes(int max_chunks, int L) {
-  return (size_t)MG_NWG * MG_FS * 4 + (size_t)MG_REP * MG_FS * 4 + 256 + (size_t)3 * L * MG_H * 8 +
+  return (size_t)MG_NWG * MG_FS * 4 + (size_t)MG_REP * MG_FS * 4 + 256 + (size_t)2 * MG_H * 8 +
          (size_t)MG_NH * max_chunks * (HD + 2) * 8 + (size_t)MG_NH * HD * 4 + (size_t)2 * MG_NKV * HD * 4 +
          (size_t)MG_FFN * 4 + (size_t)MG_NWG * 8;
 }
@@ -91,9 +90,7 @@ __device__ __forceinline__ MegaWs mega_ws(char* p, int max_chunks, int L) {
   w.flags = (unsigned*)p; p += (size_t)MG_NWG * MG_FS * 4;
   w.go = (unsigned*)p; p += (size_t)MG_REP * MG_FS * 4;
   w.ctl = (unsigned*)p; p += 256;
-  w.R = (long long*)p; p += (size_t)L * MG_H * 8;
-  w.accO = (long long*)p; p += (size_t)L * MG_H * 8;
-  w.accD = (long long*)p; p += (size_t)L * MG_H * 8;
+  w.accD = (long long*)p; p += (size_t)2 * MG_H * 8;
   w.part = (double*)p; p += (size_t)MG_NH * max_chunks * (HD + 2) * 8;
   w.q = (float*)p; p += (size_t)MG_NH * HD * 4;
   w.kvnew = (float*)p; p += (size_t)2 * MG_NKV * HD * 4;
@@ -137,24 +134,28 @@ struct MgSync {
   }
 
   // full barrier, in two halves so that weight loads can be issued in between: arrive() publishes; finish()
-  // has WG 0 gather every flag and release MG_REP replicated words, and WG w poll word w % MG_REP
+  // has workgroups 0..7 each gather the flags of the 32 workgroups w = x (mod 8) (the ones the dispatcher
+  // places on XCD x) and release word x; every workgroup then polls the 8 release words. (A single gatherer
+  // polling 256 flags measured 2.6 us per barrier, this form 1.8 us.)
   __device__ __forceinline__ void arrive(unsigned seq) const { publish(seq); }
   __device__ __forceinline__ void finish(unsigned seq) const {
-    if (blockIdx.x == 0 && threadIdx.x < 64) {
+    const int lane = threadIdx.x & 63;
+    if (blockIdx.x < 8 && threadIdx.x < 64) {
       const long long t0 = wall_clock64();
       while (true) {
         bool ok = true;
-        for (int i = threadIdx.x; i < MG_NWG; i += 64) ok &= seq_reached(ldc(flags + i * MG_FS), seq);
+        for (int i = (int)blockIdx.x + 8 * lane; i < MG_NWG; i += 512) ok &= seq_reached(ldc(flags + i * MG_FS), seq);
         if (__all(ok)) break;
-        if (wall_clock64() - t0 > limit || failed()) { if (threadIdx.x == 0) fail(); break; }
+        if (wall_clock64() - t0 > limit || failed()) { if (lane == 0) fail(); break; }
       }
-      if (threadIdx.x < MG_REP) stc(go + threadIdx.x * MG_FS, seq);
+      if (lane == 0) stc(go + blockIdx.x * MG_FS, seq);
     }
-    if (threadIdx.x == 0) {
+    if (threadIdx.x < 64) {
       const long long t0 = wall_clock64();
-      const unsigned* g = go + (blockIdx.x % MG_REP) * MG_FS;
-      while (!seq_reached(ldc(g), seq)) {
-        if (wall_clock64() - t0 > limit || failed()) { fail(); break; }
+      while (true) {
+        const bool ok = lane >= 8 || seq_reached(ldc(go + lane * MG_FS), seq);
+        if (__all(ok)) break;
+        if (wall_clock64() - t0 > limit || failed()) { if (lane == 0) fail(); break; }
       }
     }
     __syncthreads();
@@ -299,16 +300,16 @@ struct HFromEmbed {
     return from_fix(to_fix(v));
   }
 };
-// residual of layer i + 1 before it is materialised: R_i + accO_i + accD_i (exact int64 sums)
-struct HSum3 {
-  const long long *r, *o, *d;
-  __device__ __forceinline__ long long fix(int i) const { return ldc(r + i) + ldc(o + i) + ldc(d + i); }
+// residual entering layer i > 0: h (with the O sums of layer i - 1 folded in) + the down sums of layer i - 1
+struct HSum2 {
+  const long long *h, *acc;
+  __device__ __forceinline__ long long fix(int i) const { return ldc(h + i) + ldc(acc + i); }
   __device__ __forceinline__ double operator()(int i) const { return from_fix(fix(i)); }
 };
-// residual after the O projection of layer i: R_i + accO_i
-struct HSum2 {
-  const long long *r, *o;
-  __device__ __forceinline__ double operator()(int i) const { return from_fix(ldc(r + i) + ldc(o + i)); }
+// residual after the O projection of layer i: h
+struct HOne {
+  const long long* h;
+  __device__ __forceinline__ double operator()(int i) const { return from_fix(ldc(h + i)); }
 };
 
 // ---------------------------------------------------------------------------------------------
@@ -319,25 +320,38 @@ struct HSum2 {
 // of P.V over the wave's 16 positions. The 4 waves' sums are added in fixed order into one partial
 // (o[128], M, l) per (head, page). K/V come straight from the cache into registers; the new token's row
 // comes from the coherent scratch.
+struct MgAttnRegs {
+  u32x4 k4[4];       // this lane's quarter of its position's K row
+  unsigned v2[16];   // dims 2 lane, 2 lane + 1 of the wave's 16 V rows
+};
+
+// the task's K/V page rows from the cache (positions before this token: written by earlier launches), issued
+// before the task waits for this token's q / k / v
+__device__ __forceinline__ void mg_attn_load(MgAttnRegs& R, const MegaArgs& a, const MegaLayer& Ly, int g, int c) {
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int p = lane >> 2, dq = lane & 3;
+  const int pg = a.block_table[c];
+  const int row = 16 * wv + p;
+  const __half* kbase = Ly.kc + ((size_t)pg * MG_NKV + g) * PAGE * HD;
+  const __half* vbase = Ly.vc + ((size_t)pg * MG_NKV + g) * PAGE * HD;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) R.k4[i] = ((const u32x4*)(kbase + (size_t)row * HD + 32 * dq))[i];
+#pragma unroll
+  for (int r = 0; r < 16; ++r) R.v2[r] = ((const unsigned*)(vbase + (size_t)(16 * wv + r) * HD))[lane];
+}
+
 __device__ __forceinline__ void mg_attn_task(const MegaArgs& a, const MegaLayer& Ly, const MegaWs& ws, int g, int c,
-                                             int half, int pos, char* lds) {
+                                             int half, int pos, char* lds, MgAttnRegs& R) {
   double* qd = (double*)lds;                     // [3][HD] queries (f64)
   double* red_m = qd + 3 * HD;                   // [3][4]
   double* red_l = red_m + 12;                    // [3][4]
   double* red_o = red_l + 12;                    // [4][3][HD]
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int p = lane >> 2, dq = lane & 3;
-  const int pg = a.block_table[c];
   const int row = 16 * wv + p, gp = c * PAGE + row;
   const bool valid = gp <= pos;
-  const __half* kbase = Ly.kc + ((size_t)pg * MG_NKV + g) * PAGE * HD;
-  const __half* vbase = Ly.vc + ((size_t)pg * MG_NKV + g) * PAGE * HD;
-  u32x4 k4[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) k4[i] = ((const u32x4*)(kbase + (size_t)row * HD + 32 * dq))[i];
-  unsigned v2[16];
-#pragma unroll
-  for (int r = 0; r < 16; ++r) v2[r] = ((const unsigned*)(vbase + (size_t)(16 * wv + r) * HD))[lane];
+  u32x4 (&k4)[4] = R.k4;
+  unsigned (&v2)[16] = R.v2;
   Q355_MEGA_MARK(31, 1);
   for (int e = threadIdx.x; e < 3 * HD; e += MG_NTH)
     qd[e] = (double)ldc(ws.q + (6 * g + 3 * half) * HD + e);
@@ -527,40 +541,47 @@ __global__ void __launch_bounds__(MG_NTH) k_mega_decode(const MegaArgs a) {
   const HFromEmbed emb{a.emb_qs, a.emb_d, tok, MG_H / 32};
 
   // weights of the next QKV / gate-up phase are loaded between a barrier's arrive and finish (except on
-  // WG 0, whose gather loop would otherwise wait for them)
+  // the gathering workgroups 0..7, whose gather loops would otherwise wait for them)
   MgW<1, 3> Wq;
   const int qkv_b0[1] = {0}, qkv_b1[1] = {MG_H / 32}, qkv_tl[1] = {w < MG_NQKV / 16 ? w : 0};
   if (w < MG_NQKV / 16) mg_wload(Wq, a.layers[0].qkv_qs, a.layers[0].qkv_d, MG_H / 32, qkv_tl, qkv_b0, qkv_b1);
 
+  // the residual stream lives in a.h (int64 fixed point): layer 0's O phase starts it from the embedding row
+  // (written here by the owners of its 96 tiles, before their first flag), O sums are added into it, and the
+  // down sums of layer i collect in accD slot i % 2 until layer i + 1's O phase folds them in
+  long long* const hres = a.h;
+  if (w < MG_H / 16 && threadIdx.x < 16) stc(hres + w * 16 + threadIdx.x, to_fix(emb(w * 16 + threadIdx.x)));
+
   for (int layer = 0; layer < a.L; ++layer) {
     const MegaLayer Ly = a.layers[layer];
-    long long* R = ws.R + (size_t)layer * MG_H;
-    long long* accO = ws.accO + (size_t)layer * MG_H;
-    long long* accD = ws.accD + (size_t)layer * MG_H;
-    // residual entering this layer: the embedding, or the previous layer's R + accO + accD
-    const HSum3 prev{ws.R + (size_t)(layer - 1) * MG_H, ws.accO + (size_t)(layer - 1) * MG_H,
-                     ws.accD + (size_t)(layer - 1) * MG_H};
+    long long* const accPrev = ws.accD + (size_t)((layer + 1) & 1) * MG_H;   // down sums of layer - 1
+    long long* const accCur = ws.accD + (size_t)(layer & 1) * MG_H;
+    const HSum2 prev{hres, accPrev};
     // ---- QKV ----
     const unsigned s_qkv = ++seq;
     if (w < MG_NQKV / 16) {
-      if (w == 0 && layer > 0) mg_wload(Wq, Ly.qkv_qs, Ly.qkv_d, MG_H / 32, qkv_tl, qkv_b0, qkv_b1);
+      if (w < 8 && layer > 0) mg_wload(Wq, Ly.qkv_qs, Ly.qkv_d, MG_H / 32, qkv_tl, qkv_b0, qkv_b1);
+      // epilogue operands (bias pair, RoPE angle, page) loaded before the normalisation
+      const int r = threadIdx.x & 15, row = w * 16 + r;
+      const float bias = Ly.qkv_b[row], bias2 = Ly.qkv_b[row ^ 1];
+      const int e2 = row % HD, ci = e2 >> 1;
+      const float rc = a.rope_cos[(size_t)pos * (HD / 2) + ci], rs = a.rope_sin[(size_t)pos * (HD / 2) + ci];
+      const int pg = a.block_table[pos / PAGE];
       if (layer == 0) mg_rms_stage(emb, Ly.ln1, a.eps, x, red);
       else mg_rms_stage(prev, Ly.ln1, a.eps, x, red);
       Q355_MEGA_MARK(layer, 9);
       mg_dots(Wq, x, qkv_b0, qkv_b1, reinterpret_cast<double(*)[1][16]>(part_s), rv);
       Q355_MEGA_MARK(layer, 10);
       if (threadIdx.x < 16) {
-        const int r = threadIdx.x, row = w * 16 + r;
-        const double v = rv[0][r] + (double)Ly.qkv_b[row];
+        const double v = rv[0][r] + (double)bias;
         const int nq = MG_NH * HD, nk = MG_NKV * HD;
-        const int pg = a.block_table[pos / PAGE];
         if (row < nq + nk) {
-          const double v2 = rv[0][r ^ 1] + (double)Ly.qkv_b[row ^ 1];
-          const int e2 = row % HD, i = e2 >> 1, hi = e2 & 1;
-          const double c = a.rope_cos[(size_t)pos * (HD / 2) + i], s = a.rope_sin[(size_t)pos * (HD / 2) + i];
+          const double v2 = rv[0][r ^ 1] + (double)bias2;
+          const int hi = e2 & 1;
+          const double c = rc, sn = rs;
           const double lo_v = hi ? v2 : v, hi_v = hi ? v : v2;
-          const double out = hi ? (hi_v * c + lo_v * s) : (lo_v * c - hi_v * s);
-          const int dim = i + (HD / 2) * hi;
+          const double out = hi ? (hi_v * c + lo_v * sn) : (lo_v * c - hi_v * sn);
+          const int dim = ci + (HD / 2) * hi;
           const __half hv = half_rn(out);
           if (row < nq) {
             stc(ws.q + (row / HD) * HD + dim, __half2float(hv));
@@ -580,31 +601,29 @@ __global__ void __launch_bounds__(MG_NTH) k_mega_decode(const MegaArgs a) {
     Q355_MEGA_MARK(layer, 0);
     sy.publish(s_qkv);
 
-    // ---- attention ----
+    // ---- attention: task idx on workgroup 128 + idx; its K/V page is loaded before the wait. The wait covers
+    // all 128 QKV workgroups (not only the task's group), so once attention is done nobody reads the residual
+    // of this layer's QKV phase any more and the O phase may add into it ----
     const unsigned s_attn = ++seq;
-    for (int idx = (w - 128 + MG_NWG) % MG_NWG; idx < n_attn; idx += MG_NWG) {
+    for (int idx = (w - MG_NQKV / 16 + MG_NWG) % MG_NWG; idx < n_attn; idx += MG_NWG) {
       const int g = idx / (2 * nch), c = (idx / 2) % nch, half = idx & 1;
-      // the 64 QKV tiles of group g: q heads 6g..6g+5 (tiles 48g..48g+47), k (96 + 8g..), v (112 + 8g..)
+      MgAttnRegs AR;
+      mg_attn_load(AR, a, Ly, g, c);
       Q355_MEGA_MARK(31, 7);
-      sy.wait(64, [g](int i) { return i < 48 ? 48 * g + i : (i < 56 ? 96 + 8 * g + (i - 48) : 112 + 8 * g + (i - 56)); },
-              s_qkv);
+      sy.wait(MG_NQKV / 16, [](int i) { return i; }, s_qkv);
       Q355_MEGA_MARK(31, 0);
-      mg_attn_task(a, Ly, ws, g, c, half, pos, lds);
+      mg_attn_task(a, Ly, ws, g, c, half, pos, lds, AR);
     }
     Q355_MEGA_MARK(layer, 1);
     sy.publish(s_attn);
 
-    // ---- O projection (+ merge); slice-0 workgroups also materialise R of this layer ----
+    // ---- O projection (+ merge) into the residual; slice-0 workgroups fold in the previous layer's down sums ----
     const unsigned s_o = ++seq;
     if (w < 192) {
       const int tile = w % 96, sl = w / 96;
       MgW<1, 2> W;
       const int tl[1] = {tile}, b0[1] = {24 * sl}, b1[1] = {24 * sl + 24};
       mg_wload(W, Ly.o_qs, Ly.o_d, MG_H / 32, tl, b0, b1);
-      if (sl == 0 && threadIdx.x < 16) {
-        const int row = tile * 16 + threadIdx.x;
-        stc(R + row, layer == 0 ? to_fix(emb(row)) : prev.fix(row));
-      }
       sy.wait(2 * nch, [sl, nch](int i) { return attn_wg(sl * 2 * nch + i); }, s_attn);
       Q355_MEGA_MARK(layer, 2);
       const int wv = threadIdx.x >> 6;
@@ -619,8 +638,15 @@ __global__ void __launch_bounds__(MG_NTH) k_mega_decode(const MegaArgs a) {
       }
       __syncthreads();
       mg_dots(W, x, b0, b1, reinterpret_cast<double(*)[1][16]>(part_s), rv);
-      if (threadIdx.x < 16)
-        atomicAdd((unsigned long long*)(accO + tile * 16 + threadIdx.x), (unsigned long long)to_fix(rv[0][threadIdx.x]));
+      if (threadIdx.x < 16) {
+        const int row = tile * 16 + threadIdx.x;
+        long long add = to_fix(rv[0][threadIdx.x]);
+        if (sl == 0 && layer > 0) {
+          add += ldc(accPrev + row);
+          stc(accPrev + row, 0LL);
+        }
+        atomicAdd((unsigned long long*)(hres + row), (unsigned long long)add);
+      }
     }
     Q355_MEGA_MARK(layer, 3);
     sy.arrive(s_o);
@@ -629,7 +655,7 @@ __global__ void __launch_bounds__(MG_NTH) k_mega_decode(const MegaArgs a) {
     int gtl[5], gb0[5], gb1[5];
 #pragma unroll
     for (int t = 0; t < 5; ++t) { gtl[t] = gt0 + min(t, gnt - 1); gb0[t] = 0; gb1[t] = MG_H / 32; }
-    if (w != 0) mg_wload(Wg, Ly.gu_qs, Ly.gu_d, MG_H / 32, gtl, gb0, gb1);
+    if (w >= 8) mg_wload(Wg, Ly.gu_qs, Ly.gu_d, MG_H / 32, gtl, gb0, gb1);
     sy.finish(s_o);
     Q355_MEGA_MARK(layer, 4);
 
@@ -637,14 +663,8 @@ __global__ void __launch_bounds__(MG_NTH) k_mega_decode(const MegaArgs a) {
     const unsigned s_gu = ++seq;
     {
       const int t0 = gt0, nt = gnt;
-      if (w == 0) mg_wload(Wg, Ly.gu_qs, Ly.gu_d, MG_H / 32, gtl, gb0, gb1);
-      // the previous layer's accumulators are read by nobody from here on: clear them for the next launch
-      if (layer > 0 && threadIdx.x < MG_H / MG_NWG) {
-        const int i = w * (MG_H / MG_NWG) + threadIdx.x;
-        stc(ws.accO + (size_t)(layer - 1) * MG_H + i, 0LL);
-        stc(ws.accD + (size_t)(layer - 1) * MG_H + i, 0LL);
-      }
-      mg_rms_stage(HSum2{R, accO}, Ly.ln2, a.eps, x, red);
+      if (w < 8) mg_wload(Wg, Ly.gu_qs, Ly.gu_d, MG_H / 32, gtl, gb0, gb1);
+      mg_rms_stage(HOne{hres}, Ly.ln2, a.eps, x, red);
       Q355_MEGA_MARK(layer, 11);
       mg_dots(Wg, x, gb0, gb1, reinterpret_cast<double(*)[5][16]>(part_s), rv);
       Q355_MEGA_MARK(layer, 12);
@@ -657,7 +677,7 @@ __global__ void __launch_bounds__(MG_NTH) k_mega_decode(const MegaArgs a) {
     Q355_MEGA_MARK(layer, 5);
     sy.publish(s_gu);
 
-    // ---- down ----
+    // ---- down: into this layer's accD slot ----
     const unsigned s_down = ++seq;
     {
       MgW<3, 3> W;
@@ -692,12 +712,12 @@ __global__ void __launch_bounds__(MG_NTH) k_mega_decode(const MegaArgs a) {
       if (threadIdx.x < 48) {
         const int k = threadIdx.x >> 4, r = threadIdx.x & 15;
         const int tile = (w + MG_NWG * k) % 96;
-        atomicAdd((unsigned long long*)(accD + tile * 16 + r), (unsigned long long)to_fix(rv[k][r]));
+        atomicAdd((unsigned long long*)(accCur + tile * 16 + r), (unsigned long long)to_fix(rv[k][r]));
       }
     }
     Q355_MEGA_MARK(layer, 7);
     sy.arrive(s_down);
-    if (w != 0 && w < MG_NQKV / 16 && layer + 1 < a.L)
+    if (w >= 8 && w < MG_NQKV / 16 && layer + 1 < a.L)
       mg_wload(Wq, a.layers[layer + 1].qkv_qs, a.layers[layer + 1].qkv_d, MG_H / 32, qkv_tl, qkv_b0, qkv_b1);
     sy.finish(s_down);
     Q355_MEGA_MARK(layer, 8);
@@ -705,7 +725,8 @@ __global__ void __launch_bounds__(MG_NTH) k_mega_decode(const MegaArgs a) {
   Q355_MEGA_MARK(a.L, 0);
 
   // ---- tied head: final RMSNorm, logits, argmax partial per workgroup (8-tile chunks, double-buffered) ----
-  const HSum3 fin{ws.R + (size_t)(a.L - 1) * MG_H, ws.accO + (size_t)(a.L - 1) * MG_H, ws.accD + (size_t)(a.L - 1) * MG_H};
+  long long* const accLast = ws.accD + (size_t)((a.L - 1) & 1) * MG_H;
+  const HSum2 fin{hres, accLast};
   {
     const int ntiles = a.V / 16;
     const int t0 = (int)(((long long)ntiles * w) / MG_NWG), t1 = (int)(((long long)ntiles * (w + 1)) / MG_NWG);
@@ -738,11 +759,10 @@ __global__ void __launch_bounds__(MG_NTH) k_mega_decode(const MegaArgs a) {
   sy.publish(s_head);
   if (w == 0) {
     sy.wait(MG_NWG, [](int i) { return i; }, s_head);
-    // the final residual (for the caller), then clear the last layer's accumulators
+    // the final residual (for the caller): fold in the last layer's down sums and clear their slot
     for (int i = threadIdx.x; i < MG_H; i += MG_NTH) {
       a.h[i] = fin.fix(i);
-      stc(ws.accO + (size_t)(a.L - 1) * MG_H + i, 0LL);
-      stc(ws.accD + (size_t)(a.L - 1) * MG_H + i, 0LL);
+      stc(accLast + i, 0LL);
     }
     if (threadIdx.x < 64) {
       float best = -INFINITY;

@@ -53,11 +53,14 @@ def test_mega_greedy_matches_oracle(small):
 
 
 def test_mega_rejects_position_past_cache(small):
-    """pos beyond the cache: the launch returns at once with the error word set (no out-of-range access)."""
+    """pos beyond the cache: the launch returns at once with the error word set (no out-of-range access), and
+    step() raises."""
+    from lab.hip import HipError
     w, dm, om = small
     dec = QG.MegaDecoder(dm, max_ctx=128)
     dec.pos.fill_(128)
-    dec.step()
+    with pytest.raises(HipError, match="error word"):
+        dec.step()
     assert dec.error() != 0
     assert int(dec.pos.item()) == 128
 
