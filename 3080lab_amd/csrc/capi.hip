@@ -946,7 +946,7 @@ extern "C" int q355_mega_decode(const void* layers, int L, const uint8_t* emb_qs
                                 int V, const float* rope_cos, const float* rope_sin, const int32_t* block_table,
                                 int max_chunks, double eps, int32_t* tok, int32_t* pos, int64_t* h, float* logits,
                                 void* ws, int64_t spin_limit_us, void* stream) {
-  REQUIRE(layers && emb_qs && emb_d && norm && rope_cos && rope_sin && block_table && tok && pos && h && logits && ws,
+  REQUIRE(layers && emb_qs && emb_d && norm && rope_cos && rope_sin && block_table && tok && pos && h && ws,
           "mega_decode: null pointer");
   REQUIRE(L >= 1 && L <= 256, "mega_decode: L=%d", L);
   REQUIRE(V > 0 && V % 16 == 0 && V / 16 >= MG_NWG, "mega_decode: V=%d (multiple of 16, >= %d)", V, 16 * MG_NWG);

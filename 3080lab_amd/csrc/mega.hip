@@ -724,9 +724,23 @@ __global__ void __launch_bounds__(MG_NTH) k_mega_decode(const MegaArgs a) {
   }
   Q355_MEGA_MARK(a.L, 0);
 
-  // ---- tied head: final RMSNorm, logits, argmax partial per workgroup (8-tile chunks, double-buffered) ----
   long long* const accLast = ws.accD + (size_t)((a.L - 1) & 1) * MG_H;
   const HSum2 fin{hres, accLast};
+  if (!a.logits) {
+    // no head in this launch (the caller runs its own, e.g. a Q6_K output matrix): after the last barrier nobody
+    // reads the residual any more; workgroup 0 folds in the last down sums, clears their slot and moves the
+    // sequence base on. tok and pos are left to the caller's head and finish.
+    if (w == 0) {
+      for (int i = threadIdx.x; i < MG_H; i += MG_NTH) {
+        a.h[i] = fin.fix(i);
+        stc(accLast + i, 0LL);
+      }
+      if (threadIdx.x == 0) stc(ws.ctl, base + 4096u);
+    }
+    return;
+  }
+
+  // ---- tied head: final RMSNorm, logits, argmax partial per workgroup (8-tile chunks, double-buffered) ----
   {
     const int ntiles = a.V / 16;
     const int t0 = (int)(((long long)ntiles * w) / MG_NWG), t1 = (int)(((long long)ntiles * (w + 1)) / MG_NWG);

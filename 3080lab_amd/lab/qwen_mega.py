@@ -3,7 +3,8 @@
 The reference's megakernel (mega_source, lab/qwen_mega.py:43-361) streams every layer's weights through
 one persistent CUDA kernel per token with a software grid barrier; its own log records it as incorrect
 (token 1 vs 89141, data/oct15_tiles_mega/megakernel_pos128.log). Here `mega_source` names the gfx950
-persistent step q355_mega_decode: one launch per token, 256 workgroups (one per CU), every phase's weight
+persistent step q355_mega_decode: one launch per token (plus head and argmax launches for a Q6_K output matrix),
+256 workgroups (one per CU), every phase's weight
 loads issued before the phase waits for its inputs, dataflow flags between dependent phases and two full
 barriers per layer; f64 arithmetic of the batch-1 GEMV path (same oracle, same tokens).
 """
@@ -41,8 +42,6 @@ class MegaDecoder(Decoder):
 
     def __init__(self, m: DeviceModel, max_ctx: int | None = None):
         import torch
-        if m.head_q6k is not None:
-            raise ValueError("the persistent step implements the tied Q4_0 head only")
         super().__init__(m, T=1, max_ctx=max_ctx)
         assert call("q355_mega_layer_bytes") == ctypes.sizeof(MegaLayer)
         # the kernel accepts any pos < max_chunks * 64: the RoPE tables must cover all of them
@@ -62,9 +61,16 @@ class MegaDecoder(Decoder):
     def step(self):
         m, c = self.m, self.cfg
         e = m.embed
+        q6 = m.head_q6k
+        # a Q6_K output matrix (llama.cpp's output.weight): the persistent launch stops after the layers and the
+        # head + argmax run as two more launches
         call("q355_mega_decode", ptr(self.layer_table), c.L, ptr(e.qs), ptr(e.d), ptr(m.norm), c.V, ptr(m.cos),
              ptr(m.sin), ptr(self.block_table), self.max_chunks, c.eps, ptr(self.tok), ptr(self.pos), ptr(self.h),
-             ptr(self.logits), ptr(self.ws), self.SPIN_LIMIT_US)
+             None if q6 is not None else ptr(self.logits), ptr(self.ws), self.SPIN_LIMIT_US)
+        if q6 is not None:
+            call("q355_head_logits_q6k", ptr(q6.lo), ptr(q6.hi), ptr(q6.sc), ptr(q6.d), q6.N, q6.K, ptr(self.h),
+                 ptr(m.norm), c.eps, ptr(self.logits), ptr(self.pmax), ptr(self.pidx), 1)
+            call("q355_finish", ptr(self.pmax), ptr(self.pidx), self.nparts, ptr(self.tok), ptr(self.pos), 1)
         import torch
         if not torch.cuda.is_current_stream_capturing():
             self.check()

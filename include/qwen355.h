@@ -293,7 +293,9 @@ int q355_mega_layer_bytes(void);
 /* One greedy decode step of the whole model in ONE launch of 256 workgroups (one per CU; fails with
  * Q355_EINVAL if the device cannot keep 256 resident): embed tok, L layers, final norm + tied Q4_0 head,
  * tok = argmax (lowest index on ties), pos += 1; logits fp32 [V]; h int64 [1536] receives the final
- * residual. Shapes: H 1536, 12/2 heads of 128, FFN 8960, V % 16 == 0, max_chunks <= 64, pos < 64 max_chunks.
+ * residual. logits == NULL: the launch stops after the layers (h receives the final residual, tok and pos are
+ * left unchanged) so the caller can run another head, e.g. q355_head_logits_q6k + q355_finish for llama.cpp's Q6_K
+ * output.weight. Shapes: H 1536, 12/2 heads of 128, FFN 8960, V % 16 == 0, max_chunks <= 64, pos < 64 max_chunks.
  * Waits between workgroups are bounded by spin_limit_us; on expiry (or a bad pos/tok) the workspace error
  * word is set and the launch completes with invalid outputs.
  * Replaces mega_source (lab/qwen_mega.py:43-361) and the graph of FusedQwen.step (scripts/qwen_fused.py:113-180). */

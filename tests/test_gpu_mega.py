@@ -52,6 +52,28 @@ def test_mega_greedy_matches_oracle(small):
         assert x == y, f"token {i}: {x} vs {y} (margin {margins[i]:.3g})"
 
 
+def test_mega_with_q6k_head_matches_graph(small):
+    """llama.cpp's Q6_K output.weight: the persistent launch runs the layers, the Q6_K head and the argmax follow
+    as two launches; logits and tokens equal the graph decoder's, also under graph capture (generate)."""
+    from ggufio import random_q6_k
+    w, _, _ = small
+    w = dict(w)
+    w["head_q6k"] = random_q6_k(CFG_S.V * CFG_S.H // 256, np.random.default_rng(24), d=0.0005)
+    dm = QM.DeviceModel(w, CFG_S, maxlen=512)
+    prompt = [int(t) for t in np.random.default_rng(25).integers(0, CFG_S.V, 6)]
+    a = QM.Decoder(dm, T=1, max_ctx=256)
+    b = QG.MegaDecoder(dm, max_ctx=256)
+    for t in prompt:
+        a.tok.fill_(t)
+        b.tok.fill_(t)
+        a.step()
+        b.step()
+        la, lb = a.logits[0].cpu().numpy(), b.logits[0].cpu().numpy()
+        assert np.abs(la - lb).max() <= 1e-6 * np.abs(la).max()
+        assert int(a.tok.item()) == int(b.tok.item()) and int(a.pos.item()) == int(b.pos.item())
+    assert (a.generate(8) == b.generate(8)).all()
+
+
 def test_mega_rejects_position_past_cache(small):
     """pos beyond the cache: the launch returns at once with the error word set (no out-of-range access), and
     step() raises."""
