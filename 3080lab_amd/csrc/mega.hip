@@ -104,6 +104,17 @@ __device__ __forceinline__ MegaWs mega_ws(char* p, int max_chunks, int L) {
 
 __device__ __forceinline__ bool seq_reached(unsigned v, unsigned seq) { return (int)(v - seq) >= 0; }
 
+// 16-byte device-scope loads (buffer loads with the sc1 policy, as the relaxed agent-scope atomic loads use):
+// coherent with other CUs' device-scope stores, four times the width of ldc, ordinary wait-count tracking
+struct Coh16 {
+  __amdgpu_buffer_rsrc_t r;
+  __device__ __forceinline__ Coh16(const void* p, unsigned bytes)
+      : r(__builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, (int)bytes, 0x00020000)) {}
+  __device__ __forceinline__ int4 ld(unsigned byte_off) const {
+    return __builtin_bit_cast(int4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)byte_off, 0, 16));
+  }
+};
+
 // ---------------------------------------------------------------------------------------------
 // Synchronisation.
 struct MgSync {
@@ -257,10 +268,11 @@ __device__ __forceinline__ void mg_rms_stage(G get, const float* __restrict__ w,
   const int g = threadIdx.x;                  // 8 values per thread, 192 threads active
   const bool act = g < MG_H / 8;
   double hv[8];
+  get.load8(act ? g : 0, hv);
   double ss = 0.0;
 #pragma unroll
   for (int u = 0; u < 8; ++u) {
-    hv[u] = act ? get(8 * g + u) : 0.0;
+    hv[u] = act ? hv[u] : 0.0;
     ss = fma(hv[u], hv[u], ss);
   }
   float4 w0 = make_float4(0.f, 0.f, 0.f, 0.f), w1 = w0;
@@ -299,17 +311,46 @@ struct HFromEmbed {
     const double v = (double)__half2float(d[tb]) * (double)q;
     return from_fix(to_fix(v));
   }
+  __device__ __forceinline__ void load8(int g, double (&hv)[8]) const {
+#pragma unroll
+    for (int u = 0; u < 8; ++u) hv[u] = (*this)(8 * g + u);
+  }
 };
 // residual entering layer i > 0: h (with the O sums of layer i - 1 folded in) + the down sums of layer i - 1
 struct HSum2 {
   const long long *h, *acc;
   __device__ __forceinline__ long long fix(int i) const { return ldc(h + i) + ldc(acc + i); }
   __device__ __forceinline__ double operator()(int i) const { return from_fix(fix(i)); }
+  // values 8 g .. 8 g + 7 with 16-byte device-scope loads (all issued before the first use)
+  __device__ __forceinline__ void load8(int g, double (&hv)[8]) const {
+    const Coh16 H(h, MG_H * 8), A(acc, MG_H * 8);
+    int4 x[4], y[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) { x[u] = H.ld(64 * g + 16 * u); y[u] = A.ld(64 * g + 16 * u); }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const long long x0 = ((long long)(unsigned)x[u].y << 32) | (unsigned)x[u].x, x1 = ((long long)(unsigned)x[u].w << 32) | (unsigned)x[u].z;
+      const long long y0 = ((long long)(unsigned)y[u].y << 32) | (unsigned)y[u].x, y1 = ((long long)(unsigned)y[u].w << 32) | (unsigned)y[u].z;
+      hv[2 * u] = from_fix(x0 + y0);
+      hv[2 * u + 1] = from_fix(x1 + y1);
+    }
+  }
 };
 // residual after the O projection of layer i: h
 struct HOne {
   const long long* h;
   __device__ __forceinline__ double operator()(int i) const { return from_fix(ldc(h + i)); }
+  __device__ __forceinline__ void load8(int g, double (&hv)[8]) const {
+    const Coh16 H(h, MG_H * 8);
+    int4 x[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) x[u] = H.ld(64 * g + 16 * u);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      hv[2 * u] = from_fix(((long long)(unsigned)x[u].y << 32) | (unsigned)x[u].x);
+      hv[2 * u + 1] = from_fix(((long long)(unsigned)x[u].w << 32) | (unsigned)x[u].z);
+    }
+  }
 };
 
 // ---------------------------------------------------------------------------------------------
@@ -690,19 +731,24 @@ __global__ void __launch_bounds__(MG_NTH) k_mega_decode(const MegaArgs a) {
         b1[k] = b0[k] + MG_DOWN_SB;
       }
       mg_wload(W, Ly.down_qs, Ly.down_d, MG_FFN / 32, tl, b0, b1);
-      // the m values of the three slices come from gate/up tiles 4 b0 .. 4 b1 - 1 (8 m values per tile)
+      // the m values of the three slices come from gate/up tiles 4 b0 .. 4 b1 - 1 (8 m values per tile): one
+      // wait over the producers of all three (consecutive owners per slice)
+      int lo[3], n[3];
 #pragma unroll
       for (int k = 0; k < 3; ++k) {
-        const int lo = gu_owner(4 * b0[k]), hi = gu_owner(4 * b1[k] - 1);
-        sy.wait(hi - lo + 1, [lo](int i) { return lo + i; }, s_gu);
+        lo[k] = gu_owner(4 * b0[k]);
+        n[k] = gu_owner(4 * b1[k] - 1) - lo[k] + 1;
       }
+      sy.wait(n[0] + n[1] + n[2], [&](int i) { return i < n[0] ? lo[0] + i : (i < n[0] + n[1] ? lo[1] + i - n[0] : lo[2] + i - n[0] - n[1]); },
+              s_gu);
       Q355_MEGA_MARK(layer, 6);
+      const Coh16 M(ws.m, MG_FFN * 4);
       for (int task = threadIdx.x; task < 3 * MG_DOWN_SB * 4; task += MG_NTH) {
         const int k = task / (MG_DOWN_SB * 4);
         const int g = ((w + MG_NWG * k) / 96) * MG_DOWN_SB * 4 + task % (MG_DOWN_SB * 4);
-        float v[8];
-#pragma unroll
-        for (int u = 0; u < 8; ++u) v[u] = ldc(ws.m + 8 * g + u);
+        const int4 m0 = M.ld(32 * g), m1 = M.ld(32 * g + 16);
+        const float v[8] = {__int_as_float(m0.x), __int_as_float(m0.y), __int_as_float(m0.z), __int_as_float(m0.w),
+                            __int_as_float(m1.x), __int_as_float(m1.y), __int_as_float(m1.z), __int_as_float(m1.w)};
         mg_stage8(x, g, v);
       }
       __syncthreads();
