@@ -9,8 +9,8 @@
 //   QKV   WG t < 128: tile t (16 rows) of the 2048 QKV rows; RMSNorm of h + Q8_1 + dots + bias + RoPE;
 //         q and the new k/v rows -> device-coherent scratch; k/v also -> the paged cache (later tokens).
 //         needs all of h (a full barrier after the previous DOWN).
-//   ATTN  task (kv head g, page c, half) -> 3 query heads (waves 0..2); f64 partial (o, max, sum) per
-//         (head, page). Waits only for the 64 QKV tiles of group g.
+//   ATTN  task (kv head g, page c, query head) on WG 128 + task; f64 partial (o, max, sum) per (head,
+//         page). Waits for all 128 QKV tiles.
 //   O     WG w < 192: tile w % 96, heads 6 (w / 96) .. +5: merge their partials + Q8_1 + dots, add into h
 //         (int64 atomics). Waits only for the ATTN tasks of its group.
 //   GU    4-5 gate/up tiles per WG: RMSNorm of h + Q8_1 + dots + SwiGLU -> m (coherent scratch).
@@ -41,6 +41,8 @@ constexpr int MG_NTH = 256;          // threads per workgroup
 constexpr int MG_REP = 32;           // replicas of the barrier release word
 constexpr int MG_FS = 16;            // unsigneds between flags (64 B)
 constexpr int MG_H = 1536, MG_NH = 12, MG_NKV = 2, MG_FFN = 8960, MG_NQKV = 2048;
+constexpr int MG_AHPT = 1;                          // query heads per attention task
+constexpr int MG_ATPG = 6 / MG_AHPT;                // attention tasks per (kv group, page)
 constexpr int MG_GU_TILES = 2 * MG_FFN / 16;        // 1120
 constexpr int MG_DOWN_SLICES = 8, MG_DOWN_SB = MG_FFN / 32 / MG_DOWN_SLICES;   // 35 blocks per slice
 
@@ -58,7 +60,7 @@ struct MegaWs {
   unsigned* go;      // [MG_REP * MG_FS]
   unsigned* ctl;     // [0] epoch base, [16] error word
   float* q;          // [NH * HD]
-  float* kvnew;      // [2][NKV * HD]
+  __half* kvnew;     // [2][NKV * HD] the new token's k and v rows (fp16, as the cache holds them)
   double* part;      // [NH][max_chunks][HD + 2]
   float* m;          // [FFN]
   float* amax;       // [MG_NWG]
@@ -93,7 +95,7 @@ __device__ __forceinline__ MegaWs mega_ws(char* p, int max_chunks, int L) {
   w.accD = (long long*)p; p += (size_t)2 * MG_H * 8;
   w.part = (double*)p; p += (size_t)MG_NH * max_chunks * (HD + 2) * 8;
   w.q = (float*)p; p += (size_t)MG_NH * HD * 4;
-  w.kvnew = (float*)p; p += (size_t)2 * MG_NKV * HD * 4;
+  w.kvnew = (__half*)p; p += (size_t)2 * MG_NKV * HD * 4;
   w.m = (float*)p; p += (size_t)MG_FFN * 4;
   w.amax = (float*)p; p += (size_t)MG_NWG * 4;
   w.aidx = (int*)p;
@@ -112,6 +114,13 @@ struct Coh16 {
       : r(__builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, (int)bytes, 0x00020000)) {}
   __device__ __forceinline__ int4 ld(unsigned byte_off) const {
     return __builtin_bit_cast(int4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)byte_off, 0, 16));
+  }
+  __device__ __forceinline__ unsigned ld4(unsigned byte_off) const {
+    return __builtin_amdgcn_raw_buffer_load_b32(r, (int)byte_off, 0, 16);
+  }
+  // 2-byte device-scope store (the sc1 policy of the relaxed agent-scope atomic stores)
+  __device__ __forceinline__ void st2(unsigned byte_off, unsigned short v) const {
+    __builtin_amdgcn_raw_buffer_store_b16(v, r, (int)byte_off, 0, 16);
   }
 };
 
@@ -354,7 +363,8 @@ struct HOne {
 };
 
 // ---------------------------------------------------------------------------------------------
-// Attention task: kv group g, page c, query heads 6g + 3 half + (0..2). Wave w takes positions
+// Attention task: kv group g, page c, query heads 6g + hq .. + MG_AHPT - 1 (one head per task: the f64
+// score and P.V chains of one wave are latency-bound, so fewer heads per task shorten the phase). Wave w takes positions
 // 16w .. 16w + 15 of the page: lane (p = lane / 4, quarter dq = lane % 4) scores position 16w + p over
 // dims 32dq .. 32dq + 31 (f64, exact fp16 products), lanes of a position sum their quarters; the page
 // maximum is exchanged through LDS so every wave's e^(s - M) shares M, and lane l accumulates dims 2l, 2l+1
@@ -382,11 +392,12 @@ __device__ __forceinline__ void mg_attn_load(MgAttnRegs& R, const MegaArgs& a, c
 }
 
 __device__ __forceinline__ void mg_attn_task(const MegaArgs& a, const MegaLayer& Ly, const MegaWs& ws, int g, int c,
-                                             int half, int pos, char* lds, MgAttnRegs& R) {
-  double* qd = (double*)lds;                     // [3][HD] queries (f64)
-  double* red_m = qd + 3 * HD;                   // [3][4]
-  double* red_l = red_m + 12;                    // [3][4]
-  double* red_o = red_l + 12;                    // [4][3][HD]
+                                             int hq, int pos, char* lds, MgAttnRegs& R) {
+  constexpr int NQ = MG_AHPT;
+  double* qd = (double*)lds;                     // [NQ][HD] queries (f64)
+  double* red_m = qd + NQ * HD;                  // [NQ][4]
+  double* red_l = red_m + 4 * NQ;                // [NQ][4]
+  double* red_o = red_l + 4 * NQ;                // [4][NQ][HD]
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int p = lane >> 2, dq = lane & 3;
   const int row = 16 * wv + p, gp = c * PAGE + row;
@@ -394,28 +405,17 @@ __device__ __forceinline__ void mg_attn_task(const MegaArgs& a, const MegaLayer&
   u32x4 (&k4)[4] = R.k4;
   unsigned (&v2)[16] = R.v2;
   Q355_MEGA_MARK(31, 1);
-  for (int e = threadIdx.x; e < 3 * HD; e += MG_NTH)
-    qd[e] = (double)ldc(ws.q + (6 * g + 3 * half) * HD + e);
+  for (int e = threadIdx.x; e < NQ * HD; e += MG_NTH)
+    qd[e] = (double)ldc(ws.q + (6 * g + hq) * HD + e);
   // the new token's row (written in this launch) from the coherent scratch
   const int inew = pos - c * PAGE;
   if (inew >= 16 * wv && inew < 16 * wv + 16) {
+    const Coh16 KVN(ws.kvnew, 2 * MG_NKV * HD * 2);
     if (row == inew) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        unsigned u[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int d = 32 * dq + 8 * i + 2 * j;
-          const __half lo = __float2half_rn(ldc(ws.kvnew + g * HD + d));
-          const __half hi = __float2half_rn(ldc(ws.kvnew + g * HD + d + 1));
-          u[j] = (unsigned)__half_as_ushort(lo) | ((unsigned)__half_as_ushort(hi) << 16);
-        }
-        k4[i] = u32x4{u[0], u[1], u[2], u[3]};
-      }
+      for (int i = 0; i < 4; ++i) k4[i] = __builtin_bit_cast(u32x4, KVN.ld((g * HD + 32 * dq + 8 * i) * 2));
     }
-    const __half lo = __float2half_rn(ldc(ws.kvnew + MG_NKV * HD + g * HD + 2 * lane));
-    const __half hi = __float2half_rn(ldc(ws.kvnew + MG_NKV * HD + g * HD + 2 * lane + 1));
-    const unsigned nv = (unsigned)__half_as_ushort(lo) | ((unsigned)__half_as_ushort(hi) << 16);
+    const unsigned nv = KVN.ld4((MG_NKV * HD + g * HD + 2 * lane) * 2);
 #pragma unroll
     for (int r = 0; r < 16; ++r) v2[r] = (16 * wv + r == inew) ? nv : v2[r];
   }
@@ -424,9 +424,9 @@ __device__ __forceinline__ void mg_attn_task(const MegaArgs& a, const MegaLayer&
   __syncthreads();
   Q355_MEGA_MARK(31, 2);
 
-  double ev[3];
+  double ev[NQ];
 #pragma unroll
-  for (int h = 0; h < 3; ++h) {
+  for (int h = 0; h < NQ; ++h) {
     const double* qh = qd + h * HD + 32 * dq;
     double sp[4] = {0.0, 0.0, 0.0, 0.0};
 #pragma unroll
@@ -446,11 +446,12 @@ __device__ __forceinline__ void mg_attn_task(const MegaArgs& a, const MegaLayer&
     const double mw = wave_max_d(sc);                   // each position appears 4 times: harmless for max
     if (lane == 0) red_m[h * 4 + wv] = mw;
     ev[h] = sc;
+    Q355_MEGA_MARK(31, 8 + h);
   }
   __syncthreads();
   Q355_MEGA_MARK(31, 3);
 #pragma unroll
-  for (int h = 0; h < 3; ++h) {
+  for (int h = 0; h < NQ; ++h) {
     const double M = fmax(fmax(red_m[h * 4], red_m[h * 4 + 1]), fmax(red_m[h * 4 + 2], red_m[h * 4 + 3]));
     const double e = valid ? exp(ev[h] - M) : 0.0;
     const double lw = wave_sum_d(dq == 0 ? e : 0.0);    // one copy of each position
@@ -466,17 +467,17 @@ __device__ __forceinline__ void mg_attn_task(const MegaArgs& a, const MegaLayer&
       if (r & 1) { o2 = fma(er, (double)vf.x, o2); o3 = fma(er, (double)vf.y, o3); }
       else { o0 = fma(er, (double)vf.x, o0); o1 = fma(er, (double)vf.y, o1); }
     }
-    red_o[(wv * 3 + h) * HD + 2 * lane] = o0 + o2;
-    red_o[(wv * 3 + h) * HD + 2 * lane + 1] = o1 + o3;
+    red_o[(wv * NQ + h) * HD + 2 * lane] = o0 + o2;
+    red_o[(wv * NQ + h) * HD + 2 * lane + 1] = o1 + o3;
     if (lane == 0) red_l[h * 4 + wv] = lw;
   }
   __syncthreads();
   Q355_MEGA_MARK(31, 4);
-  for (int e = threadIdx.x; e < 3 * HD; e += MG_NTH) {
+  for (int e = threadIdx.x; e < NQ * HD; e += MG_NTH) {
     const int h = e / HD, d = e % HD;
-    const double o = ((red_o[(0 * 3 + h) * HD + d] + red_o[(1 * 3 + h) * HD + d]) + red_o[(2 * 3 + h) * HD + d]) +
-                     red_o[(3 * 3 + h) * HD + d];
-    double* P = ws.part + ((size_t)(6 * g + 3 * half + h) * a.max_chunks + c) * (HD + 2);
+    const double o = ((red_o[(0 * NQ + h) * HD + d] + red_o[(1 * NQ + h) * HD + d]) + red_o[(2 * NQ + h) * HD + d]) +
+                     red_o[(3 * NQ + h) * HD + d];
+    double* P = ws.part + ((size_t)(6 * g + hq + h) * a.max_chunks + c) * (HD + 2);
     stc(P + d, o);
     if (d == 0) {
       const double M = fmax(fmax(red_m[h * 4], red_m[h * 4 + 1]), fmax(red_m[h * 4 + 2], red_m[h * 4 + 3]));
@@ -492,6 +493,7 @@ __device__ __forceinline__ void mg_attn_task(const MegaArgs& a, const MegaLayer&
 // merge of one head's page partials (one wave, coherent loads), as attn_merge_head
 __device__ __forceinline__ void mg_merge_head(const double* P, int nch, double* out) {
   const int lane = threadIdx.x & 63;
+  const Coh16 PC(P, nch * (HD + 2) * 8);
   const double* pc = P + (size_t)min(lane, nch - 1) * (HD + 2);
   const double mc = ldc(pc + HD), lc = ldc(pc + HD + 1);
   const double M = wave_max_d(lane < nch ? mc : -INFINITY);
@@ -502,10 +504,10 @@ __device__ __forceinline__ void mg_merge_head(const double* P, int nch, double* 
   for (int c0 = 0; c0 < nch; c0 += 8) {
     double v0[8], v1[8];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const double* q = P + (size_t)min(c0 + u, nch - 1) * (HD + 2) + 2 * lane;
-      v0[u] = ldc(q);
-      v1[u] = ldc(q + 1);
+    for (int u = 0; u < 8; ++u) {                     // dims 2 lane, 2 lane + 1: one 16-byte load (rows are
+      const int4 t = PC.ld(((min(c0 + u, nch - 1) * (HD + 2)) + 2 * lane) * 8);   // 1040 B apart)
+      v0[u] = __builtin_bit_cast(double, make_int2(t.x, t.y));
+      v1[u] = __builtin_bit_cast(double, make_int2(t.z, t.w));
     }
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
@@ -574,7 +576,7 @@ __global__ void __launch_bounds__(MG_NTH) k_mega_decode(const MegaArgs a) {
     return;
   }
   const int nch = pos / PAGE + 1;
-  const int n_attn = MG_NKV * nch * 2;
+  const int n_attn = MG_NKV * nch * MG_ATPG;
   MgX x;
   x.q = (int8_t*)lds;                                  // K blocks of the widest operand (down: 280)
   x.d = (float*)(lds + MG_FFN);
@@ -614,6 +616,7 @@ __global__ void __launch_bounds__(MG_NTH) k_mega_decode(const MegaArgs a) {
       mg_dots(Wq, x, qkv_b0, qkv_b1, reinterpret_cast<double(*)[1][16]>(part_s), rv);
       Q355_MEGA_MARK(layer, 10);
       if (threadIdx.x < 16) {
+        const Coh16 KVN(ws.kvnew, 2 * MG_NKV * HD * 2);
         const double v = rv[0][r] + (double)bias;
         const int nq = MG_NH * HD, nk = MG_NKV * HD;
         if (row < nq + nk) {
@@ -629,13 +632,13 @@ __global__ void __launch_bounds__(MG_NTH) k_mega_decode(const MegaArgs a) {
           } else {
             const int kvh = (row - nq) / HD;
             Ly.kc[(((size_t)pg * MG_NKV + kvh) * PAGE + pos % PAGE) * HD + dim] = hv;
-            stc(ws.kvnew + kvh * HD + dim, __half2float(hv));
+            KVN.st2((kvh * HD + dim) * 2, __half_as_ushort(hv));
           }
         } else {
           const int rvv = row - nq - nk, kvh = rvv / HD, dim = rvv % HD;
           const __half hv = half_rn(v);
           Ly.vc[(((size_t)pg * MG_NKV + kvh) * PAGE + pos % PAGE) * HD + dim] = hv;
-          stc(ws.kvnew + MG_NKV * HD + kvh * HD + dim, __half2float(hv));
+          KVN.st2((MG_NKV * HD + kvh * HD + dim) * 2, __half_as_ushort(hv));
         }
       }
     }
@@ -647,13 +650,13 @@ __global__ void __launch_bounds__(MG_NTH) k_mega_decode(const MegaArgs a) {
     // of this layer's QKV phase any more and the O phase may add into it ----
     const unsigned s_attn = ++seq;
     for (int idx = (w - MG_NQKV / 16 + MG_NWG) % MG_NWG; idx < n_attn; idx += MG_NWG) {
-      const int g = idx / (2 * nch), c = (idx / 2) % nch, half = idx & 1;
+      const int g = idx / (MG_ATPG * nch), c = (idx / MG_ATPG) % nch, hq = (idx % MG_ATPG) * MG_AHPT;
       MgAttnRegs AR;
       mg_attn_load(AR, a, Ly, g, c);
       Q355_MEGA_MARK(31, 7);
       sy.wait(MG_NQKV / 16, [](int i) { return i; }, s_qkv);
       Q355_MEGA_MARK(31, 0);
-      mg_attn_task(a, Ly, ws, g, c, half, pos, lds, AR);
+      mg_attn_task(a, Ly, ws, g, c, hq, pos, lds, AR);
     }
     Q355_MEGA_MARK(layer, 1);
     sy.publish(s_attn);
@@ -665,7 +668,7 @@ __global__ void __launch_bounds__(MG_NTH) k_mega_decode(const MegaArgs a) {
       MgW<1, 2> W;
       const int tl[1] = {tile}, b0[1] = {24 * sl}, b1[1] = {24 * sl + 24};
       mg_wload(W, Ly.o_qs, Ly.o_d, MG_H / 32, tl, b0, b1);
-      sy.wait(2 * nch, [sl, nch](int i) { return attn_wg(sl * 2 * nch + i); }, s_attn);
+      sy.wait(MG_ATPG * nch, [sl, nch](int i) { return attn_wg(sl * MG_ATPG * nch + i); }, s_attn);
       Q355_MEGA_MARK(layer, 2);
       const int wv = threadIdx.x >> 6;
       for (int hh = wv; hh < 6; hh += 4)
