@@ -108,10 +108,17 @@ __device__ __forceinline__ bool seq_reached(unsigned v, unsigned seq) { return (
 
 // 16-byte device-scope loads (buffer loads with the sc1 policy, as the relaxed agent-scope atomic loads use):
 // coherent with other CUs' device-scope stores, four times the width of ldc, ordinary wait-count tracking
+// The base address must be the same in every lane of the wave (it is moved to scalar registers; a per-lane
+// base would make the compiler loop over the distinct values one load at a time).
 struct Coh16 {
   __amdgpu_buffer_rsrc_t r;
+  __device__ __forceinline__ static void* uniform(const void* p) {
+    const unsigned long long v = (unsigned long long)p;
+    const unsigned lo = __builtin_amdgcn_readfirstlane((unsigned)v), hi = __builtin_amdgcn_readfirstlane((unsigned)(v >> 32));
+    return (void*)(((unsigned long long)hi << 32) | lo);
+  }
   __device__ __forceinline__ Coh16(const void* p, unsigned bytes)
-      : r(__builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, (int)bytes, 0x00020000)) {}
+      : r(__builtin_amdgcn_make_buffer_rsrc(uniform(p), 0, (int)bytes, 0x00020000)) {}
   __device__ __forceinline__ int4 ld(unsigned byte_off) const {
     return __builtin_bit_cast(int4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)byte_off, 0, 16));
   }
@@ -523,6 +530,62 @@ __device__ __forceinline__ void mg_merge_head(const double* P, int nch, double* 
   out[2 * lane + 1] = o1 / L;
 }
 
+// merge of the 6 heads of one kv group when they have at most 8 page partials, every load issued at once (one
+// memory round trip): thread t < 48 takes (head t / 8, chunk t % 8) and forms w_c = e^(m_c - M) and L (the
+// max and the pairwise sum over its 8 lanes, chunks past nch as zero: the same tree as mg_merge_head's 64-lane
+// sum) into LDS; then thread t < 192 takes head t / 32, dims 4 (t % 32) .. + 3: o = sequential fmas in chunk
+// order, o / L -- mg_merge_head's arithmetic.
+__device__ __forceinline__ void mg_merge6_short(const double* P0, int max_chunks, int nch, double (*ob)[HD],
+                                                double (*wsh)[9]) {
+  const int h = threadIdx.x >> 5, dq = threadIdx.x & 31;
+  int4 ml, va[8], vb[8];
+  const Coh16 PC(P0, 6 * max_chunks * (HD + 2) * 8);     // the 6 heads' partials, one uniform base
+  if (threadIdx.x < 48) {                                // (m, l) first: the weights start while the values arrive
+    const unsigned hc = (unsigned)(threadIdx.x >> 3) * max_chunks + min((int)threadIdx.x & 7, nch - 1);
+    ml = PC.ld((hc * (HD + 2) + HD) * 8);
+  }
+  if (threadIdx.x < 192) {
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const unsigned c = ((unsigned)h * max_chunks + min(u, nch - 1)) * (HD + 2);
+      va[u] = PC.ld((c + 4 * dq) * 8);
+      vb[u] = PC.ld((c + 4 * dq + 2) * 8);
+    }
+  }
+  __asm__ __volatile__("" ::: "memory");                 // the value loads stay issued here
+  if (threadIdx.x < 48) {
+    const int hh = threadIdx.x >> 3, c = threadIdx.x & 7;
+    const double m = c < nch ? __builtin_bit_cast(double, make_int2(ml.x, ml.y)) : -INFINITY;
+    double M = fmax(m, dpp_d<DPP_XOR1>(m));              // max and sum over the 8 lanes of a head
+    M = fmax(M, dpp_d<DPP_XOR2>(M));
+    M = fmax(M, dpp_d<DPP_HALF_MIRROR>(M));
+    const double w = c < nch ? exp(m - M) : 0.0;
+    double t = w * (c < nch ? __builtin_bit_cast(double, make_int2(ml.z, ml.w)) : 0.0);
+    t += dpp_d<DPP_XOR1>(t);
+    t += dpp_d<DPP_XOR2>(t);
+    t += dpp_d<DPP_HALF_MIRROR>(t);
+    wsh[hh][c] = w;
+    if (c == 0) wsh[hh][8] = t;
+  }
+  Q355_MEGA_MARK(32, 1);
+  __syncthreads();
+  Q355_MEGA_MARK(32, 2);
+  if (threadIdx.x < 192) {
+    double o[4] = {0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const double w = wsh[h][u];
+      o[0] = fma(w, __builtin_bit_cast(double, make_int2(va[u].x, va[u].y)), o[0]);
+      o[1] = fma(w, __builtin_bit_cast(double, make_int2(va[u].z, va[u].w)), o[1]);
+      o[2] = fma(w, __builtin_bit_cast(double, make_int2(vb[u].x, vb[u].y)), o[2]);
+      o[3] = fma(w, __builtin_bit_cast(double, make_int2(vb[u].z, vb[u].w)), o[3]);
+    }
+    const double L = wsh[h][8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) ob[h][4 * dq + i] = o[i] / L;
+  }
+}
+
 // ---------------------------------------------------------------------------------------------
 // which workgroup runs which task
 __device__ __forceinline__ int gu_tile0(int w) { return (MG_GU_TILES * w) / MG_NWG; }
@@ -670,9 +733,15 @@ __global__ void __launch_bounds__(MG_NTH) k_mega_decode(const MegaArgs a) {
       mg_wload(W, Ly.o_qs, Ly.o_d, MG_H / 32, tl, b0, b1);
       sy.wait(MG_ATPG * nch, [sl, nch](int i) { return attn_wg(sl * MG_ATPG * nch + i); }, s_attn);
       Q355_MEGA_MARK(layer, 2);
-      const int wv = threadIdx.x >> 6;
-      for (int hh = wv; hh < 6; hh += 4)
-        mg_merge_head(ws.part + (size_t)(6 * sl + hh) * a.max_chunks * (HD + 2), nch, ob[hh]);
+      if (nch <= 8) {
+        mg_merge6_short(ws.part + (size_t)(6 * sl) * a.max_chunks * (HD + 2), a.max_chunks, nch, ob,
+                        reinterpret_cast<double(*)[9]>(part_s));
+      } else {
+        const int wv = threadIdx.x >> 6;
+        for (int hh = wv; hh < 6; hh += 4)
+          mg_merge_head(ws.part + (size_t)(6 * sl + hh) * a.max_chunks * (HD + 2), nch, ob[hh]);
+      }
+      Q355_MEGA_MARK(layer, 15);
       __syncthreads();
       if (threadIdx.x < 96) {                            // 768 values, 8 per thread, quads whole
         float v[8];

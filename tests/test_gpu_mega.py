@@ -15,7 +15,7 @@ CFG_S = QM.Config(L=2, V=4096)
 @pytest.fixture(scope="module")
 def small(cuda):
     w = QM.random_weights(CFG_S, seed=21)
-    return w, QM.DeviceModel(w, CFG_S, maxlen=512), OM.Model(OM.Config(L=2, V=4096), w, maxlen=512)
+    return w, QM.DeviceModel(w, CFG_S, maxlen=1024), OM.Model(OM.Config(L=2, V=4096), w, maxlen=512)
 
 
 def test_mega_step_matches_graph_step(small):
@@ -34,6 +34,33 @@ def test_mega_step_matches_graph_step(small):
         assert np.abs(la - lb).max() <= 1e-6 * np.abs(la).max()
         assert int(a.tok.item()) == int(b.tok.item())
         assert int(a.pos.item()) == int(b.pos.item())
+    assert np.abs(a.h_f64().cpu().numpy() - b.h_f64().cpu().numpy()).max() < 1e-9
+
+
+@pytest.mark.parametrize("pos", [300, 700])
+def test_mega_matches_graph_over_many_pages(small, pos):
+    """Contexts of several pages (5 and 11 at the first step: the short and the general partial merge): caches
+    filled with the same N(0, 1) rows, then 4 steps of both decoders; logits to f64 rounding, tokens equal."""
+    import torch
+    w, dm, om = small
+    a = QM.Decoder(dm, T=1, max_ctx=1024)
+    b = QG.MegaDecoder(dm, max_ctx=1024)
+    g = torch.Generator(device="cuda").manual_seed(pos)
+    for i in range(CFG_S.L):
+        a.kc[i].normal_(generator=g)
+        a.vc[i].normal_(generator=g)
+        b.kc[i].copy_(a.kc[i])
+        b.vc[i].copy_(a.vc[i])
+    for d in (a, b):
+        d.pos.fill_(pos)
+        d.tok.fill_(77)
+    for _ in range(4):
+        a.step()
+        b.step()
+        la, lb = a.logits[0].cpu().numpy(), b.logits[0].cpu().numpy()
+        assert b.error() == 0
+        assert np.abs(la - lb).max() <= 1e-6 * np.abs(la).max()
+        assert int(a.tok.item()) == int(b.tok.item()) and int(a.pos.item()) == int(b.pos.item())
     assert np.abs(a.h_f64().cpu().numpy() - b.h_f64().cpu().numpy()).max() < 1e-9
 
 
