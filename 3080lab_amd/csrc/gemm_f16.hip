@@ -15,6 +15,10 @@
 #include "common.h"
 #include "q355_kernels.h"
 
+#ifndef Q355_TRACE_POINT
+#define Q355_TRACE_POINT(k)
+#endif
+
 namespace q355 {
 
 typedef _Float16 fh8 __attribute__((ext_vector_type(8)));
@@ -147,6 +151,7 @@ __global__ void __launch_bounds__(NW * 64) k_gemm_f16(const GemvArgs a) {
 // registers; partials reduce over waves through LDS into the shared epilogues.
 template <int TG, int NT, int NW, int KPW, int EPI>
 __global__ void __launch_bounds__(NW * 64) k_gemm_f16r(const GemvArgs a) {
+  Q355_TRACE_POINT(0);
   __shared__ float part[NW][NT][16 * TG][16];
   constexpr int TT = 16 * TG;
   const int K = a.K, nb = K / 32;
@@ -177,6 +182,7 @@ __global__ void __launch_bounds__(NW * 64) k_gemm_f16r(const GemvArgs a) {
     static_assert(NT * TT * 16 <= NW * 64, "one QKV output per thread");
     qp = qkv_prefetch<TT, NT>(a, tile0);
   }
+  Q355_TRACE_POINT(1);
   ff4 acc[NT][TG];
 #pragma unroll
   for (int t = 0; t < NT; ++t)
@@ -199,9 +205,12 @@ __global__ void __launch_bounds__(NW * 64) k_gemm_f16r(const GemvArgs a) {
     for (int g = 0; g < TG; ++g)
 #pragma unroll
       for (int v = 0; v < 4; ++v) part[wv][t][16 * g + li][4 * lg + v] = acc[t][g][v];
+  Q355_TRACE_POINT(2);
   __syncthreads();
+  Q355_TRACE_POINT(3);
   if constexpr (EPI == EPI_QKV) qkv_store<NW, TT, NT>(a, part, tile0, qp);
   else epilogue<NW, TT, NT, EPI>(a, part, tile0);
+  Q355_TRACE_POINT(5);
 }
 
 // Decode-batch O product + residual in the fp16 arithmetic with the split-attention merge in its activation

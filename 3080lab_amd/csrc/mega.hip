@@ -6,14 +6,14 @@
 // rounding of q/K/V), so the tokens follow the same oracle.
 //
 // Phases of one layer and their dependencies:
-//   QKV   WG t < 128: tile t (16 rows) of the 2048 QKV rows; RMSNorm of h + Q8_1 + dots + bias + RoPE;
-//         q and the new k/v rows -> device-coherent scratch; k/v also -> the paged cache (later tokens).
+//   QKV   WG 8 + t, t < 128: tile t (16 rows) of the 2048 QKV rows; RMSNorm of h + Q8_1 + dots + bias +
+//         RoPE; q and the new k/v rows -> device-coherent scratch; k/v also -> the paged cache (later tokens).
 //         needs all of h (a full barrier after the previous DOWN).
-//   ATTN  task (kv head g, page c, query head) on WG 128 + task; f64 partial (o, max, sum) per (head,
+//   ATTN  task (kv head g, page c, query head) on WG 136 + task; f64 partial (o, max, sum) per (head,
 //         page). Waits for all 128 QKV tiles.
 //   O     WG w < 192: tile w % 96, heads 6 (w / 96) .. +5: merge their partials + Q8_1 + dots, add into h
 //         (int64 atomics). Waits only for the ATTN tasks of its group.
-//   GU    4-5 gate/up tiles per WG: RMSNorm of h + Q8_1 + dots + SwiGLU -> m (coherent scratch).
+//   GU    4-5 gate/up tiles per WG 8..255: RMSNorm of h + Q8_1 + dots + SwiGLU -> m (coherent scratch).
 //         needs all of h (a full barrier after O).
 //   DOWN  3 (tile, 35-block K slice) tasks per WG: Q8_1 of the m slice + dots, add into h. Waits only
 //         for the GU workgroups that produced the slice.
@@ -588,14 +588,22 @@ __device__ __forceinline__ void mg_merge6_short(const double* P0, int max_chunks
 
 // ---------------------------------------------------------------------------------------------
 // which workgroup runs which task
-__device__ __forceinline__ int gu_tile0(int w) { return (MG_GU_TILES * w) / MG_NWG; }
+// Workgroups 0..7 gather the barrier flags; their gather loops would wait for any weight loads in flight (the
+// vector memory counter is in order), so they take no QKV or gate/up tiles: QKV tile t runs on workgroup
+// MG_GATH + t, the gate/up tiles spread over workgroups MG_GATH..255 (at most 5 each either way), attention
+// task i on workgroup MG_GATH + 128 + i.
+constexpr int MG_GATH = 8;
+constexpr int MG_QKV_WG0 = MG_GATH, MG_ATT_WG0 = MG_GATH + MG_NQKV / 16;
+__device__ __forceinline__ int gu_tile0(int w) {
+  return w < MG_GATH ? 0 : (MG_GU_TILES * (w - MG_GATH)) / (MG_NWG - MG_GATH);
+}
 __device__ __forceinline__ int gu_owner(int t) {      // the workgroup whose tile range holds gate/up tile t
-  int w = (t * MG_NWG) / MG_GU_TILES;
+  int w = MG_GATH + (t * (MG_NWG - MG_GATH)) / MG_GU_TILES;
   while (w + 1 < MG_NWG && gu_tile0(w + 1) <= t) ++w;
   while (gu_tile0(w) > t) --w;
   return w;
 }
-__device__ __forceinline__ int attn_wg(int idx) { return (128 + idx) % MG_NWG; }
+__device__ __forceinline__ int attn_wg(int idx) { return (MG_ATT_WG0 + idx) % MG_NWG; }
 
 // head chunk ck of this workgroup's tile range [t0, t1): tiles t0 + 8 ck .. (clamped to t1 - 1)
 __device__ __forceinline__ void mg_head_load(MgW<8, 3>& W, const MegaArgs& a, int t0, int t1, int ck) {
@@ -646,11 +654,12 @@ __global__ void __launch_bounds__(MG_NTH) k_mega_decode(const MegaArgs a) {
   x.s = (int*)(lds + MG_FFN + (MG_FFN / 32) * 4);
   const HFromEmbed emb{a.emb_qs, a.emb_d, tok, MG_H / 32};
 
-  // weights of the next QKV / gate-up phase are loaded between a barrier's arrive and finish (except on
-  // the gathering workgroups 0..7, whose gather loops would otherwise wait for them)
+  // weights of the next QKV / gate-up phase are loaded between a barrier's arrive and finish
   MgW<1, 3> Wq;
-  const int qkv_b0[1] = {0}, qkv_b1[1] = {MG_H / 32}, qkv_tl[1] = {w < MG_NQKV / 16 ? w : 0};
-  if (w < MG_NQKV / 16) mg_wload(Wq, a.layers[0].qkv_qs, a.layers[0].qkv_d, MG_H / 32, qkv_tl, qkv_b0, qkv_b1);
+  const int qt = w - MG_QKV_WG0;                       // QKV tile of this workgroup (valid for 0..127)
+  const bool is_qkv = qt >= 0 && qt < MG_NQKV / 16;
+  const int qkv_b0[1] = {0}, qkv_b1[1] = {MG_H / 32}, qkv_tl[1] = {is_qkv ? qt : 0};
+  if (is_qkv) mg_wload(Wq, a.layers[0].qkv_qs, a.layers[0].qkv_d, MG_H / 32, qkv_tl, qkv_b0, qkv_b1);
 
   // the residual stream lives in a.h (int64 fixed point): layer 0's O phase starts it from the embedding row
   // (written here by the owners of its 96 tiles, before their first flag), O sums are added into it, and the
@@ -665,10 +674,9 @@ __global__ void __launch_bounds__(MG_NTH) k_mega_decode(const MegaArgs a) {
     const HSum2 prev{hres, accPrev};
     // ---- QKV ----
     const unsigned s_qkv = ++seq;
-    if (w < MG_NQKV / 16) {
-      if (w < 8 && layer > 0) mg_wload(Wq, Ly.qkv_qs, Ly.qkv_d, MG_H / 32, qkv_tl, qkv_b0, qkv_b1);
+    if (is_qkv) {
       // epilogue operands (bias pair, RoPE angle, page) loaded before the normalisation
-      const int r = threadIdx.x & 15, row = w * 16 + r;
+      const int r = threadIdx.x & 15, row = qt * 16 + r;
       const float bias = Ly.qkv_b[row], bias2 = Ly.qkv_b[row ^ 1];
       const int e2 = row % HD, ci = e2 >> 1;
       const float rc = a.rope_cos[(size_t)pos * (HD / 2) + ci], rs = a.rope_sin[(size_t)pos * (HD / 2) + ci];
@@ -712,12 +720,12 @@ __global__ void __launch_bounds__(MG_NTH) k_mega_decode(const MegaArgs a) {
     // all 128 QKV workgroups (not only the task's group), so once attention is done nobody reads the residual
     // of this layer's QKV phase any more and the O phase may add into it ----
     const unsigned s_attn = ++seq;
-    for (int idx = (w - MG_NQKV / 16 + MG_NWG) % MG_NWG; idx < n_attn; idx += MG_NWG) {
+    for (int idx = (w - MG_ATT_WG0 + MG_NWG) % MG_NWG; idx < n_attn; idx += MG_NWG) {
       const int g = idx / (MG_ATPG * nch), c = (idx / MG_ATPG) % nch, hq = (idx % MG_ATPG) * MG_AHPT;
       MgAttnRegs AR;
       mg_attn_load(AR, a, Ly, g, c);
       Q355_MEGA_MARK(31, 7);
-      sy.wait(MG_NQKV / 16, [](int i) { return i; }, s_qkv);
+      sy.wait(MG_NQKV / 16, [](int i) { return MG_QKV_WG0 + i; }, s_qkv);
       Q355_MEGA_MARK(31, 0);
       mg_attn_task(a, Ly, ws, g, c, hq, pos, lds, AR);
     }
@@ -767,16 +775,15 @@ __global__ void __launch_bounds__(MG_NTH) k_mega_decode(const MegaArgs a) {
     MgW<5, 3> Wg;
     int gtl[5], gb0[5], gb1[5];
 #pragma unroll
-    for (int t = 0; t < 5; ++t) { gtl[t] = gt0 + min(t, gnt - 1); gb0[t] = 0; gb1[t] = MG_H / 32; }
-    if (w >= 8) mg_wload(Wg, Ly.gu_qs, Ly.gu_d, MG_H / 32, gtl, gb0, gb1);
+    for (int t = 0; t < 5; ++t) { gtl[t] = gt0 + min(t, max(gnt - 1, 0)); gb0[t] = 0; gb1[t] = MG_H / 32; }
+    if (gnt > 0) mg_wload(Wg, Ly.gu_qs, Ly.gu_d, MG_H / 32, gtl, gb0, gb1);
     sy.finish(s_o);
     Q355_MEGA_MARK(layer, 4);
 
     // ---- gate/up + SwiGLU ----
     const unsigned s_gu = ++seq;
-    {
+    if (gnt > 0) {                                       // (the gathering workgroups have no tiles)
       const int t0 = gt0, nt = gnt;
-      if (w < 8) mg_wload(Wg, Ly.gu_qs, Ly.gu_d, MG_H / 32, gtl, gb0, gb1);
       mg_rms_stage(HOne{hres}, Ly.ln2, a.eps, x, red);
       Q355_MEGA_MARK(layer, 11);
       mg_dots(Wg, x, gb0, gb1, reinterpret_cast<double(*)[5][16]>(part_s), rv);
@@ -835,7 +842,7 @@ __global__ void __launch_bounds__(MG_NTH) k_mega_decode(const MegaArgs a) {
     }
     Q355_MEGA_MARK(layer, 7);
     sy.arrive(s_down);
-    if (w >= 8 && w < MG_NQKV / 16 && layer + 1 < a.L)
+    if (is_qkv && layer + 1 < a.L)
       mg_wload(Wq, a.layers[layer + 1].qkv_qs, a.layers[layer + 1].qkv_d, MG_H / 32, qkv_tl, qkv_b0, qkv_b1);
     sy.finish(s_down);
     Q355_MEGA_MARK(layer, 8);

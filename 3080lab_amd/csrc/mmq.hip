@@ -190,6 +190,7 @@ __device__ __forceinline__ long q8_1_mfma8(const float (&x)[8], float& df) {
 // (xf, the SwiGLU output) quantized to Q8_1 in registers. Partials reduce over waves through LDS.
 template <int TG, int NT, int NW, int KPW, int EPI, bool XF32>
 __global__ void __launch_bounds__(NW * 64) k_mmq_r(const GemvArgs a) {
+  Q355_TRACE_POINT(0);
   __shared__ float part[NW][NT][16 * TG][16];
   constexpr int TT = 16 * TG;
   const int K = a.K, nb = K / 32;
@@ -246,6 +247,7 @@ __global__ void __launch_bounds__(NW * 64) k_mmq_r(const GemvArgs a) {
     static_assert(NT * TT * 16 <= NW * 64, "one QKV output per thread");
     qp = qkv_prefetch<TT, NT>(a, tile0);
   }
+  Q355_TRACE_POINT(1);
   float acc[NT][TG][4];
 #pragma unroll
   for (int t = 0; t < NT; ++t)
@@ -286,9 +288,12 @@ __global__ void __launch_bounds__(NW * 64) k_mmq_r(const GemvArgs a) {
     for (int g = 0; g < TG; ++g)
 #pragma unroll
       for (int v = 0; v < 4; ++v) part[wv][t][16 * g + li][4 * lg + v] = acc[t][g][v];
+  Q355_TRACE_POINT(2);
   __syncthreads();
+  Q355_TRACE_POINT(3);
   if constexpr (EPI == EPI_QKV) qkv_store<NW, TT, NT>(a, part, tile0, qp);
   else epilogue<NW, TT, NT, EPI>(a, part, tile0);
+  Q355_TRACE_POINT(5);
 }
 
 template <int TG, int NT, int NW, int EPI>
