@@ -145,16 +145,18 @@ struct MgSync {
   __device__ __forceinline__ bool failed() const { return ldc(err) != 0u; }
   __device__ __forceinline__ void fail() const { stc(err, 1u); }
 
-  // wave 0 polls the flags of workgroups id(0..n-1) until all reach seq; then the workgroup proceeds
+  // wave 0 polls the flags of workgroups id(0..n-1) until all reach seq; then the workgroup proceeds. (Keeping
+  // several rounds of polls in flight, staggered, measured slower: a flag takes ~1 us to be seen either way.)
   template <typename F>
   __device__ __forceinline__ void wait(int n, F id, unsigned seq) const {
     if (threadIdx.x < 64) {
       const long long t0 = wall_clock64();
       while (true) {
+        const unsigned e = ldc(err);                     // in flight with the flags: one round trip per poll
         bool ok = true;
         for (int i = threadIdx.x; i < n; i += 64) ok &= seq_reached(ldc(flags + id(i) * MG_FS), seq);
         if (__all(ok)) break;
-        if (wall_clock64() - t0 > limit || failed()) { if (threadIdx.x == 0) fail(); break; }
+        if (e != 0u || wall_clock64() - t0 > limit) { if (threadIdx.x == 0) fail(); break; }
       }
     }
     __syncthreads();
@@ -170,19 +172,21 @@ struct MgSync {
     if (blockIdx.x < 8 && threadIdx.x < 64) {
       const long long t0 = wall_clock64();
       while (true) {
+        const unsigned e = ldc(err);
         bool ok = true;
         for (int i = (int)blockIdx.x + 8 * lane; i < MG_NWG; i += 512) ok &= seq_reached(ldc(flags + i * MG_FS), seq);
         if (__all(ok)) break;
-        if (wall_clock64() - t0 > limit || failed()) { if (lane == 0) fail(); break; }
+        if (e != 0u || wall_clock64() - t0 > limit) { if (lane == 0) fail(); break; }
       }
       if (lane == 0) stc(go + blockIdx.x * MG_FS, seq);
     }
     if (threadIdx.x < 64) {
       const long long t0 = wall_clock64();
       while (true) {
+        const unsigned e = ldc(err);
         const bool ok = lane >= 8 || seq_reached(ldc(go + lane * MG_FS), seq);
         if (__all(ok)) break;
-        if (wall_clock64() - t0 > limit || failed()) { if (lane == 0) fail(); break; }
+        if (e != 0u || wall_clock64() - t0 > limit) { if (lane == 0) fail(); break; }
       }
     }
     __syncthreads();
@@ -795,6 +799,10 @@ __global__ void __launch_bounds__(MG_NTH) k_mega_decode(const MegaArgs a) {
       }
     }
     Q355_MEGA_MARK(layer, 5);
+#ifdef Q355_MEGA_PROBE
+    __builtin_amdgcn_s_waitcnt(0);
+    Q355_MEGA_MARK(33, 0);
+#endif
     sy.publish(s_gu);
 
     // ---- down: into this layer's accD slot ----
