@@ -13,6 +13,10 @@
 #include "common.h"
 #include "q355_kernels.h"
 
+#ifndef Q355_TRACE_POINT
+#define Q355_TRACE_POINT(k)
+#endif
+
 namespace q355 {
 
 constexpr int KROW = HD + 8;  // padded K row in LDS (halves)
@@ -215,6 +219,7 @@ __device__ __forceinline__ void attn_out8(const AttnArgs& a, int j, int h, int d
 
 template <int KW>
 __global__ void __launch_bounds__(4 * PAGE / KW * 64) k_attn_decode_mfma(const AttnArgs a) {
+  Q355_TRACE_POINT(0);
   constexpr int NWV = 4 * PAGE / KW, ROW = KW + 4;     // waves; Vt row (one dim, KW keys) in halves
   __shared__ __align__(16) _Float16 vt[NWV][HD][ROW];
   __shared__ float wml[NWV][16][2];
@@ -278,6 +283,7 @@ __global__ void __launch_bounds__(4 * PAGE / KW * 64) k_attn_decode_mfma(const A
         bm = fmaxf(bm, sc[t][v]);
       }
     bm = col4_max(bm);                                  // key 0 of a live wave is valid: finite
+    Q355_TRACE_POINT(1);
     ml2 = bm * sl2;
     ah8 pB[KW / 32];
 #pragma unroll
@@ -321,7 +327,9 @@ __global__ void __launch_bounds__(4 * PAGE / KW * 64) k_attn_decode_mfma(const A
   }
 
   // the wave partials -> LDS (over the Vt slices), merged per (head, 8 dims) by thread t < 256
+  Q355_TRACE_POINT(2);
   __syncthreads();
+  Q355_TRACE_POINT(3);
   float* po = (float*)&vt[0][0][0];                     // [NWV waves][16 heads][HD]
 #pragma unroll
   for (int dt = 0; dt < 8; ++dt) *(af4*)(po + (wv * 16 + li) * HD + 16 * dt + 4 * lg) = acc[dt];

@@ -523,25 +523,6 @@ static int launch_mmq_r_tg(const GemvArgs& a, hipStream_t s) {
     hipLaunchKernelGGL((k_mmq_r<TG, 1, 16, 3, EPI, XF32>), dim3(a.N / 16), dim3(1024), 0, s, a);
     return launched("mmq");
   }
-  if constexpr (EPI == EPI_SWIGLU_Q8 && !XF32 && TG == 2) {
-    // 17..32 tokens: one 64-row workgroup per Q8_1 output block (280 for gate_up), 4 waves x 12 blocks, every
-    // weight read once (the pipelined kernel's two 16-token groups read each weight twice)
-    if (nb > 4 * 12) return -1;
-    hipLaunchKernelGGL((k_mmq_r<TG, 4, 4, 12, EPI, XF32>), dim3(a.N / 64), dim3(256), 0, s, a);
-    return launched("mmq");
-  }
-  if constexpr (EPI == EPI_RESID_FIX && !XF32 && TG == 2) {
-    // 17..32 tokens, Q8_1 activations: 64-row workgroups of 4 waves over about 256 / (N / 64) K slices
-    int KS = 256 / (a.N / 64);
-    KS = KS < 1 ? 1 : (KS > nb / 4 ? nb / 4 : KS);
-    const int per = (nb + KS - 1) / KS;
-    const dim3 grid(a.N / 64, KS);
-    if (per <= 8) hipLaunchKernelGGL((k_mmq_r<TG, 4, 4, 2, EPI, XF32>), grid, dim3(256), 0, s, a);
-    else if (per <= 16) hipLaunchKernelGGL((k_mmq_r<TG, 4, 4, 4, EPI, XF32>), grid, dim3(256), 0, s, a);
-    else if (per <= 32) hipLaunchKernelGGL((k_mmq_r<TG, 4, 4, 8, EPI, XF32>), grid, dim3(256), 0, s, a);
-    else return -1;
-    return launched("mmq");
-  }
   if constexpr (EPI == EPI_RESID_FIX && XF32) {
     if (a.N % 64) return -1;
     if (nb >= 64) {
@@ -564,12 +545,6 @@ static int launch_mmq_tg(const GemvArgs& a, int KS, hipStream_t s) {
   if constexpr (EPI == EPI_SWIGLU) {
     if (a.T <= 32) {
       const int r = a.T <= 16 ? launch_mmq_r_tg<1, EPI, false>(a, s) : launch_mmq_r_tg<2, EPI, false>(a, s);
-      if (r >= 0) return r;
-    }
-  }
-  if constexpr (EPI == EPI_SWIGLU_Q8 || EPI == EPI_RESID_FIX) {
-    if (a.T > 16 && a.T <= 32) {
-      const int r = launch_mmq_r_tg<2, EPI, false>(a, s);
       if (r >= 0) return r;
     }
   }
