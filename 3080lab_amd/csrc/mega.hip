@@ -10,9 +10,9 @@
 //         RoPE; q and the new k/v rows -> device-coherent scratch; k/v also -> the paged cache (later tokens).
 //         needs all of h (a full barrier after the previous DOWN).
 //   ATTN  task (kv head g, page c, query head) on WG 136 + task; f64 partial (o, max, sum) per (head,
-//         page). Waits for all 128 QKV tiles.
+//         page). Waits for its 24 QKV producers (q of its head, k and v of its group).
 //   O     WG w < 192: tile w % 96, heads 6 (w / 96) .. +5: merge their partials + Q8_1 + dots, add into h
-//         (int64 atomics). Waits only for the ATTN tasks of its group.
+//         (int64 atomics). Waits for every ATTN task.
 //   GU    4-5 gate/up tiles per WG 8..255: RMSNorm of h + Q8_1 + dots + SwiGLU -> m (coherent scratch).
 //         needs all of h (a full barrier after O).
 //   DOWN  3 (tile, 35-block K slice) tasks per WG: Q8_1 of the m slice + dots, add into h. Waits only
@@ -720,16 +720,19 @@ __global__ void __launch_bounds__(MG_NTH) k_mega_decode(const MegaArgs a) {
     Q355_MEGA_MARK(layer, 0);
     sy.publish(s_qkv);
 
-    // ---- attention: task idx on workgroup 128 + idx; its K/V page is loaded before the wait. The wait covers
-    // all 128 QKV workgroups (not only the task's group), so once attention is done nobody reads the residual
-    // of this layer's QKV phase any more and the O phase may add into it ----
+    // ---- attention: task idx on workgroup MG_ATT_WG0 + idx; its K/V page is loaded before it waits for its
+    // q, k and v producers ----
     const unsigned s_attn = ++seq;
     for (int idx = (w - MG_ATT_WG0 + MG_NWG) % MG_NWG; idx < n_attn; idx += MG_NWG) {
       const int g = idx / (MG_ATPG * nch), c = (idx / MG_ATPG) % nch, hq = (idx % MG_ATPG) * MG_AHPT;
       MgAttnRegs AR;
       mg_attn_load(AR, a, Ly, g, c);
       Q355_MEGA_MARK(31, 7);
-      sy.wait(MG_NQKV / 16, [](int i) { return MG_QKV_WG0 + i; }, s_qkv);
+      // its 24 producers: the 8 q tiles of head 6 g + hq and the 8 k and 8 v tiles of group g
+      const int hq0 = (6 * g + hq) * (HD / 16), kt0 = MG_NH * (HD / 16) + g * (HD / 16);
+      sy.wait(3 * (HD / 16), [hq0, kt0](int i) {
+        return MG_QKV_WG0 + (i < 8 ? hq0 + i : (i < 16 ? kt0 + i - 8 : kt0 + MG_NKV * (HD / 16) + i - 16));
+      }, s_qkv);
       Q355_MEGA_MARK(31, 0);
       mg_attn_task(a, Ly, ws, g, c, hq, pos, lds, AR);
     }
@@ -743,7 +746,9 @@ __global__ void __launch_bounds__(MG_NTH) k_mega_decode(const MegaArgs a) {
       MgW<1, 2> W;
       const int tl[1] = {tile}, b0[1] = {24 * sl}, b1[1] = {24 * sl + 24};
       mg_wload(W, Ly.o_qs, Ly.o_d, MG_H / 32, tl, b0, b1);
-      sy.wait(MG_ATPG * nch, [sl, nch](int i) { return attn_wg(sl * MG_ATPG * nch + i); }, s_attn);
+      // every attention task (not only this slice's): once all are done, every QKV workgroup is done (each
+      // produced some task's q, k or v), so nobody reads this layer's QKV-phase residual any more
+      sy.wait(MG_NKV * MG_ATPG * nch, [](int i) { return attn_wg(i); }, s_attn);
       Q355_MEGA_MARK(layer, 2);
       if (nch <= 8) {
         mg_merge6_short(ws.part + (size_t)(6 * sl) * a.max_chunks * (HD + 2), a.max_chunks, nch, ob,
