@@ -102,14 +102,39 @@ __device__ __forceinline__ float quad_sum(float v) {
   v += dpp<DPP_XOR1>(v);
   return v + dpp<DPP_XOR2>(v);
 }
+// v + v(lane ^ 16) and v + v(lane ^ 32) with the gfx950 cross-row lane swaps (v_permlane16_swap /
+// v_permlane32_swap) instead of an LDS permute: each lane adds its own value and its partner's, in either
+// order, which is the same IEEE sum.
+__device__ __forceinline__ float xsum16(float v) {
+  const unsigned u = __float_as_uint(v);
+  const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float xsum32(float v) {
+  const unsigned u = __float_as_uint(v);
+  const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ double xsum16_d(double v) {
+  const int2 x = __builtin_bit_cast(int2, v);
+  const auto lo = __builtin_amdgcn_permlane16_swap(x.x, x.x, false, false);
+  const auto hi = __builtin_amdgcn_permlane16_swap(x.y, x.y, false, false);
+  return __builtin_bit_cast(double, make_int2(lo[0], hi[0])) + __builtin_bit_cast(double, make_int2(lo[1], hi[1]));
+}
+__device__ __forceinline__ double xsum32_d(double v) {
+  const int2 x = __builtin_bit_cast(int2, v);
+  const auto lo = __builtin_amdgcn_permlane32_swap(x.x, x.x, false, false);
+  const auto hi = __builtin_amdgcn_permlane32_swap(x.y, x.y, false, false);
+  return __builtin_bit_cast(double, make_int2(lo[0], hi[0])) + __builtin_bit_cast(double, make_int2(lo[1], hi[1]));
+}
 // Full wave64 sum: 4 DPP steps inside each row of 16, then two cross-row exchanges.
 __device__ __forceinline__ float wave_sum_fast(float v) {
   v += dpp<DPP_XOR1>(v);
   v += dpp<DPP_XOR2>(v);
   v += dpp<DPP_HALF_MIRROR>(v);
   v += dpp<DPP_MIRROR>(v);
-  v += __shfl_xor(v, 16, 64);
-  return v + __shfl_xor(v, 32, 64);
+  v = xsum16(v);
+  return xsum32(v);
 }
 
 // Q8_1 rule of every quantizer in the library (and of the oracle): the reference's QUANT_Q8

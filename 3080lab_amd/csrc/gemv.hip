@@ -567,8 +567,7 @@ __global__ void __launch_bounds__(NW * 64) k_gemv(const GemvArgs a) {
 #pragma unroll
     for (int j = 0; j < T; ++j) {
       double v = acc[t][j];
-      v += __shfl_xor(v, 16, 64);
-      v += __shfl_xor(v, 32, 64);
+      v = xsum32_d(xsum16_d(v));
       if (lane < 16) part[wv][t][j][r] = v;
     }
   __syncthreads();

@@ -269,8 +269,7 @@ __device__ __forceinline__ void mg_dots(const MgW<NT, KPL>& W, const MgX& x, con
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
     double v = acc[t];
-    v += __shfl_xor(v, 16, 64);
-    v += __shfl_xor(v, 32, 64);
+    v = xsum32_d(xsum16_d(v));
     if (lane < 16) part[wv][t][r] = v;
   }
   __syncthreads();
