@@ -127,6 +127,36 @@ __device__ __forceinline__ double xsum32_d(double v) {
   const auto hi = __builtin_amdgcn_permlane32_swap(x.y, x.y, false, false);
   return __builtin_bit_cast(double, make_int2(lo[0], hi[0])) + __builtin_bit_cast(double, make_int2(lo[1], hi[1]));
 }
+// (value, index) argmax over the 64 lanes, larger value first and the lower index on ties (a total order, so
+// the pairing pattern does not matter): DPP steps inside each row of 16, then the two cross-row lane swaps.
+// Every lane ends with the result. All 64 lanes must be active.
+__device__ __forceinline__ void amax_take(float& v, int& i, float ov, int oi) {
+  if (ov > v || (ov == v && oi < i)) { v = ov; i = oi; }
+}
+template <int CTRL>
+__device__ __forceinline__ void amax_dpp(float& v, int& i) {
+  amax_take(v, i, dpp<CTRL>(v), dpp<CTRL>(i));
+}
+__device__ __forceinline__ void wave_argmax(float& v, int& i) {
+  amax_dpp<DPP_XOR1>(v, i);
+  amax_dpp<DPP_XOR2>(v, i);
+  amax_dpp<DPP_HALF_MIRROR>(v, i);
+  amax_dpp<DPP_MIRROR>(v, i);
+  {
+    const unsigned u = __float_as_uint(v);
+    const auto rv = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    const auto ri = __builtin_amdgcn_permlane16_swap(i, i, false, false);
+    const bool lo = (__lane_id() & 16) == 0;                     // own value in slot 0 (rows 0, 2), else 1
+    amax_take(v, i, __uint_as_float(lo ? rv[1] : rv[0]), (int)(lo ? ri[1] : ri[0]));
+  }
+  {
+    const unsigned u = __float_as_uint(v);
+    const auto rv = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    const auto ri = __builtin_amdgcn_permlane32_swap(i, i, false, false);
+    const bool lo = __lane_id() < 32;
+    amax_take(v, i, __uint_as_float(lo ? rv[1] : rv[0]), (int)(lo ? ri[1] : ri[0]));
+  }
+}
 // Full wave64 sum: 4 DPP steps inside each row of 16, then two cross-row exchanges.
 __device__ __forceinline__ float wave_sum_fast(float v) {
   v += dpp<DPP_XOR1>(v);

@@ -306,12 +306,7 @@ __device__ __forceinline__ void epilogue(const GemvArgs& a, A (&part)[NW][NT][T]
           if (a.y) a.y[(size_t)j * N + tile0 * 16 + rr] = x;   // optional fp32 logits
           if (x > v) { v = x; idx = tile0 * 16 + rr; }
         }
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) {
-          const float ov = __shfl_xor(v, o, 64);
-          const int oi = __shfl_xor(idx, o, 64);
-          if (ov > v || (ov == v && oi < idx)) { v = ov; idx = oi; }
-        }
+        wave_argmax(v, idx);
         if (l == 0) {
           a.pmax[(size_t)j * gridDim.x + blockIdx.x] = v;
           a.pidx[(size_t)j * gridDim.x + blockIdx.x] = idx;
@@ -619,12 +614,7 @@ __global__ void __launch_bounds__(256) k_finish(const float* __restrict__ pmax, 
     int i = pidx[(size_t)j * nparts + p];
     if (x > v || (x == v && i < idx)) { v = x; idx = i; }
   }
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    float ov = __shfl_xor(v, o, 64);
-    int oi = __shfl_xor(idx, o, 64);
-    if (ov > v || (ov == v && oi < idx)) { v = ov; idx = oi; }
-  }
+  wave_argmax(v, idx);
   if ((threadIdx.x & 63) == 0) { bv[threadIdx.x >> 6] = v; bi[threadIdx.x >> 6] = idx; }
   __syncthreads();
   if (threadIdx.x == 0) {

@@ -896,12 +896,7 @@ __global__ void __launch_bounds__(MG_NTH) k_mega_decode(const MegaArgs a) {
       if (k + 1 < nck) mg_head_chunk(WB, a, x, hb0, hb1, part_s, rv, t0, t1, k + 1, best, bidx);
     }
     if (threadIdx.x < 64) {
-#pragma unroll
-      for (int o = 32; o > 0; o >>= 1) {
-        const float ov = __shfl_xor(best, o, 64);
-        const int oi = __shfl_xor(bidx, o, 64);
-        if (ov > best || (ov == best && oi < bidx)) { best = ov; bidx = oi; }
-      }
+      wave_argmax(best, bidx);
       if (threadIdx.x == 0) { stc(ws.amax + w, best); stc(ws.aidx + w, bidx); }
     }
   }
@@ -923,12 +918,7 @@ __global__ void __launch_bounds__(MG_NTH) k_mega_decode(const MegaArgs a) {
         const int id = ldc(ws.aidx + i);
         if (v > best || (v == best && id < bidx)) { best = v; bidx = id; }
       }
-#pragma unroll
-      for (int o = 32; o > 0; o >>= 1) {
-        const float ov = __shfl_xor(best, o, 64);
-        const int oi = __shfl_xor(bidx, o, 64);
-        if (ov > best || (ov == best && oi < bidx)) { best = ov; bidx = oi; }
-      }
+      wave_argmax(best, bidx);
       if (threadIdx.x == 0) {
         *a.tok = bidx;
         *a.pos = pos + 1;
