@@ -663,6 +663,10 @@ __global__ void __launch_bounds__(MG_NTH) k_mega_decode(const MegaArgs a) {
   const bool is_qkv = qt >= 0 && qt < MG_NQKV / 16;
   const int qkv_b0[1] = {0}, qkv_b1[1] = {MG_H / 32}, qkv_tl[1] = {is_qkv ? qt : 0};
   if (is_qkv) mg_wload(Wq, a.layers[0].qkv_qs, a.layers[0].qkv_d, MG_H / 32, qkv_tl, qkv_b0, qkv_b1);
+  // O weights (workgroups w < 192: tile w % 96, K slice w / 96), loaded well before the O phase: at the start
+  // of the layer on the gathering workgroups, after the QKV flag, or before the attention task's K/V
+  MgW<1, 2> Wo;
+  const int otl[1] = {w % 96}, ob0[1] = {24 * (w / 96)}, ob1[1] = {24 * (w / 96) + 24};
 
   // the residual stream lives in a.h (int64 fixed point): layer 0's O phase starts it from the embedding row
   // (written here by the owners of its 96 tiles, before their first flag), O sums are added into it, and the
@@ -677,6 +681,7 @@ __global__ void __launch_bounds__(MG_NTH) k_mega_decode(const MegaArgs a) {
     const HSum2 prev{hres, accPrev};
     // ---- QKV ----
     const unsigned s_qkv = ++seq;
+    if (w < MG_QKV_WG0) mg_wload(Wo, Ly.o_qs, Ly.o_d, MG_H / 32, otl, ob0, ob1);
     if (is_qkv) {
       // epilogue operands (bias pair, RoPE angle, page) loaded before the normalisation
       const int r = threadIdx.x & 15, row = qt * 16 + r;
@@ -718,6 +723,7 @@ __global__ void __launch_bounds__(MG_NTH) k_mega_decode(const MegaArgs a) {
     }
     Q355_MEGA_MARK(layer, 0);
     sy.publish(s_qkv);
+    if (is_qkv) mg_wload(Wo, Ly.o_qs, Ly.o_d, MG_H / 32, otl, ob0, ob1);   // (QKV workgroups 8..135 are O ones)
 
     // ---- attention: task idx on workgroup MG_ATT_WG0 + idx; its K/V page is loaded before it waits for its
     // q, k and v producers ----
@@ -725,6 +731,7 @@ __global__ void __launch_bounds__(MG_NTH) k_mega_decode(const MegaArgs a) {
     for (int idx = (w - MG_ATT_WG0 + MG_NWG) % MG_NWG; idx < n_attn; idx += MG_NWG) {
       const int g = idx / (MG_ATPG * nch), c = (idx / MG_ATPG) % nch, hq = (idx % MG_ATPG) * MG_AHPT;
       MgAttnRegs AR;
+      if (w < 192 && idx < MG_NWG - MG_ATT_WG0) mg_wload(Wo, Ly.o_qs, Ly.o_d, MG_H / 32, otl, ob0, ob1);
       mg_attn_load(AR, a, Ly, g, c);
       Q355_MEGA_MARK(31, 7);
       // its 24 producers: the 8 q tiles of head 6 g + hq and the 8 k and 8 v tiles of group g
@@ -735,16 +742,18 @@ __global__ void __launch_bounds__(MG_NTH) k_mega_decode(const MegaArgs a) {
       Q355_MEGA_MARK(31, 0);
       mg_attn_task(a, Ly, ws, g, c, hq, pos, lds, AR);
     }
+    if (w >= MG_ATT_WG0 && w < 192 && w - MG_ATT_WG0 >= n_attn)   // O workgroups without an attention task
+      mg_wload(Wo, Ly.o_qs, Ly.o_d, MG_H / 32, otl, ob0, ob1);
     Q355_MEGA_MARK(layer, 1);
     sy.publish(s_attn);
 
     // ---- O projection (+ merge) into the residual; slice-0 workgroups fold in the previous layer's down sums ----
     const unsigned s_o = ++seq;
     if (w < 192) {
-      const int tile = w % 96, sl = w / 96;
-      MgW<1, 2> W;
-      const int tl[1] = {tile}, b0[1] = {24 * sl}, b1[1] = {24 * sl + 24};
-      mg_wload(W, Ly.o_qs, Ly.o_d, MG_H / 32, tl, b0, b1);
+      const int tile = otl[0], sl = w / 96;
+      const MgW<1, 2>& W = Wo;
+      const int(&b0)[1] = ob0;
+      const int(&b1)[1] = ob1;
       // every attention task (not only this slice's): once all are done, every QKV workgroup is done (each
       // produced some task's q, k or v), so nobody reads this layer's QKV-phase residual any more
       sy.wait(MG_NKV * MG_ATPG * nch, [](int i) { return attn_wg(i); }, s_attn);
