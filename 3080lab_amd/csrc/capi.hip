@@ -191,6 +191,34 @@ extern "C" int q355_qkv_rope_kv(const uint8_t* qs, const void* d, int K, const i
   return launch_gemv<PRO_RMS, EPI_QKV, 1, 4, 3>(a, 1, (hipStream_t)stream);
 }
 
+// Layer 0's QKV product with the embedding in its prologue: h = the tied Q4_0 embedding row of tok[j] (the
+// values q355_embed_q4_0 writes, computed by every workgroup), RMSNorm etc. as q355_qkv_rope_kv; h_out
+// receives the row (the residual stream of the step). One launch (and one graph node) instead of two.
+extern "C" int q355_qkv_rope_kv_embed(const uint8_t* qs, const void* d, int K, const uint8_t* emb_qs,
+                                      const void* emb_d, int V, const int32_t* tok, int64_t* h_out, const float* nw,
+                                      double eps, const float* bias, const float* rope_cos, const float* rope_sin,
+                                      const int32_t* pos, const int32_t* block_table, int bt_stride, int seq_stride,
+                                      void* kcache, void* vcache, void* qout, int nh, int nkv, int T, void* stream) {
+  const int N = (nh + 2 * nkv) * HD;
+  REQUIRE(nh > 0 && nkv > 0 && nh % nkv == 0 && nh / nkv <= 8, "qkv_rope_kv_embed: nh=%d nkv=%d", nh, nkv);
+  if (int e = check_mat("qkv_rope_kv_embed", qs, d, N, K)) return e;
+  if (int e = check_mat("qkv_rope_kv_embed (embedding)", emb_qs, emb_d, V, K)) return e;
+  REQUIRE(K <= 1536, "qkv_rope_kv_embed: K=%d > 1536 (fused RMSNorm prologue)", K);
+  REQUIRE(tok && h_out && nw && bias && rope_cos && rope_sin && pos && block_table && kcache && vcache && qout,
+          "qkv_rope_kv_embed: null pointer");
+  REQUIRE(T >= 1 && T <= 4, "qkv_rope_kv_embed: T=%d outside 1..4", T);
+  REQUIRE(bt_stride > 0 && (seq_stride == 0 || seq_stride == 1), "qkv_rope_kv_embed: bt_stride=%d seq_stride=%d",
+          bt_stride, seq_stride);
+  GemvArgs a = {};
+  a.qs = qs; a.d = (const __half*)d; a.N = N; a.K = K; a.T = T;
+  a.emb_qs = emb_qs; a.emb_d = (const __half*)emb_d; a.emb_v = V; a.tok = tok; a.hout = (long long*)h_out;
+  a.nw = nw; a.eps = eps; a.aux = bias;
+  a.rope_cos = rope_cos; a.rope_sin = rope_sin; a.pos = pos; a.block_table = block_table;
+  a.bt_stride = bt_stride; a.seq_stride = seq_stride;
+  a.kcache = (__half*)kcache; a.vcache = (__half*)vcache; a.qout = (__half*)qout; a.nh = nh; a.nkv = nkv;
+  return launch_gemv<PRO_EMB, EPI_QKV, 1, 4, 3>(a, 1, (hipStream_t)stream);
+}
+
 extern "C" int q355_ffn_gate_up(const uint8_t* qs, const void* d, int N2, int K, const int64_t* h, const float* nw,
                                 double eps, float* m, int T, void* stream) {
   if (int e = check_mat("ffn_gate_up", qs, d, N2, K)) return e;

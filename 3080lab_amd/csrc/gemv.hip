@@ -116,7 +116,7 @@ struct KSlice {
 template <int T, int NW, int PRO>
 struct XLoad {
   static constexpr int NTH = NW * 64;
-  static constexpr bool R = PRO == PRO_RMS, F = PRO == PRO_F32, Q = PRO == PRO_Q8;
+  static constexpr bool R = PRO == PRO_RMS || PRO == PRO_EMB, F = PRO == PRO_F32, Q = PRO == PRO_Q8;
   static constexpr int P8 = (T * 1536 / 8 + NTH - 1) / NTH;   // RMS: 8-value tasks per thread (K <= 1536)
   static constexpr int PF = (T * 2304 / 8 + NTH - 1) / NTH;   // F32: tasks per thread (slice <= 2304 values)
   static constexpr int PT = (T * 288 + NTH - 1) / NTH;        // Q8: 32-blocks per thread (K <= 9216)
@@ -135,9 +135,24 @@ struct XLoad {
       for (int p = 0; p < P8; ++p) {
         const int task = min(threadIdx.x + NTH * p, ntask - 1);
         const int j = task / ng, g = task % ng;
-        const longlong2* hp = (const longlong2*)(a.hfix + (size_t)j * K + 8 * g);
+        if (PRO == PRO_EMB) {
+          // values 8 g .. 8 g + 7 of the embedding row: block g / 4, bytes 8 (g & 1) .. + 7, low nibbles
+          // for the block's first 16 values, high for the rest (k_embed_q4_0's arithmetic)
+          const int t = min(max(a.tok[j], 0), a.emb_v - 1), b = g >> 2;
+          const size_t idx = ((size_t)(t >> 4) * (K / 32) + b) * 16 + (t & 15);
+          const uint2 w = ((const uint2*)a.emb_qs)[idx * 2 + (g & 1)];
+          const double dw = (double)__half2float(a.emb_d[idx]);
+          const int sh = (g & 2) ? 4 : 0;
 #pragma unroll
-        for (int u = 0; u < 4; ++u) { const longlong2 v = hp[u]; hl[p][2 * u] = v.x; hl[p][2 * u + 1] = v.y; }
+          for (int u = 0; u < 8; ++u) {
+            const unsigned byte = ((u < 4 ? w.x : w.y) >> (8 * (u & 3))) & 0xFFu;
+            hl[p][u] = to_fix(dw * (double)((int)((byte >> sh) & 15u) - 8));
+          }
+        } else {
+          const longlong2* hp = (const longlong2*)(a.hfix + (size_t)j * K + 8 * g);
+#pragma unroll
+          for (int u = 0; u < 4; ++u) { const longlong2 v = hp[u]; hl[p][2 * u] = v.x; hl[p][2 * u + 1] = v.y; }
+        }
         const float4* wp = (const float4*)(a.nw + 8 * g);
         xa[p] = wp[0];
         xb[p] = wp[1];
@@ -190,6 +205,17 @@ struct XLoad {
     } else if (R) {
       // RMSNorm in f64: the quantizer input x = h * rsqrt(mean(h^2) + eps) * w matches the f64 oracle
       const int ng = K / 8, ntask = a.T * ng;
+      if (PRO == PRO_EMB && blockIdx.x == 0 && blockIdx.y == 0) {   // the residual stream starts here
+#pragma unroll
+        for (int p = 0; p < P8; ++p) {
+          const int task = threadIdx.x + NTH * p;
+          if (task < ntask) {
+            longlong2* dst = (longlong2*)(a.hout + (size_t)(task / ng) * K + 8 * (task % ng));
+#pragma unroll
+            for (int u = 0; u < 4; ++u) dst[u] = make_longlong2(hl[p][2 * u], hl[p][2 * u + 1]);
+          }
+        }
+      }
       double ss[T];
 #pragma unroll
       for (int j = 0; j < T; ++j) ss[j] = 0.0;

@@ -6,7 +6,7 @@
 
 namespace q355 {
 
-enum Prologue { PRO_Q8 = 0, PRO_RMS = 1, PRO_ATTN = 2, PRO_F32 = 3 };
+enum Prologue { PRO_Q8 = 0, PRO_RMS = 1, PRO_ATTN = 2, PRO_F32 = 3, PRO_EMB = 4 };
 enum Epilogue {
   EPI_STORE = 0,       // y = acc (fp32)
   EPI_RESID = 1,       // y += acc (fp32, one writer per element: no K split)
@@ -49,6 +49,13 @@ struct GemvArgs {
   const long long* hfix;       // [T][K] residual stream, int64 fixed point
   const float* nw;             // [K] RMSNorm weight
   double eps;
+  // PRO_EMB input: as PRO_RMS, with h = the tied Q4_0 embedding row of tok[j] (exact in fixed point, the
+  // values k_embed_q4_0 writes); workgroup (0, 0) also writes that row to hout
+  const uint8_t* emb_qs;
+  const __half* emb_d;
+  const int* tok;
+  int emb_v;
+  long long* hout;
   // PRO_F32 input (quantized to Q8_1 in the prologue)
   const float* xf;             // [T][K]
   // PRO_ATTN input: split-K attention partials [T][nh][attn_max_chunks][HD + 2], merged and quantized

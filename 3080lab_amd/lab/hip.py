@@ -33,6 +33,8 @@ _SIGS = {
     "q355_gemv_blockdots": [_P, c_int, c_int, _P, c_int, _P, _P],
     "q355_qkv_rope_kv": [_P, _P, c_int, _P, _P, c_double, _P, _P, _P, _P, _P, c_int, c_int, _P, _P, _P,
                          c_int, c_int, c_int, _P],
+    "q355_qkv_rope_kv_embed": [_P, _P, c_int, _P, _P, c_int, _P, _P, _P, c_double, _P, _P, _P, _P, _P, c_int,
+                               c_int, _P, _P, _P, c_int, c_int, c_int, _P],
     "q355_ffn_gate_up": [_P, _P, c_int, c_int, _P, _P, c_double, _P, c_int, _P],
     "q355_ffn_down": [_P, _P, c_int, c_int, _P, _P, c_int, _P],
     "q355_head_logits": [_P, _P, c_int, c_int, _P, _P, c_double, _P, _P, _P, c_int, _P],

@@ -258,13 +258,22 @@ class Decoder:
         self.h.copy_(torch.round(t.to(torch.float64) * FIX_SCALE).to(torch.int64))
 
     # -- per-layer ops (each is one library call) --
-    def layer(self, i: int):
+    def layer(self, i: int, embed: bool = False):
+        """Layer i; with embed=True its QKV launch also takes the embedding of tok (q355_qkv_rope_kv_embed:
+        the same h and q/k/v as embed() followed by layer(i), one launch fewer)."""
         m, c, T = self.m, self.cfg, self.T
         L = m.layers[i]
         qkv, o, gu, down = L["qkv"], L["o"], L["gu"], L["down"]
-        call("q355_qkv_rope_kv", ptr(qkv.qs), ptr(qkv.d), c.H, ptr(self.h), ptr(L["ln1"]), c.eps, ptr(L["qkv_b"]),
-             ptr(m.cos), ptr(m.sin), ptr(self.pos), ptr(self.block_table), self.max_chunks, 1,
-             ptr(self.kc[i]), ptr(self.vc[i]), ptr(self.q), c.NH, c.NKV, T)
+        if embed:
+            e = m.embed
+            call("q355_qkv_rope_kv_embed", ptr(qkv.qs), ptr(qkv.d), c.H, ptr(e.qs), ptr(e.d), e.N, ptr(self.tok),
+                 ptr(self.h), ptr(L["ln1"]), c.eps, ptr(L["qkv_b"]), ptr(m.cos), ptr(m.sin), ptr(self.pos),
+                 ptr(self.block_table), self.max_chunks, 1, ptr(self.kc[i]), ptr(self.vc[i]), ptr(self.q), c.NH,
+                 c.NKV, T)
+        else:
+            call("q355_qkv_rope_kv", ptr(qkv.qs), ptr(qkv.d), c.H, ptr(self.h), ptr(L["ln1"]), c.eps,
+                 ptr(L["qkv_b"]), ptr(m.cos), ptr(m.sin), ptr(self.pos), ptr(self.block_table), self.max_chunks, 1,
+                 ptr(self.kc[i]), ptr(self.vc[i]), ptr(self.q), c.NH, c.NKV, T)
         call("q355_attn_decode", ptr(self.q), ptr(self.kc[i]), ptr(self.vc[i]), ptr(self.pos), ptr(self.block_table),
              self.max_chunks, c.NH, c.NKV, self.max_chunks, self.scale, ptr(self.part), None, None, None, T, 0)
         call("q355_attn_o_resid", ptr(o.qs), ptr(o.d), o.N, ptr(self.part), self.max_chunks, ptr(self.pos), c.NH,
@@ -288,10 +297,10 @@ class Decoder:
         call("q355_finish", ptr(self.pmax), ptr(self.pidx), self.nparts, ptr(self.tok), ptr(self.pos), self.T)
 
     def step(self):
-        """One decode step for all T sequences: embed tok at pos, 28 layers, head, tok <- argmax, pos += 1."""
-        self.embed()
+        """One decode step for all T sequences: embed tok at pos (inside layer 0's QKV launch), 28 layers, head,
+        tok <- argmax, pos += 1."""
         for i in range(self.cfg.L):
-            self.layer(i)
+            self.layer(i, embed=(i == 0))
         self.head()
 
     # -- graph capture / replay (scripts/qwen_fused.py:148-180) --

@@ -73,6 +73,17 @@ int q355_qkv_rope_kv(const uint8_t* qs, const void* d, int K, const int64_t* h, 
                      const int32_t* block_table, int bt_stride, int seq_stride, void* kcache, void* vcache,
                      void* qout, int nh, int nkv, int T, void* stream);
 
+/* Layer 0's q355_qkv_rope_kv with q355_embed_q4_0 in its prologue: h = the tied Q4_0 embedding row of
+ * tok[j] (clamped to 0..V-1; q355_embed_q4_0 skips an out-of-range token instead), exact in fixed point,
+ * written to h_out as the step's residual stream. Replaces the EMBED_F32 launch plus the first layer's
+ * RMSNORM_F32W_1P + gemv_source('biasf') + ATTN4 RoPE/KV head (lab/qwen_kernels.py:284-290, 33, 517-546)
+ * with one launch. K <= 1536. */
+int q355_qkv_rope_kv_embed(const uint8_t* qs, const void* d, int K, const uint8_t* emb_qs, const void* emb_d,
+                           int V, const int32_t* tok, int64_t* h_out, const float* nw, double eps,
+                           const float* bias, const float* rope_cos, const float* rope_sin, const int32_t* pos,
+                           const int32_t* block_table, int bt_stride, int seq_stride, void* kcache, void* vcache,
+                           void* qout, int nh, int nkv, int T, void* stream);
+
 /* Fused ln2 RMSNorm + Q8_1 + gate_up GEMV (rows interleaved gate, up) + SwiGLU: m fp32 [T][N2/2].
  * Replaces gemv_source('swiglu') (lab/qwen_kernels.py:21-28). K <= 1536. */
 int q355_ffn_gate_up(const uint8_t* qs, const void* d, int N2, int K, const int64_t* h, const float* nw, double eps,

@@ -307,6 +307,28 @@ def test_embed_head(one_layer):
     assert dec.tok.cpu().numpy().tolist() == [int(np.argmax(r)) for r in dec.logits.cpu().numpy()]
 
 
+def test_qkv_with_embedding_equals_embed_then_qkv(one_layer):
+    """q355_qkv_rope_kv_embed (layer 0's QKV with the embedding in its prologue) gives bit-equal h, q and K/V
+    cache rows to q355_embed_q4_0 followed by q355_qkv_rope_kv, at T = 1 and 3."""
+    import torch
+    w, dm, om = one_layer
+    for T in (1, 3):
+        a = QM.Decoder(dm, T=T, max_ctx=128)
+        b = QM.Decoder(dm, T=T, max_ctx=128)
+        toks = np.array([3, 1000, 1023][:T], np.int32)
+        for d in (a, b):
+            d.tok.copy_(to_dev(toks))
+            d.pos.copy_(to_dev(np.array([5, 70, 127][:T], np.int32)))
+            d.h.fill_(12345)                      # stale residual: both paths must overwrite it
+        a.embed()
+        a.layer(0)
+        b.layer(0, embed=True)
+        sync()
+        assert torch.equal(a.q, b.q)
+        assert torch.equal(a.kc[0], b.kc[0]) and torch.equal(a.vc[0], b.vc[0])
+        assert torch.equal(a.h, b.h)
+
+
 # --------------------------------------------------------------------------------------------------
 # BASELINE config 1: one decoder layer, decode at batch 1 with 512 past positions of N(0,1) fp16 KV
 
