@@ -34,9 +34,11 @@ def one_live_block_problem(N, K, T, seed):
     dx = (2.0 ** -rng.integers(2, 9, (T, nb))).astype(np.float16)
     # expected block values S = dot - 8 sum(q_x) of each row's live block, and y = d_w d_x S (exact)
     qw = OQ.q4_0_blocks(wb)[1].reshape(N, K)
-    dots = OQ.block_dots(qw, xq).astype(np.int64)                         # [T, N, nb]
     sq = xq.reshape(T, nb, 32).astype(np.int64).sum(axis=2)             # [T, nb]
-    S = dots[:, np.arange(N), live] - 8 * sq[:, live]                    # [T, N]
+    S = np.empty((T, N), np.int64)
+    for b in np.unique(live):                                           # the live blocks' dots only
+        rows = np.nonzero(live == b)[0]
+        S[:, rows] = OQ.block_dots(qw[rows, 32 * b:32 * b + 32], xq[:, 32 * b:32 * b + 32])[:, :, 0] - 8 * sq[:, b:b + 1]
     y = (dw[np.arange(N), live].astype(np.float64)[None] * dx[:, live].astype(np.float64) * S)
     assert np.array_equal(y.astype(np.float32).astype(np.float64), y)   # exact in fp32 by construction
     return wb, xq, dx, S, y.astype(np.float32), dw[np.arange(N), live], live
