@@ -227,7 +227,10 @@ __global__ void __launch_bounds__(4 * PAGE / KW * 64) k_attn_decode_mfma(const A
   const int li = lane & 15, lg = lane >> 4;
   const int G = a.nh / a.nkv;
   const int nsp = (a.max_chunks + 3) / 4;
-  const int j = blockIdx.y, kvh = blockIdx.x / nsp, sp = blockIdx.x % nsp;
+  // split-major order over the grid (nkv * nsp, T): all first splits are dispatched first, so the live
+  // workgroups start early and the splits past short contexts (which return at once) come last
+  const int wid = blockIdx.x + gridDim.x * blockIdx.y, per = gridDim.y * a.nkv;
+  const int sp = wid / per, j = (wid % per) / a.nkv, kvh = wid % a.nkv;
   const int c = sp * 4 + wv / (PAGE / KW), k0 = (wv % (PAGE / KW)) * KW;   // page, first key in it
   // the page index does not depend on the position: both loads are in flight together
   const int pg = a.block_table[(size_t)j * a.bt_stride + min(c, a.max_chunks - 1)];
