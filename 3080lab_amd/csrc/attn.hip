@@ -85,8 +85,8 @@ __global__ void __launch_bounds__(G / HS * W * 64) k_attn_decode(const AttnArgs 
 #pragma unroll
   for (int i = 0; i < PER; ++i) {
     const int e = min((int)threadIdx.x + NT * i, PAGE * HD / 8 - 1);   // clamped: loads stay unconditional
-    kr[i] = kp[e];
-    vr[i] = vp[e];
+    kr[i] = ld_stream16(kp + e);
+    vr[i] = ld_stream16(vp + e);
   }
   if (part == 0) {
     const half2 qv = ((const half2*)(a.q + ((size_t)j * a.nh + hq) * HD))[lane];
@@ -253,12 +253,12 @@ __global__ void __launch_bounds__(4 * PAGE / KW * 64) k_attn_decode_mfma(const A
 #pragma unroll
     for (int t = 0; t < KW / 16; ++t)
 #pragma unroll
-      for (int cc = 0; cc < 4; ++cc) kA[t][cc] = *(const uint4*)(kp + (16 * t + li) * HD + 32 * cc + 8 * lg);
+      for (int cc = 0; cc < 4; ++cc) kA[t][cc] = ld_stream16(kp + (16 * t + li) * HD + 32 * cc + 8 * lg);
     unsigned vr[KW / 8][8];
 #pragma unroll
     for (int kg = 0; kg < KW / 8; ++kg)
 #pragma unroll
-      for (int u = 0; u < 8; ++u) vr[kg][u] = vp[(kg * 8 + u) * (HD / 2) + lane];
+      for (int u = 0; u < 8; ++u) vr[kg][u] = ld_stream4(vp + (kg * 8 + u) * (HD / 2) + lane);
     ah8 qB[4];
 #pragma unroll
     for (int cc = 0; cc < 4; ++cc) {

@@ -32,6 +32,15 @@ __device__ __forceinline__ uint4 ld_stream16(const void* p) {
   return make_uint4(v.x, v.y, v.z, v.w);
 }
 
+__device__ __forceinline__ uint2 ld_stream8(const void* p) {
+  typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+  u32x2 v = __builtin_nontemporal_load((const u32x2*)p);
+  return make_uint2(v.x, v.y);
+}
+
+__device__ __forceinline__ unsigned ld_stream4(const void* p) { return __builtin_nontemporal_load((const unsigned*)p); }
+__device__ __forceinline__ unsigned ld_stream2(const void* p) { return __builtin_nontemporal_load((const unsigned short*)p); }
+
 __device__ __forceinline__ int dot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
 
 // Exact int32 dot of one Q4_0 block (16 B of GGUF qs, unsigned nibbles 0..15) with 32 int8 values.

@@ -79,7 +79,7 @@ __global__ void __launch_bounds__(NW * 64) k_gemm_f16(const GemvArgs a) {
     {                                                                                              \
       const int b_ = c0 + min((bb), nbc - 1);                                                      \
       _Pragma("unroll") for (int t = 0; t < NT; ++t) {                                             \
-        w[t] = wq[t][b_ * 32];                                                                     \
+        w[t] = ld_stream8(wq[t] + b_ * 32);                                                        \
         dv[t] = wd[t][b_ * 16];                                                                    \
       }                                                                                            \
     }
@@ -168,7 +168,7 @@ __global__ void __launch_bounds__(NW * 64) k_gemm_f16r(const GemvArgs a) {
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
       const size_t base = ((size_t)(tile0 + t) * nb + b) * 16 + li;
-      w[i][t] = ((const uint2*)a.qs)[base * 2 + (lg & 1)];
+      w[i][t] = ld_stream8((const uint2*)a.qs + base * 2 + (lg & 1));
       dsc[i][t] = a.d[base];
     }
 #pragma unroll
@@ -231,7 +231,7 @@ __global__ void __launch_bounds__(256) k_gemm_f16_attn_o(const GemvArgs a) {
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
     const size_t base = ((size_t)(tile0 + t) * nb + b) * 16 + li;
-    w[t] = ((const uint2*)a.qs)[base * 2 + (lg & 1)];
+    w[t] = ld_stream8((const uint2*)a.qs + base * 2 + (lg & 1));
     dsc[t] = a.d[base];
   }
   {

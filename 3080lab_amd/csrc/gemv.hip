@@ -531,11 +531,11 @@ __global__ void __launch_bounds__(NW * 64) k_gemv(const GemvArgs a) {
       const size_t idx = ((size_t)(tile0 + t) * nb + bc) * 16 + r;
       w[t][i] = ld_stream16(qs + idx);
       if constexpr (Q6) {
-        hq[t][i] = ((const uint2*)a.qhi)[idx];
-        sc6[t][i] = ((const unsigned short*)a.qsc)[idx];
+        hq[t][i] = ld_stream8((const uint2*)a.qhi + idx);
+        sc6[t][i] = ld_stream2((const unsigned short*)a.qsc + idx);
         dh[t][i] = dd[((size_t)(tile0 + t) * (nb / 8) + bc / 8) * 16 + r];
       } else {
-        dh[t][i] = dd[idx];
+        dh[t][i] = ld_stream2(dd + idx);
       }
     }
   }

@@ -219,7 +219,7 @@ __device__ __forceinline__ void mg_wload(MgW<NT, KPL>& W, const uint8_t* qs8, co
       const int b = min(b0[t] + kl + 16 * i, b1[t] - 1);
       const size_t idx = ((size_t)tile[t] * nb + b) * 16 + r;
       W.w[t][i] = ld_stream16(qs + idx);
-      W.dh[t][i] = dd[idx];
+      W.dh[t][i] = ld_stream2(dd + idx);
     }
   __asm__ __volatile__("" ::: "memory");
 #pragma unroll

@@ -210,7 +210,7 @@ __global__ void __launch_bounds__(NW * 64) k_mmq_r(const GemvArgs a) {
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
       const size_t base = ((size_t)(tile0 + t) * nb + b) * 16;
-      w[i][t] = ((const uint2*)a.qs)[(base + li) * 2 + (lg & 1)];
+      w[i][t] = ld_stream8((const uint2*)a.qs + (base + li) * 2 + (lg & 1));
     }
 #pragma unroll
     for (int q = 0; q < NQ; ++q) {
@@ -336,7 +336,7 @@ __global__ void __launch_bounds__(NW * 64) k_mmq(const GemvArgs a) {
     auto load_blk = [&](int bb, uint2 (&w)[NT], float (&dv)[NQ]) {
       const int b = c0 + min(bb, nbc - 1);
 #pragma unroll
-      for (int t = 0; t < NT; ++t) w[t] = wq[t][b * 32];
+      for (int t = 0; t < NT; ++t) w[t] = ld_stream8(wq[t] + b * 32);
 #pragma unroll
       for (int q = 0; q < NQ; ++q) dv[q] = 4 * q + lg < NT ? __half2float(wd[q][b * 16]) : 0.f;
     };
@@ -417,7 +417,7 @@ __global__ void __launch_bounds__(NW * 64) k_mmq_reg(const GemvArgs a) {
   for (int i = 0; i < KPW; ++i) {
     const int b = ks.b0 + min(wv + NW * i, nbs - 1);
 #pragma unroll
-    for (int t = 0; t < NT; ++t) w[i][t] = qs[(((size_t)(tile0 + t) * nb + b) * 16 + li) * 2 + (lg & 1)];
+    for (int t = 0; t < NT; ++t) w[i][t] = ld_stream8(qs + (((size_t)(tile0 + t) * nb + b) * 16 + li) * 2 + (lg & 1));
   }
   __asm__ __volatile__("" ::: "memory");
   // scales of the slice -> LDS (zero for blocks past the slice is not needed: those blocks are skipped)
