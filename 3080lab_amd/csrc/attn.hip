@@ -67,15 +67,18 @@ __global__ void __launch_bounds__(G / HS * W * 64) k_attn_decode(const AttnArgs 
   __shared__ F xm[GH][W], xl[GH][W];
   __shared__ __align__(16) F xo[W > 1 ? GH : 1][W > 1 ? W - 1 : 1][HD];
 
+  // grid.x = (query-head groups) x CH chunk slots, CH = max_chunks rounded up to a multiple of 8: workgroup
+  // x runs on XCD x mod 8 = c mod 8, so the G / HS workgroups that stage the same K/V page share one L2
   const int j = blockIdx.y;
-  const int c = blockIdx.x % a.max_chunks, r = blockIdx.x / a.max_chunks;
+  const int CH = (a.max_chunks + 7) & ~7;
+  const int c = blockIdx.x % CH, r = blockIdx.x / CH;
   const int kvh = r / HS, hs = r % HS;
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int hh = wv / W, part = wv % W;
   const int pos = a.pos[j];
+  if (c >= a.max_chunks || c * PAGE > pos) return;  // chunk slot beyond the table or the context: nothing to do
   const int pg = a.block_table[(size_t)j * a.bt_stride + c];
   const int hq = kvh * G + hs * GH + hh;
-  if (c * PAGE > pos) return;                       // chunk beyond the context: nothing to do
   const int nvalid = min(PAGE, pos + 1 - c * PAGE);
 
   const uint4* kp = (const uint4*)(a.kcache + ((size_t)pg * a.nkv + kvh) * PAGE * HD);

@@ -336,7 +336,7 @@ extern "C" int q355_attn_decode(const void* q, const void* kcache, const void* v
   } else {
     // one query head per workgroup, 16 waves of 4 positions each (short serial f64 chains per lane); the
     // workgroups of a KV head's group each stage its K/V page (from L2 after the first)
-    const dim3 grid(nh * max_chunks, T);
+    const dim3 grid(nh * ((max_chunks + 7) & ~7), T);   // chunk slots padded to 8: one XCD per page
     switch (nh / nkv) {
       case 4: hipLaunchKernelGGL((k_attn_decode<4, double, 16, 4>), grid, dim3(1024), 0, s, a); break;
       case 6: hipLaunchKernelGGL((k_attn_decode<6, double, 16, 6>), grid, dim3(1024), 0, s, a); break;

@@ -650,7 +650,11 @@ __global__ void __launch_bounds__(MG_NTH) k_mega_decode(const MegaArgs a) {
     return;
   }
   const int nch = pos / PAGE + 1;
-  const int n_attn = MG_NKV * nch * MG_ATPG;
+  // attention slots: slot = hq * P8 + (page pc = g * nch + c), P8 = the page count rounded up to 8, so the tasks
+  // that stage one K/V page run on workgroups 136 + slot of one XCD (x mod 8) and share its L2
+  const int P8 = (MG_NKV * nch + 7) & ~7;
+  const int n_slot = MG_ATPG * P8;
+  const int n_attn_wg = n_slot < MG_NWG ? n_slot : MG_NWG;
   MgX x;
   x.q = (int8_t*)lds;                                  // K blocks of the widest operand (down: 280)
   x.d = (float*)(lds + MG_FFN);
@@ -728,10 +732,12 @@ __global__ void __launch_bounds__(MG_NTH) k_mega_decode(const MegaArgs a) {
     // ---- attention: task idx on workgroup MG_ATT_WG0 + idx; its K/V page is loaded before it waits for its
     // q, k and v producers ----
     const unsigned s_attn = ++seq;
-    for (int idx = (w - MG_ATT_WG0 + MG_NWG) % MG_NWG; idx < n_attn; idx += MG_NWG) {
-      const int g = idx / (MG_ATPG * nch), c = (idx / MG_ATPG) % nch, hq = (idx % MG_ATPG) * MG_AHPT;
-      MgAttnRegs AR;
+    for (int idx = (w - MG_ATT_WG0 + MG_NWG) % MG_NWG; idx < n_slot; idx += MG_NWG) {
       if (w < 192 && idx < MG_NWG - MG_ATT_WG0) mg_wload(Wo, Ly.o_qs, Ly.o_d, MG_H / 32, otl, ob0, ob1);
+      const int pc = idx % P8, hq = (idx / P8) * MG_AHPT;
+      if (pc >= MG_NKV * nch) continue;              // padding slot (uniform per workgroup)
+      const int g = pc / nch, c = pc % nch;
+      MgAttnRegs AR;
       mg_attn_load(AR, a, Ly, g, c);
       Q355_MEGA_MARK(31, 7);
       // its 24 producers: the 8 q tiles of head 6 g + hq and the 8 k and 8 v tiles of group g
@@ -742,7 +748,7 @@ __global__ void __launch_bounds__(MG_NTH) k_mega_decode(const MegaArgs a) {
       Q355_MEGA_MARK(31, 0);
       mg_attn_task(a, Ly, ws, g, c, hq, pos, lds, AR);
     }
-    if (w >= MG_ATT_WG0 && w < 192 && w - MG_ATT_WG0 >= n_attn)   // O workgroups without an attention task
+    if (w >= MG_ATT_WG0 && w < 192 && w - MG_ATT_WG0 >= n_slot)   // O workgroups without an attention slot
       mg_wload(Wo, Ly.o_qs, Ly.o_d, MG_H / 32, otl, ob0, ob1);
     Q355_MEGA_MARK(layer, 1);
     sy.publish(s_attn);
@@ -756,7 +762,7 @@ __global__ void __launch_bounds__(MG_NTH) k_mega_decode(const MegaArgs a) {
       const int(&b1)[1] = ob1;
       // every attention task (not only this slice's): once all are done, every QKV workgroup is done (each
       // produced some task's q, k or v), so nobody reads this layer's QKV-phase residual any more
-      sy.wait(MG_NKV * MG_ATPG * nch, [](int i) { return attn_wg(i); }, s_attn);
+      sy.wait(n_attn_wg, [](int i) { return attn_wg(i); }, s_attn);
       Q355_MEGA_MARK(layer, 2);
       if (nch <= 8) {
         mg_merge6_short(ws.part + (size_t)(6 * sl) * a.max_chunks * (HD + 2), a.max_chunks, nch, ob,
