@@ -234,12 +234,14 @@ def test_ffn_gate_up_down(one_layer):
 
 
 @pytest.mark.parametrize("fp32", [0, 1])
-@pytest.mark.parametrize("positions", [[0, 63], [64, 511], [1000, 5]])
-def test_attn_decode(cuda, positions, fp32):
+@pytest.mark.parametrize("positions,max_chunks", [([0, 63], 16), ([64, 511], 16), ([1000, 5], 16),
+                                                  # chunk counts that are not a multiple of 8: the batch-1
+                                                  # grid pads its chunk slots to 8, the padding must exit
+                                                  ([319, 200, 0], 5), ([831, 64], 13)])
+def test_attn_decode(cuda, positions, max_chunks, fp32):
     import torch
     c = CFG1
     T = len(positions)
-    max_chunks = 16
     rng = np.random.default_rng(sum(positions))
     n_pages = T * max_chunks
     kc = rng.standard_normal((n_pages, c.NKV, 64, c.HD)).astype(np.float16)
