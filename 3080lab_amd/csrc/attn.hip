@@ -56,7 +56,7 @@ __device__ __forceinline__ float exp_t(float v) { return expf(v); }
 // with W > 1 the waves of a head exchange their maximum and sum through LDS, so their P.V parts
 // (lane l: dims 2l, 2l+1) share the page maximum and add, in wave order, into one partial (o[128], m, l) per
 // (head, page). HS workgroups share a page, each taking G / HS heads of the group (its K/V page staged by
-// each). More waves per head shorten the serial f64 chains of each lane (the batch-1 latency).
+// each). The library launches W = 4, HS = G.
 template <int G, typename F, int W, int HS>
 __global__ void __launch_bounds__(G / HS * W * 64) k_attn_decode(const AttnArgs a) {
   static_assert(G % HS == 0 && (W == 1 || W == 2 || W == 4 || W == 8 || W == 16), "k_attn_decode: head split / wave count");

@@ -334,13 +334,14 @@ extern "C" int q355_attn_decode(const void* q, const void* kcache, const void* v
     hipLaunchKernelGGL(k_attn_merge_split, dim3(nkv, T), dim3(256), 0, s, a);
     return launched("attn_merge_split");
   } else {
-    // one query head per workgroup, 16 waves of 4 positions each (short serial f64 chains per lane); the
-    // workgroups of a KV head's group each stage its K/V page (from L2 after the first)
+    // one query head per workgroup, 4 waves of 16 positions each; the workgroups of a KV head's group each
+    // stage its K/V page (from L2 after the first). Measured at position 256 (graph of 28 launches): 4 waves
+    // 4.16 us, 8 waves 4.18, 16 waves 4.64, 2 waves 4.95
     const dim3 grid(nh * ((max_chunks + 7) & ~7), T);   // chunk slots padded to 8: one XCD per page
     switch (nh / nkv) {
-      case 4: hipLaunchKernelGGL((k_attn_decode<4, double, 16, 4>), grid, dim3(1024), 0, s, a); break;
-      case 6: hipLaunchKernelGGL((k_attn_decode<6, double, 16, 6>), grid, dim3(1024), 0, s, a); break;
-      default: hipLaunchKernelGGL((k_attn_decode<8, double, 16, 8>), grid, dim3(1024), 0, s, a); break;
+      case 4: hipLaunchKernelGGL((k_attn_decode<4, double, 4, 4>), grid, dim3(256), 0, s, a); break;
+      case 6: hipLaunchKernelGGL((k_attn_decode<6, double, 4, 6>), grid, dim3(256), 0, s, a); break;
+      default: hipLaunchKernelGGL((k_attn_decode<8, double, 4, 8>), grid, dim3(256), 0, s, a); break;
     }
   }
   if (int e = launched("attn_decode")) return e;
