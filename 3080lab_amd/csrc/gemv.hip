@@ -113,12 +113,12 @@ struct KSlice {
 
 // Activation operand, stage 1 (loads into registers) and stage 2 (quantize / copy into LDS).
 // RMS / F32 / ATTN: a task is 8 consecutive values of one token (4 lanes = one Q8_1 block).
-template <int T, int NW, int PRO>
+template <int T, int NW, int PRO, int KPL>
 struct XLoad {
   static constexpr int NTH = NW * 64;
   static constexpr bool R = PRO == PRO_RMS || PRO == PRO_EMB, F = PRO == PRO_F32, Q = PRO == PRO_Q8;
   static constexpr int P8 = (T * 1536 / 8 + NTH - 1) / NTH;   // RMS: 8-value tasks per thread (K <= 1536)
-  static constexpr int PF = (T * 2304 / 8 + NTH - 1) / NTH;   // F32: tasks per thread (slice <= 2304 values)
+  static constexpr int PF = (T * 16 * NW * KPL + NTH - 1) / NTH;   // F32: tasks per thread (slice <= 4 NW KPL blocks)
   static constexpr int PT = (T * 288 + NTH - 1) / NTH;        // Q8: 32-blocks per thread (K <= 9216)
   static constexpr int NX = R ? P8 : (F ? PF : 1);
   long long hl[R ? P8 : 1][8];
@@ -510,7 +510,7 @@ __global__ void __launch_bounds__(NW * 64) k_gemv(const GemvArgs a) {
   const int r = lane & 15, kl = wv * 4 + (lane >> 4);
   const int tile0 = blockIdx.x * NT;
 
-  XLoad<T, NW, PRO> xl;
+  XLoad<T, NW, PRO, KPL> xl;
   xl.load(a, ks);
 
   const uint4* __restrict__ qs = (const uint4*)a.qs;
