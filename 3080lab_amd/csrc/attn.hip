@@ -251,7 +251,11 @@ __global__ void __launch_bounds__(4 * PAGE / KW * 64) k_attn_decode_mfma(const A
   for (int dt = 0; dt < 8; ++dt) acc[dt] = af4{0.f, 0.f, 0.f, 0.f};
   float ml2 = -INFINITY, rs = 0.f;
   if (live) {
-    // every load first: K operands (16 B per lane per 16-key tile), V dwords, q
+    // every load first, in the order of use: q, K operands (16 B per lane per 16-key tile), V dwords; the
+    // wait for q and K (in-order counter) then leaves the V loads in flight during the scores and softmax
+    uint4 qr[4];                                        // unconditional (clamped head): straight-line loads
+#pragma unroll
+    for (int cc = 0; cc < 4; ++cc) qr[cc] = *(const uint4*)(a.q + ((size_t)j * a.nh + kvh * G + min(li, G - 1)) * HD + 32 * cc + 8 * lg);
     uint4 kA[KW / 16][4];
 #pragma unroll
     for (int t = 0; t < KW / 16; ++t)
@@ -262,12 +266,12 @@ __global__ void __launch_bounds__(4 * PAGE / KW * 64) k_attn_decode_mfma(const A
     for (int kg = 0; kg < KW / 8; ++kg)
 #pragma unroll
       for (int u = 0; u < 8; ++u) vr[kg][u] = ld_stream4(vp + (kg * 8 + u) * (HD / 2) + lane);
+    __asm__ __volatile__("" ::: "memory");              // keep every load above issued before the first product
     ah8 qB[4];
 #pragma unroll
     for (int cc = 0; cc < 4; ++cc) {
-      uint4 q = make_uint4(0, 0, 0, 0);
-      if (li < G) q = *(const uint4*)(a.q + ((size_t)j * a.nh + hq) * HD + 32 * cc + 8 * lg);
-      qB[cc] = *reinterpret_cast<ah8*>(&q);
+      const uint4 q = li < G ? qr[cc] : make_uint4(0, 0, 0, 0);
+      qB[cc] = *reinterpret_cast<const ah8*>(&q);
     }
 
     // S^T: keys 16t + 4lg + v (rows), head li (column)
