@@ -89,7 +89,7 @@ int q355_qkv_rope_kv_embed(const uint8_t* qs, const void* d, int K, const uint8_
 int q355_ffn_gate_up(const uint8_t* qs, const void* d, int N2, int K, const int64_t* h, const float* nw, double eps,
                      float* m, int T, void* stream);
 
-/* Fused Q8_1 of m + down GEMV + residual: h[T][N] += Wd . Q8_1(m) (4 K slices, fixed-point atomics).
+/* Fused Q8_1 of m + down GEMV + residual: h[T][N] += Wd . Q8_1(m) (2 K slices, fixed-point atomics).
  * Replaces swiglu_q8's quantizer (lab/qwen_batched.py:1363-1396) + gemv_source('resid') for down (:34).
  * K % 128 == 0, K <= 9216. */
 int q355_ffn_down(const uint8_t* qs, const void* d, int N, int K, const float* m, int64_t* h, int T, void* stream);
