@@ -635,10 +635,19 @@ __global__ void __launch_bounds__(256) k_finish(const float* __restrict__ pmax, 
   const int j = blockIdx.x;
   float v = -INFINITY;
   int idx = 0x7fffffff;
-  for (int p = threadIdx.x; p < nparts; p += blockDim.x) {
-    float x = pmax[(size_t)j * nparts + p];
-    int i = pidx[(size_t)j * nparts + p];
-    if (x > v || (x == v && i < idx)) { v = x; idx = i; }
+  // 8 partials per thread per round, all loaded before the first comparison (one memory latency per round)
+  for (int p0 = 0; p0 < nparts; p0 += 8 * blockDim.x) {
+    float x[8];
+    int ix[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int p = p0 + threadIdx.x + u * blockDim.x;
+      x[u] = p < nparts ? pmax[(size_t)j * nparts + p] : -INFINITY;
+      ix[u] = p < nparts ? pidx[(size_t)j * nparts + p] : 0x7fffffff;
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      if (x[u] > v || (x[u] == v && ix[u] < idx)) { v = x[u]; idx = ix[u]; }
   }
   wave_argmax(v, idx);
   if ((threadIdx.x & 63) == 0) { bv[threadIdx.x >> 6] = v; bi[threadIdx.x >> 6] = idx; }
