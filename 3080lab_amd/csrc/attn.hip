@@ -492,4 +492,298 @@ __global__ void __launch_bounds__(64) k_attn_merge(const AttnArgs a) {
   }
 }
 
+// ---------------------------------------------------------------------------------------------
+// f64 batched decode attention (the int8 batched path): the arithmetic of the batch-1 kernel above -- f64
+// scores, softmax and P.V from fp16 q/K/V widened exactly -- at the throughput of a batch. Workgroup
+// (token j, KV head, split sp) = SPG pages c = SPG sp + pg, all G query heads of the group, 4 waves per page:
+// wave (pg, dq) owns dims 32 dq .. 32 dq + 31 of page pg, so each wave's dependency chain is a quarter of
+// a page's work and a batch launches four waves per page (the latency of one wave is hidden by the others).
+//  1. scores: lane = key; its 32 K values widened once, then per head 32 FMAs whose q operands are the f64
+//     queries (q64, written by the QKV epilogue), replicated in every 16-lane row and read as row-broadcast
+//     DPP operands of v_fmac_f64; partials -> LDS;
+//  2. softmax: wave h sums the 4 quarters in order, max / exp / sum over the split's keys (f64 exp);
+//  3. P.V: lane (dim pair 32 dq + 2 (l % 16), keys 4 t + l / 16 of page pg); the p of the row's 16 keys sit
+//     one per lane and reach the FMAs as row-broadcast DPP operands; the 4 key groups add through lane
+//     swaps and the pages of the split in page order.
+// A token whose context fits one split is finished here (Q8_1 oq/ods, fp32 o32 if asked); otherwise each
+// split writes its unnormalised (o[G][HD], M[G], L[G]) to part [T][nkv][nsp][G][HD + 2] (nsp =
+// ceil(max_chunks / SPG)) and k_attn_merge_f64 finishes the token in split order.
+// acc += bcast(q, lane i of each 16-lane row) * k_i for i = 0..15: v_fmac_f64 with a DPP row_newbcast source
+// (gfx950's 64-bit DPP), so a row-uniform f64 operand costs no broadcast instruction. s_nop 1: the two wait
+// states a DPP source needs after a VALU write of it.
+__device__ __forceinline__ void fma16_bcast(double& acc, double q, const double (&k)[16]) {
+  asm("s_nop 1\n\t"
+      "v_fmac_f64_dpp %0, %1, %2 row_newbcast:0 row_mask:0xf bank_mask:0xf\n\t"
+      "v_fmac_f64_dpp %0, %1, %3 row_newbcast:1 row_mask:0xf bank_mask:0xf\n\t"
+      "v_fmac_f64_dpp %0, %1, %4 row_newbcast:2 row_mask:0xf bank_mask:0xf\n\t"
+      "v_fmac_f64_dpp %0, %1, %5 row_newbcast:3 row_mask:0xf bank_mask:0xf\n\t"
+      "v_fmac_f64_dpp %0, %1, %6 row_newbcast:4 row_mask:0xf bank_mask:0xf\n\t"
+      "v_fmac_f64_dpp %0, %1, %7 row_newbcast:5 row_mask:0xf bank_mask:0xf\n\t"
+      "v_fmac_f64_dpp %0, %1, %8 row_newbcast:6 row_mask:0xf bank_mask:0xf\n\t"
+      "v_fmac_f64_dpp %0, %1, %9 row_newbcast:7 row_mask:0xf bank_mask:0xf\n\t"
+      "v_fmac_f64_dpp %0, %1, %10 row_newbcast:8 row_mask:0xf bank_mask:0xf\n\t"
+      "v_fmac_f64_dpp %0, %1, %11 row_newbcast:9 row_mask:0xf bank_mask:0xf\n\t"
+      "v_fmac_f64_dpp %0, %1, %12 row_newbcast:10 row_mask:0xf bank_mask:0xf\n\t"
+      "v_fmac_f64_dpp %0, %1, %13 row_newbcast:11 row_mask:0xf bank_mask:0xf\n\t"
+      "v_fmac_f64_dpp %0, %1, %14 row_newbcast:12 row_mask:0xf bank_mask:0xf\n\t"
+      "v_fmac_f64_dpp %0, %1, %15 row_newbcast:13 row_mask:0xf bank_mask:0xf\n\t"
+      "v_fmac_f64_dpp %0, %1, %16 row_newbcast:14 row_mask:0xf bank_mask:0xf\n\t"
+      "v_fmac_f64_dpp %0, %1, %17 row_newbcast:15 row_mask:0xf bank_mask:0xf"
+      : "+v"(acc)
+      : "v"(q), "v"(k[0]), "v"(k[1]), "v"(k[2]), "v"(k[3]), "v"(k[4]), "v"(k[5]), "v"(k[6]), "v"(k[7]), "v"(k[8]),
+        "v"(k[9]), "v"(k[10]), "v"(k[11]), "v"(k[12]), "v"(k[13]), "v"(k[14]), "v"(k[15]));
+}
+// o[h][u], o[h + 1][u] += bcast(p[h], p[h + 1]: lane T of each row) * v_u (two heads of one P.V key)
+template <int T>
+__device__ __forceinline__ void fma_pv2(double& o00, double& o01, double& o10, double& o11, double p0, double p1,
+                                        double v0, double v1) {
+  asm("s_nop 1\n\t"
+      "v_fmac_f64_dpp %0, %4, %6 row_newbcast:%8 row_mask:0xf bank_mask:0xf\n\t"
+      "v_fmac_f64_dpp %1, %4, %7 row_newbcast:%8 row_mask:0xf bank_mask:0xf\n\t"
+      "v_fmac_f64_dpp %2, %5, %6 row_newbcast:%8 row_mask:0xf bank_mask:0xf\n\t"
+      "v_fmac_f64_dpp %3, %5, %7 row_newbcast:%8 row_mask:0xf bank_mask:0xf"
+      : "+v"(o00), "+v"(o01), "+v"(o10), "+v"(o11)
+      : "v"(p0), "v"(p1), "v"(v0), "v"(v1), "n"(T));
+}
+template <int T, int G>
+__device__ __forceinline__ void pv_key(double (&o)[G][2], const double (&pr)[G], const unsigned (&vr)[16], int kg,
+                                       int nvalid) {
+  const unsigned vv = 4 * T + kg < nvalid ? vr[T] : 0u;   // rows past the context may hold anything
+  const float2 vf = __half22float2(*(const __half2*)&vv);
+  const double v0 = (double)vf.x, v1 = (double)vf.y;
+#pragma unroll
+  for (int h = 0; h < G; h += 2) fma_pv2<T>(o[h][0], o[h][1], o[h + 1][0], o[h + 1][1], pr[h], pr[h + 1], v0, v1);
+}
+template <int G, int... T>
+__device__ __forceinline__ void pv_keys(double (&o)[G][2], const double (&pr)[G], const unsigned (&vr)[16], int kg,
+                                        int nvalid, std::integer_sequence<int, T...>) {
+  (pv_key<T, G>(o, pr, vr, kg, nvalid), ...);
+}
+
+template <int G, int SPG>
+__global__ void __launch_bounds__(SPG * 256) k_attn_batch_f64(const AttnArgs a) {
+  static_assert(G % 2 == 0 && G <= 8 && G <= 4 * SPG, "heads per KV group");
+  constexpr int KEYS = SPG * PAGE;
+  __shared__ __align__(16) double sq[4][G][KEYS];      // score partials per dim quarter
+  __shared__ __align__(16) double ps[KEYS][G];         // p per key (16-byte reads give two heads)
+  __shared__ __align__(16) double po[SPG][G][HD];      // per-page P.V
+  __shared__ double xm[G], xl[G];
+  const int lane = threadIdx.x & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int pg = wv >> 2, dq = wv & 3;
+  const int nsp = (a.max_chunks + SPG - 1) / SPG;
+  // split-major order over the grid (nkv * nsp, T): the first splits of every token are dispatched first
+  const int wid = blockIdx.x + gridDim.x * blockIdx.y, per = gridDim.y * a.nkv;
+  const int sp = wid / per, j = (wid % per) / a.nkv, kvh = wid % a.nkv;
+  const int c = sp * SPG + pg;
+  // the page id does not depend on the position: both loads are in flight together
+  const int pgid = a.block_table[(size_t)j * a.bt_stride + min(c, a.max_chunks - 1)];
+  const int pos = a.pos[j];
+  const int nch = pos / PAGE + 1, nsplit = (nch + SPG - 1) / SPG;
+  if (sp >= nsplit) return;                             // uniform per workgroup
+  const bool live = c < nch;                            // uniform per wave; page 0 of the split is always live
+  const int nvalid = live ? min(PAGE, pos + 1 - c * PAGE) : 0;
+  const size_t base = live ? (((size_t)pgid * a.nkv + kvh) * PAGE * HD) : 0;
+
+  // this wave's f64 q values: qd[h][f] holds dims 32 dq + 16 f + (l % 16) of head h in every 16-lane row, so
+  // the scores' FMAs take them as row-broadcast DPP operands
+  double qd[G][2];
+  const int kg = lane >> 4, dp = lane & 15;
+  unsigned vr[16];
+  if (live) {
+    const double* q = a.q64 + ((size_t)j * a.nh + kvh * G) * HD + 32 * dq + (lane & 15);
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+      qd[h][0] = q[h * HD];
+      qd[h][1] = q[h * HD + 16];
+    }
+    // V operands of phase 3 (in flight during the scores): keys 4 t + l / 16, dims 32 dq + 2 (l % 16)
+#pragma unroll
+    for (int t = 0; t < 16; ++t)
+      vr[t] = ld_stream4(a.vcache + base + (size_t)(4 * t + kg) * HD + 32 * dq + 2 * dp);
+  }
+  // 1. scores of this wave's dim quarter
+  if (live) {
+    uint4 kr[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) kr[i] = ld_stream16(a.kcache + base + (size_t)lane * HD + 32 * dq + 8 * i);
+    double acc[G];
+#pragma unroll
+    for (int h = 0; h < G; ++h) acc[h] = 0.0;
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf) {                    // 16 dims at a time (fewer live registers)
+      double kd[16];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const __half2* k2 = (const __half2*)&kr[2 * hf + i];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const float2 kf = __half22float2(k2[u]);
+          kd[8 * i + 2 * u] = (double)kf.x;
+          kd[8 * i + 2 * u + 1] = (double)kf.y;
+        }
+      }
+#pragma unroll
+      for (int h = 0; h < G; ++h) fma16_bcast(acc[h], qd[h][hf], kd);
+    }
+#pragma unroll
+    for (int h = 0; h < G; ++h) sq[dq][h][pg * PAGE + lane] = acc[h];
+  } else {
+#pragma unroll
+    for (int h = 0; h < G; ++h) sq[dq][h][pg * PAGE + lane] = 0.0;
+  }
+  __syncthreads();
+  // 2. softmax: wave h < G takes head h over the split's keys (SPG per lane)
+  if (wv < G) {
+    const int h = wv;
+    double sv[SPG], m = -INFINITY;
+#pragma unroll
+    for (int g = 0; g < SPG; ++g) {
+      const int key = g * PAGE + lane;
+      const bool ok = sp * SPG * PAGE + key <= pos;
+      const double v = ((sq[0][h][key] + sq[1][h][key]) + sq[2][h][key]) + sq[3][h][key];
+      sv[g] = ok ? v * a.scale : -INFINITY;
+      m = fmax(m, sv[g]);
+    }
+    const double M = wave_max_d(m);                     // key 0 of the split is valid: finite
+    double l = 0.0;
+#pragma unroll
+    for (int g = 0; g < SPG; ++g) {
+      const double p = sv[g] == -INFINITY ? 0.0 : exp(sv[g] - M);
+      ps[g * PAGE + lane][h] = p;
+      l += p;
+    }
+    l = wave_sum_d(l);
+    if (lane == 0) { xm[h] = M; xl[h] = l; }
+  }
+  __syncthreads();
+  // 3. P.V of this wave's dims and page: lane (row kg, position t) holds p of key 4 t + kg of the page, which
+  // the FMAs of key 4 t + kg read as a row broadcast
+  if (live) {
+    double pr[G];
+    const double* prow = &ps[pg * PAGE + 4 * dp + kg][0];
+#pragma unroll
+    for (int h = 0; h < G; h += 2) {
+      const double2 v = *(const double2*)(prow + h);
+      pr[h] = v.x;
+      pr[h + 1] = v.y;
+    }
+    double o[G][2];
+#pragma unroll
+    for (int h = 0; h < G; ++h) o[h][0] = o[h][1] = 0.0;
+    pv_keys<G>(o, pr, vr, kg, nvalid, std::make_integer_sequence<int, 16>{});
+    // the 4 key groups (lanes l, l ^ 16, l ^ 32, l ^ 48): two lane swaps; x + y == y + x, so all four lanes
+    // end with the same bits
+#pragma unroll
+    for (int h = 0; h < G; ++h)
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        double x = o[h][u];
+        {
+          const int2 b = *reinterpret_cast<const int2*>(&x);
+          const auto rl = __builtin_amdgcn_permlane16_swap((unsigned)b.x, (unsigned)b.x, false, false);
+          const auto rh = __builtin_amdgcn_permlane16_swap((unsigned)b.y, (unsigned)b.y, false, false);
+          const int2 a0 = make_int2((int)rl[0], (int)rh[0]), a1 = make_int2((int)rl[1], (int)rh[1]);
+          x = *reinterpret_cast<const double*>(&a0) + *reinterpret_cast<const double*>(&a1);
+        }
+        {
+          const int2 b = *reinterpret_cast<const int2*>(&x);
+          const auto rl = __builtin_amdgcn_permlane32_swap((unsigned)b.x, (unsigned)b.x, false, false);
+          const auto rh = __builtin_amdgcn_permlane32_swap((unsigned)b.y, (unsigned)b.y, false, false);
+          const int2 a0 = make_int2((int)rl[0], (int)rh[0]), a1 = make_int2((int)rl[1], (int)rh[1]);
+          x = *reinterpret_cast<const double*>(&a0) + *reinterpret_cast<const double*>(&a1);
+        }
+        o[h][u] = x;
+      }
+    if (lane < 16) {
+#pragma unroll
+      for (int h = 0; h < G; ++h) *(double2*)&po[pg][h][32 * dq + 2 * dp] = make_double2(o[h][0], o[h][1]);
+    }
+  }
+  __syncthreads();
+  // 4. thread (head h, dims 8 dg .. 8 dg + 7): the split's live pages in page order
+  const int t = threadIdx.x;
+  if (t >= G * 16) return;                              // whole quads (Q8_1 blocks) stay together
+  const int h = t >> 4, dg = t & 15;
+  const int nlive = min(SPG, nch - sp * SPG);
+  double od[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) od[i] = po[0][h][8 * dg + i];
+  for (int g = 1; g < nlive; ++g)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) od[i] += po[g][h][8 * dg + i];
+  if (nsplit == 1) {
+    float of[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) of[i] = (float)(od[i] / xl[h]);
+    attn_out8(a, j, kvh * G + h, dg, of, true);
+    return;
+  }
+  double* P = a.part + ((((size_t)j * a.nkv + kvh) * nsp + sp) * G + h) * (HD + 2);
+#pragma unroll
+  for (int i = 0; i < 8; i += 2) *(double2*)(P + 8 * dg + i) = make_double2(od[i], od[i + 1]);
+  if (dg == 0) *(double2*)(P + HD) = make_double2(xm[h], xl[h]);
+}
+
+// Merge of k_attn_batch_f64's split partials, f64, in split order: o = sum_s e^(M_s - M) o_s / sum_s
+// e^(M_s - M) L_s (M = max_s M_s). Workgroup (KV head, token), thread (head t / 64, dims 2 (t % 64), + 1):
+// the splits' (M, L) and two values are loaded in batches of up to 20 splits (one memory latency each; a
+// later batch rescales the earlier sums to its maximum), then Q8_1 per 16-lane row (one 32-value block).
+template <int G, int SPG>
+__global__ void __launch_bounds__(G * 64) k_attn_merge_f64(const AttnArgs a) {
+  constexpr int SB = 20;                                // splits per load batch (2 KB of context per split)
+  const int nsp = (a.max_chunks + SPG - 1) / SPG;
+  const int kvh = blockIdx.x, j = blockIdx.y;
+  const int nsplit = (a.pos[j] / PAGE + 1 + SPG - 1) / SPG;
+  if (nsplit == 1) return;                              // finished by the attention kernel
+  const int h = threadIdx.x >> 6, dp = threadIdx.x & 63;
+  const double* P0 = a.part + (((size_t)j * a.nkv + kvh) * nsp * G + h) * (HD + 2);
+  const size_t st = (size_t)G * (HD + 2);
+  double M = -INFINITY, o0 = 0.0, o1 = 0.0, L = 0.0;
+  for (int s0 = 0; s0 < nsplit; s0 += SB) {             // one batch (one memory latency) up to SB splits
+    double2 ml[SB], x[SB];
+#pragma unroll
+    for (int s = 0; s < SB; ++s)
+      if (s0 + s < nsplit) {
+        ml[s] = *(const double2*)(P0 + (s0 + s) * st + HD);
+        x[s] = *(const double2*)(P0 + (s0 + s) * st + 2 * dp);
+      }
+    double Mb = M;
+#pragma unroll
+    for (int s = 0; s < SB; ++s)
+      if (s0 + s < nsplit) Mb = fmax(Mb, ml[s].x);
+    if (s0) {                                           // rescale the earlier batches to the new maximum
+      const double r = exp(M - Mb);
+      o0 *= r; o1 *= r; L *= r;
+    }
+    M = Mb;
+#pragma unroll
+    for (int s = 0; s < SB; ++s)
+      if (s0 + s < nsplit) {
+        const double f = exp(ml[s].x - M);
+        L = fma(f, ml[s].y, L);
+        o0 = fma(f, x[s].x, o0);
+        o1 = fma(f, x[s].y, o1);
+      }
+  }
+  const float v0 = (float)(o0 / L), v1 = (float)(o1 / L);
+  const size_t n = (size_t)a.nh * HD, e = (size_t)j * n + (size_t)(kvh * G + h) * HD + 2 * dp;
+  if (a.o32) *(float2*)(a.o32 + e) = make_float2(v0, v1);
+  // Q8_1 of the row's 32 values (16 lanes x 2), the rule of q8_code
+  float amax = fmaxf(fabsf(v0), fabsf(v1));
+  amax = fmaxf(amax, dpp<DPP_XOR1>(amax));
+  amax = fmaxf(amax, dpp<DPP_XOR2>(amax));
+  amax = fmaxf(amax, dpp<DPP_HALF_MIRROR>(amax));
+  amax = fmaxf(amax, dpp<DPP_MIRROR>(amax));
+  const float d32 = q8_scale(amax);
+  const int q0 = q8_code(v0, d32), q1 = q8_code(v1, d32);
+  int sq = q0 + q1;
+  sq += dpp<DPP_XOR1>(sq);
+  sq += dpp<DPP_XOR2>(sq);
+  sq += dpp<DPP_HALF_MIRROR>(sq);
+  sq += dpp<DPP_MIRROR>(sq);
+  *(short*)(a.oq + e) = (short)((q0 & 255) | ((q1 & 255) << 8));
+  if ((dp & 15) == 0) a.ods[e / 32] = __halves2half2(__float2half_rn(d32), q8_s16(d32, sq));
+}
+
 }  // namespace q355

@@ -471,7 +471,7 @@ static int launch_mmq(GemvArgs a, int KS, hipStream_t s) {
   constexpr size_t LDS_MAX = 65536;
   const int nb = a.K / 32, per = (nb + KS - 1) / KS;
   const dim3 grid(a.N / (16 * NT), KS, (a.T + TT - 1) / TT);
-  const size_t pb = (size_t)NW * NT * TT * 16 * 4;
+  const size_t pb = (size_t)NW * NT * TT * 16 * sizeof(MmqAcc<TG>);     // wave partials
   if (per <= NW * 5) {
     // narrow K slices (decode): the whole slice's nibbles in registers (KPW blocks per wave), its activations
     // and scales in LDS; wider slices run faster through the pipelined kernel below
@@ -651,6 +651,43 @@ extern "C" int q355_attn_decode_partials(const void* q, const void* kcache, cons
   return launched("attn_decode_partials");
 }
 
+// Batched decode attention of the int8 path in f64 (k_attn_batch_f64, 4 pages per split) + the f64 split merge
+// -> Q8_1 oq/ods (and fp32 o32 if asked). q64: the f64 queries the QKV epilogue writes.
+constexpr int ATTN64_SPG = 2;                         // pages per split (4 waves per page)
+
+template <int G>
+static int launch_attn_f64(const AttnArgs& a, int T, hipStream_t s) {
+  const int nsp = (a.max_chunks + ATTN64_SPG - 1) / ATTN64_SPG;
+  hipLaunchKernelGGL((k_attn_batch_f64<G, ATTN64_SPG>), dim3(a.nkv * nsp, T), dim3(ATTN64_SPG * 256), 0, s, a);
+  if (int e = launched("attn_decode_f64")) return e;
+  if (nsp == 1) return Q355_OK;                         // every token fits one split: finished above
+  hipLaunchKernelGGL((k_attn_merge_f64<G, ATTN64_SPG>), dim3(a.nkv, T), dim3(G * 64), 0, s, a);
+  return launched("attn_merge_f64");
+}
+
+extern "C" int q355_attn_decode_f64(const double* q64, const void* kcache, const void* vcache, const int32_t* pos,
+                                    const int32_t* block_table, int bt_stride, int nh, int nkv, int max_chunks,
+                                    double scale, double* part, int8_t* oq, void* ods, float* o32, int T,
+                                    void* stream) {
+  REQUIRE(q64 && kcache && vcache && pos && block_table && part && oq && ods, "attn_decode_f64: null pointer");
+  REQUIRE(nh > 0 && nkv > 0 && nh % nkv == 0, "attn_decode_f64: nh=%d nkv=%d", nh, nkv);
+  REQUIRE(nh / nkv == 6 || nh / nkv == 4 || nh / nkv == 8, "attn_decode_f64: GQA group %d (4, 6 or 8 supported)",
+          nh / nkv);
+  REQUIRE(max_chunks > 0 && max_chunks <= bt_stride && max_chunks <= 64, "attn_decode_f64: max_chunks=%d bt_stride=%d",
+          max_chunks, bt_stride);
+  REQUIRE(T > 0 && T <= 65535, "attn_decode_f64: T=%d", T);
+  AttnArgs a = {};
+  a.q64 = q64; a.kcache = (const __half*)kcache; a.vcache = (const __half*)vcache;
+  a.pos = pos; a.block_table = block_table; a.bt_stride = bt_stride; a.nh = nh; a.nkv = nkv;
+  a.max_chunks = max_chunks; a.scale = scale; a.part = part; a.oq = oq; a.ods = (half2*)ods; a.o32 = o32;
+  hipStream_t s = (hipStream_t)stream;
+  switch (nh / nkv) {
+    case 4: return launch_attn_f64<4>(a, T, s);
+    case 6: return launch_attn_f64<6>(a, T, s);
+    default: return launch_attn_f64<8>(a, T, s);
+  }
+}
+
 extern "C" int q355_attn_decode_partials_f16(const void* q, const void* kcache, const void* vcache, const int32_t* pos,
                                              const int32_t* block_table, int bt_stride, int nh, int nkv, int max_chunks,
                                              double scale, double* part, void* oh, int T, void* stream) {
@@ -700,7 +737,7 @@ extern "C" int q355_mmq_attn_o_resid(const uint8_t* qs, const void* d, int N, co
   // one K slice per head (4 blocks), 16 tokens per workgroup
   constexpr int TT = 16, NT = 4, NW = 4, per = 4;
   const size_t xb = (size_t)TT * (per * 32 + 16) + (size_t)TT * per * 8 + (size_t)NT * per * 32;
-  const size_t pb = (size_t)NW * NT * TT * 16 * 4;
+  const size_t pb = (size_t)NW * NT * TT * 16 * sizeof(MmqAcc<1>);
   hipLaunchKernelGGL((k_mmq_reg<1, NT, NW, 1, EPI_RESID_FIX, true>), dim3(N / 64, nh, (T + TT - 1) / TT), dim3(256),
                      xb > pb ? xb : pb, (hipStream_t)stream, a);
   return launched("mmq_attn_o_resid");
@@ -897,7 +934,8 @@ extern "C" int q355_qkv_finish(int64_t* acc, const float* bias, const float* rop
 extern "C" int q355_mmq_qkv_rope(const uint8_t* qs, const void* d, int N, int K, const int8_t* xq, const void* xds,
                                  int T, const float* bias, const float* rope_cos, const float* rope_sin,
                                  const int32_t* pos, const int32_t* block_table, int bt_stride, int seq_stride,
-                                 void* kcache, void* vcache, void* qout, int nh, int nkv, void* stream) {
+                                 void* kcache, void* vcache, void* qout, double* q64, int nh, int nkv,
+                                 void* stream) {
   if (int e = check_mat("mmq_qkv_rope", qs, d, N, K)) return e;
   REQUIRE(xq && xds && bias && rope_cos && rope_sin && pos && block_table && kcache && vcache && qout,
           "mmq_qkv_rope: null pointer");
@@ -909,7 +947,8 @@ extern "C" int q355_mmq_qkv_rope(const uint8_t* qs, const void* d, int N, int K,
   a.qs = qs; a.d = (const __half*)d; a.N = N; a.K = K; a.T = T; a.xq = xq; a.xds = (const half2*)xds;
   a.aux = bias; a.rope_cos = rope_cos; a.rope_sin = rope_sin; a.pos = pos; a.block_table = block_table;
   a.bt_stride = bt_stride; a.seq_stride = seq_stride;
-  a.kcache = (__half*)kcache; a.vcache = (__half*)vcache; a.qout = (__half*)qout; a.nh = nh; a.nkv = nkv;
+  a.kcache = (__half*)kcache; a.vcache = (__half*)vcache; a.qout = (__half*)qout; a.qout64 = q64;
+  a.nh = nh; a.nkv = nkv;
   if (T <= 32) {                                     // decode batches: register-resident, all tokens per workgroup
     const int r = T <= 16 ? launch_mmq_r_tg<1, EPI_QKV, false>(a, (hipStream_t)stream)
                           : launch_mmq_r_tg<2, EPI_QKV, false>(a, (hipStream_t)stream);

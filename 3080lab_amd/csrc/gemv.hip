@@ -421,7 +421,9 @@ __device__ __forceinline__ void epilogue(const GemvArgs& a, A (&part)[NW][NT][T]
         const double out = hi ? (hi_v * c + lo_v * s) : (lo_v * c - hi_v * s);
         const int dim = i + (HD / 2) * hi;
         if (row < nq) {
-          a.qout[(size_t)j * nq + (row / HD) * HD + dim] = half_rn(out);
+          const __half hq = half_rn(out);
+          a.qout[(size_t)j * nq + (row / HD) * HD + dim] = hq;
+          if (a.qout64) a.qout64[(size_t)j * nq + (row / HD) * HD + dim] = (double)__half2float(hq);
         } else {
           const int kvh = (row - nq) / HD;
           a.kcache[(((size_t)pg * a.nkv + kvh) * PAGE + pos % PAGE) * HD + dim] = half_rn(out);
@@ -478,7 +480,9 @@ __device__ __forceinline__ void qkv_store(const GemvArgs& a, A (&part)[NW][NT][T
     const double out = hi ? (hi_v * c + lo_v * s) : (lo_v * c - hi_v * s);
     const int dim = i + (HD / 2) * hi;
     if (row < nq) {
-      a.qout[(size_t)q.j * nq + (row / HD) * HD + dim] = half_rn(out);
+      const __half hq = half_rn(out);
+      a.qout[(size_t)q.j * nq + (row / HD) * HD + dim] = hq;
+      if (a.qout64) a.qout64[(size_t)q.j * nq + (row / HD) * HD + dim] = (double)__half2float(hq);
     } else {
       a.kcache[(((size_t)q.pg * a.nkv + (row - nq) / HD) * PAGE + q.pos % PAGE) * HD + dim] = half_rn(out);
     }

@@ -35,6 +35,14 @@ constexpr int TILE_CB = 4;                           // K blocks per LDS chunk
 #define Q355_TRACE_POINT(k)
 #endif
 
+// acc += (d_w d_x / 16) (16 dot'): both factors are exact in fp32 (a product of two fp16 values; an int32 below
+// 2^20), so the f64 form adds the exact block term with one f64 rounding -- decode-batch products accumulate
+// in f64, so every Q8_1 quantizer input downstream agrees with the f64 oracle far below a quantization step;
+// prefill-size products keep fp32 (their outputs are checked at fp32 tolerance).
+__device__ __forceinline__ float mac(float s, int c, float acc) { return fmaf(s, (float)c, acc); }
+__device__ __forceinline__ double mac(float s, int c, double acc) { return fma((double)s, (double)c, acc); }
+template <int TG> using MmqAcc = typename std::conditional<TG == 1, double, float>::type;
+
 // One K block (LDS column bb) against NT tiles x TG token groups: all NT * TG MFMAs are issued before
 // any of their results is scaled, so the matrix-core latency overlaps instead of stalling each product.
 // Weights enter as 16 (q - 8) (snib8) and xd holds d_x / 16, so d_w xd (16 dot') = d_w d_x (dot - 8 sum q_x)
@@ -42,9 +50,9 @@ constexpr int TILE_CB = 4;                           // K blocks per LDS chunk
 // dwl[q]: d_w of row li of tile 4 q + lg (0 past NT); the d_w d_x products of all outputs come from 4-block
 // outer products on the matrix cores (lane l receives d_w[tile][4 lg + v] d_x[token li] in register
 // 4 (tile % 4) + v).
-template <int NT, int TG>
+template <int NT, int TG, typename ACC>
 __device__ __forceinline__ void mmq_block(const uint2 (&w)[NT], const float (&dwl)[(NT + 3) / 4], const int8_t* __restrict__ xq,
-                                          int xstride, const float* xd, int ld, int bb, int li, int lg, float (&acc)[NT][TG][4]) {
+                                          int xstride, const float* xd, int ld, int bb, int li, int lg, ACC (&acc)[NT][TG][4]) {
   v4i c[NT][TG];
   float dx[TG];
   const v4i zero = {0, 0, 0, 0};
@@ -66,7 +74,7 @@ __device__ __forceinline__ void mmq_block(const uint2 (&w)[NT], const float (&dw
 #pragma unroll
     for (int t = 0; t < NT; ++t)
 #pragma unroll
-      for (int v = 0; v < 4; ++v) acc[t][g][v] = fmaf(sc[t >> 2][4 * (t & 3) + v], (float)c[t][g][v], acc[t][g][v]);
+      for (int v = 0; v < 4; ++v) acc[t][g][v] = mac(sc[t >> 2][4 * (t & 3) + v], c[t][g][v], acc[t][g][v]);
   }
 }
 
@@ -191,7 +199,7 @@ __device__ __forceinline__ long q8_1_mfma8(const float (&x)[8], float& df) {
 template <int TG, int NT, int NW, int KPW, int EPI, bool XF32>
 __global__ void __launch_bounds__(NW * 64) k_mmq_r(const GemvArgs a) {
   Q355_TRACE_POINT(0);
-  __shared__ float part[NW][NT][16 * TG][16];
+  __shared__ double part[NW][NT][16 * TG][16];
   constexpr int TT = 16 * TG;
   const int K = a.K, nb = K / 32;
   const KSlice ks(nb);
@@ -272,13 +280,13 @@ __global__ void __launch_bounds__(NW * 64) k_mmq_r(const GemvArgs a) {
     qp = qkv_prefetch<TT, NT>(a, tile0);
   }
   Q355_TRACE_POINT(1);
-  float acc[NT][TG][4];
+  double acc[NT][TG][4];
 #pragma unroll
   for (int t = 0; t < NT; ++t)
 #pragma unroll
     for (int g = 0; g < TG; ++g)
 #pragma unroll
-      for (int v = 0; v < 4; ++v) acc[t][g][v] = 0.f;
+      for (int v = 0; v < 4; ++v) acc[t][g][v] = 0.0;
 #pragma unroll
   for (int i = 0; i < KPW; ++i) {
     if (ks.b0 + wv + NW * i < ks.b1) {                    // uniform per wave
@@ -302,7 +310,7 @@ __global__ void __launch_bounds__(NW * 64) k_mmq_r(const GemvArgs a) {
         for (int t = 0; t < NT; ++t)
 #pragma unroll
           for (int v = 0; v < 4; ++v)
-            acc[t][g][v] = fmaf(sc[t >> 2][4 * (t & 3) + v], (float)c[t][g][v], acc[t][g][v]);
+            acc[t][g][v] = mac(sc[t >> 2][4 * (t & 3) + v], c[t][g][v], acc[t][g][v]);
       }
     }
   }
@@ -347,13 +355,14 @@ __global__ void __launch_bounds__(NW * 64) k_mmq(const GemvArgs a) {
   for (int q = 0; q < NQ; ++q) wd[q] = a.d + (size_t)(tile0 + min(4 * q + lg, NT - 1)) * nb * 16 + li;
   uint2 wA[NT], wB[NT];
   float dA[NQ], dB[NQ];
-  float acc[NT][TG][4];
+  using ACC = MmqAcc<TG>;
+  ACC acc[NT][TG][4];
 #pragma unroll
   for (int t = 0; t < NT; ++t)
 #pragma unroll
     for (int g = 0; g < TG; ++g)
 #pragma unroll
-      for (int v = 0; v < 4; ++v) acc[t][g][v] = 0.f;
+      for (int v = 0; v < 4; ++v) acc[t][g][v] = 0;
 
   for (int c0 = ks.b0; c0 < ks.b1; c0 += ch) {      // chunks of the K slice
     const int nbc = min(ch, ks.b1 - c0);
@@ -371,7 +380,7 @@ __global__ void __launch_bounds__(NW * 64) k_mmq(const GemvArgs a) {
     Q355_TRACE_POINT(1);
 
     auto compute_blk = [&](int bb, const uint2 (&w)[NT], const float (&dv)[NQ]) {
-      mmq_block<NT, TG>(w, dv, xq, xstride, xd, ch, bb, li, lg, acc);
+      mmq_block<NT, TG, ACC>(w, dv, xq, xstride, xd, ch, bb, li, lg, acc);
     };
     // 2-deep pipeline over this wave's blocks wv, wv + NW, ... of the chunk
     int bb = wv;
@@ -388,7 +397,7 @@ __global__ void __launch_bounds__(NW * 64) k_mmq(const GemvArgs a) {
   // partials -> LDS (reusing the activation area), then the shared epilogues
   __syncthreads();
   Q355_TRACE_POINT(3);
-  float(&part)[NW][NT][TT][16] = *reinterpret_cast<float(*)[NW][NT][TT][16]>(lds);
+  ACC(&part)[NW][NT][TT][16] = *reinterpret_cast<ACC(*)[NW][NT][TT][16]>(lds);
 #pragma unroll
   for (int t = 0; t < NT; ++t)
 #pragma unroll
@@ -454,13 +463,14 @@ __global__ void __launch_bounds__(NW * 64) k_mmq_reg(const GemvArgs a) {
   else stage_x<TT, NW>(a, xq, xd, xstride, nbs, tok0, ntok, ks.b0, nbs);
   __syncthreads();
   Q355_TRACE_POINT(1);
-  float acc[NT][TG][4];
+  using ACC = MmqAcc<TG>;
+  ACC acc[NT][TG][4];
 #pragma unroll
   for (int t = 0; t < NT; ++t)
 #pragma unroll
     for (int g = 0; g < TG; ++g)
 #pragma unroll
-      for (int v = 0; v < 4; ++v) acc[t][g][v] = 0.f;
+      for (int v = 0; v < 4; ++v) acc[t][g][v] = 0;
 #pragma unroll
   for (int i = 0; i < KPW; ++i) {
     const int bb = wv + NW * i;
@@ -469,13 +479,13 @@ __global__ void __launch_bounds__(NW * 64) k_mmq_reg(const GemvArgs a) {
 #pragma unroll
       for (int q = 0; q < (NT + 3) / 4; ++q)
         dv[q] = 4 * q + lg < NT ? __half2float(((const __half*)wsc)[((4 * q + lg) * nbs + bb) * 16 + li]) : 0.f;
-      mmq_block<NT, TG>(w[i], dv, xq, xstride, xd, nbs, bb, li, lg, acc);
+      mmq_block<NT, TG, ACC>(w[i], dv, xq, xstride, xd, nbs, bb, li, lg, acc);
     }
   }
   Q355_TRACE_POINT(2);
   __syncthreads();
   Q355_TRACE_POINT(3);
-  float(&part)[NW][NT][TT][16] = *reinterpret_cast<float(*)[NW][NT][TT][16]>(lds);
+  ACC(&part)[NW][NT][TT][16] = *reinterpret_cast<ACC(*)[NW][NT][TT][16]>(lds);
 #pragma unroll
   for (int t = 0; t < NT; ++t)
 #pragma unroll
@@ -723,6 +733,11 @@ __global__ void __launch_bounds__(256) k_mmq_tile(const GemvArgs a) {
                                      : a.kcache + (((size_t)pg * a.nkv + (row - nq) / HD) * PAGE + pos % PAGE) * HD;
               dst[i] = lo;
               dst[i + HD / 2] = hi;
+              if (row < nq && a.qout64) {
+                double* d64 = a.qout64 + (size_t)tok * nq + (row / HD) * HD;
+                d64[i] = (double)__half2float(lo);
+                d64[i + HD / 2] = (double)__half2float(hi);
+              }
             } else {
               const int rv = row - nq - nk;
               __half2* vd = (__half2*)(a.vcache + (((size_t)pg * a.nkv + rv / HD) * PAGE + pos % PAGE) * HD + rv % HD);

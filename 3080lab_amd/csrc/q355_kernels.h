@@ -78,6 +78,7 @@ struct GemvArgs {
   __half* kcache;              // [n_pages][nkv][PAGE][HD]
   __half* vcache;
   __half* qout;                // [T][nh*HD]
+  double* qout64;              // optional: the same q values widened to f64 [T][nh*HD] (k_attn_batch_f64 input)
   int nh, nkv;
   // SWIGLU_Q8 output: Q8_1 of silu(g) * u, [T][N/2] and [T][N/64]
   int8_t* oq;
@@ -121,6 +122,7 @@ __host__ __device__ inline size_t pf_ws_floats(int nqb, int nkv, int G, int max_
 
 struct AttnArgs {
   const __half* q;             // [T][nh*HD] RoPE'd fp16 queries
+  const double* q64;           // the same queries widened to f64 (k_attn_batch_f64)
   const __half* kcache;        // [n_pages][nkv][PAGE][HD]
   const __half* vcache;
   const int* pos;              // [T] position of the token (attends to 0..pos)

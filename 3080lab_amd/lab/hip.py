@@ -61,8 +61,9 @@ _SIGS = {
     "q355_mega_decode": [_P, c_int, _P, _P, _P, c_int, _P, _P, _P, c_int, c_double, _P, _P, _P, _P, _P,
                          ctypes.c_int64, _P],
     "q355_qkv_finish": [_P, _P, _P, _P, _P, _P, c_int, c_int, _P, _P, _P, c_int, c_int, c_int, _P],
-    "q355_mmq_qkv_rope": [_P, _P, c_int, c_int, _P, _P, c_int, _P, _P, _P, _P, _P, c_int, c_int, _P, _P, _P, c_int,
-                          c_int, _P],
+    "q355_mmq_qkv_rope": [_P, _P, c_int, c_int, _P, _P, c_int, _P, _P, _P, _P, _P, c_int, c_int, _P, _P, _P, _P,
+                          c_int, c_int, _P],
+    "q355_attn_decode_f64": [_P, _P, _P, _P, _P, c_int, c_int, c_int, c_int, c_double, _P, _P, _P, _P, c_int, _P],
     "q355_gemm_f16_qkv_rope": [_P, _P, c_int, c_int, _P, c_int, _P, _P, _P, _P, _P, c_int, c_int, _P, _P, _P,
                                c_int, c_int, _P],
 }

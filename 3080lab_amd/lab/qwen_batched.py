@@ -101,6 +101,7 @@ class BatchedDecoder:
         self.mq = torch.zeros(B, c.FFN, dtype=torch.int8, device=dev)
         self.mds = torch.zeros(B, c.FFN // 32, 2, dtype=torch.float16, device=dev)
         self.q = torch.zeros(B, c.NH * c.HD, dtype=torch.float16, device=dev)
+        self.q64 = torch.zeros(B, c.NH * c.HD, dtype=torch.float64, device=dev)   # the int8 path's f64 queries
         self.part = torch.zeros(B, c.NH, self.max_chunks, c.HD + 2, dtype=torch.float64, device=dev)
         self.aq = torch.zeros(B, c.NH * c.HD, dtype=torch.int8, device=dev)
         self.xh = torch.zeros(B, max(H, c.NH * c.HD), dtype=torch.float16, device=dev)
@@ -167,23 +168,15 @@ class BatchedDecoder:
         m, c, B = self.m, self.cfg, self.B
         L = m.layers[i]
         self._norm(L["ln1"])
-        W = L["qkv"]                 # bias, RoPE and the K/V write in the product's epilogue
+        W = L["qkv"]                 # bias, RoPE and the K/V write in the product's epilogue; q also widened to f64
         call("q355_mmq_qkv_rope", ptr(W.qs), ptr(W.d), W.N, W.K, ptr(self.xq), ptr(self.xds), B, ptr(L["qkv_b"]),
              ptr(m.cos), ptr(m.sin), ptr(self.pos), ptr(self.block_table), self.max_chunks, 1, ptr(self.kc[i]),
-             ptr(self.vc[i]), ptr(self.q), c.NH, c.NKV)
-        if B <= MERGE_IN_O_MAX_B:
-            # attention leaves split partials; the O product merges them per head while staging its activations
-            call("q355_attn_decode_partials", ptr(self.q), ptr(self.kc[i]), ptr(self.vc[i]), ptr(self.pos),
-                 ptr(self.block_table), self.max_chunks, c.NH, c.NKV, self.max_chunks, self.scale, ptr(self.part),
-                 ptr(self.aq), ptr(self.ads), B)
-            W = L["o"]
-            call("q355_mmq_attn_o_resid", ptr(W.qs), ptr(W.d), W.N, ptr(self.part), self.max_chunks, ptr(self.pos),
-                 c.NH, c.NKV, ptr(self.aq), ptr(self.ads), ptr(self.h), B)
-        else:
-            call("q355_attn_decode", ptr(self.q), ptr(self.kc[i]), ptr(self.vc[i]), ptr(self.pos),
-                 ptr(self.block_table), self.max_chunks, c.NH, c.NKV, self.max_chunks, self.scale, ptr(self.part),
-                 ptr(self.aq), ptr(self.ads), None, B, 1)
-            self._mmq(L["o"], self.aq, self.ads, 6, yfix=self.h)
+             ptr(self.vc[i]), ptr(self.q), ptr(self.q64), c.NH, c.NKV)
+        # f64 attention (the batch-1 arithmetic), split merge in f64 -> Q8_1
+        call("q355_attn_decode_f64", ptr(self.q64), ptr(self.kc[i]), ptr(self.vc[i]), ptr(self.pos),
+             ptr(self.block_table), self.max_chunks, c.NH, c.NKV, self.max_chunks, self.scale, ptr(self.part),
+             ptr(self.aq), ptr(self.ads), None, B)
+        self._mmq(L["o"], self.aq, self.ads, 6, yfix=self.h)
         self._norm(L["ln2"])
         if B <= 16:
             # SwiGLU kept in fp32 and quantized to Q8_1 inside the down product (register-resident kernels;
@@ -322,7 +315,7 @@ class Prefill:
             # one writer per output: the finish (bias, RoPE, K/V write) runs in the GEMM epilogue
             call("q355_mmq_qkv_rope", ptr(W.qs), ptr(W.d), W.N, W.K, ptr(self.xq), ptr(self.xds), P, ptr(L["qkv_b"]),
                  ptr(m.cos), ptr(m.sin), ptr(self.pos), ptr(d.block_table), d.max_chunks, 0, ptr(d.kc[i]),
-                 ptr(d.vc[i]), ptr(self.q), c.NH, c.NKV)
+                 ptr(d.vc[i]), ptr(self.q), None, c.NH, c.NKV)
         else:
             call("q355_mmq_q4_0_q8_1", ptr(W.qs), ptr(W.d), W.N, W.K, ptr(self.xq), ptr(self.xds), P, 6,
                  None, ptr(self.qkv_acc), None, None, None, None)

@@ -265,12 +265,23 @@ int q355_qkv_finish(int64_t* acc, const float* bias, const float* rope_cos, cons
 
 /* QKV: Q4_0 x Q8_1 product of T tokens on int8 MFMA (register-resident for T <= 32 and K <= 1536, LDS-tiled
  * otherwise) with the QKV finish in its epilogue: + bias, RoPE, fp16 q out [T][nh*128], fp16 K/V cache rows at pos[j] of sequence j * seq_stride
- * (arguments as q355_qkv_finish). N = (nh + 2 nkv) * 128 in the device row order, N % 128 == 0.
+ * (arguments as q355_qkv_finish). q64 (optional, may be NULL): the same fp16 q values widened to f64 [T][nh*128],
+ * the input of q355_attn_decode_f64. N = (nh + 2 nkv) * 128 in the device row order, N % 128 == 0.
  * Replaces gemm_q4i8_ms_source with the 'biasf_kv' epilogue (lab/qwen_batched.py:1271-1561, 1316-1362). */
 int q355_mmq_qkv_rope(const uint8_t* qs, const void* d, int N, int K, const int8_t* xq, const void* xds, int T,
                       const float* bias, const float* rope_cos, const float* rope_sin, const int32_t* pos,
                       const int32_t* block_table, int bt_stride, int seq_stride, void* kcache, void* vcache,
-                      void* qout, int nh, int nkv, void* stream);
+                      void* qout, double* q64, int nh, int nkv, void* stream);
+
+/* Batched decode attention of the int8 path, in f64 (the batch-1 arithmetic: f64 scores, softmax and P.V of
+ * the fp16 q/K/V): T tokens, token j attends to positions 0 .. pos[j] of its paged K/V (block_table row j).
+ * q64 [T][nh*128] f64 (q355_mmq_qkv_rope's q64). Splits of 2 pages, 4 waves per page, the GQA group's query
+ * heads together; splits merged in f64 in split order -> Q8_1 oq [T][nh*128] / ods [T][nh*4] (and fp32 o32,
+ * optional). part: scratch of T * nh * ceil(max_chunks / 2) * 130 doubles. GQA group 4, 6 or 8.
+ * Replaces the batched ATTN4 + combine of scripts/qwen_batched_decode.py:156-187 (lab/qwen_kernels.py:517-605). */
+int q355_attn_decode_f64(const double* q64, const void* kcache, const void* vcache, const int32_t* pos,
+                         const int32_t* block_table, int bt_stride, int nh, int nkv, int max_chunks, double scale,
+                         double* part, int8_t* oq, void* ods, float* o32, int T, void* stream);
 
 /* Causal GQA prefill attention (fp16 MFMA, fp32 accumulation) for one sequence: queries q fp16
  * [P][nh*128] at positions pos0 .. pos0 + P - 1 attend to keys 0 .. their own position in the paged cache

@@ -82,9 +82,9 @@ def test_attn_prefill_bad_args(cuda):
     with pytest.raises(HipError, match="null output"):
         call("q355_attn_prefill_q8_1", 1, 1, 1, 1, 0, 16, 12, 2, 0.1, None, 1, None, 0)
     with pytest.raises(HipError, match="mmq_qkv_rope"):        # N must be (nh + 2 nkv) * 128
-        call("q355_mmq_qkv_rope", 16, 16, 1024, 1536, 16, 16, 64, 16, 16, 16, 16, 16, 4, 0, 16, 16, 16, 12, 2)
+        call("q355_mmq_qkv_rope", 16, 16, 1024, 1536, 16, 16, 64, 16, 16, 16, 16, 16, 4, 0, 16, 16, 16, None, 12, 2)
     with pytest.raises(HipError, match="mmq_qkv_rope"):        # seq_stride is 0 or 1
-        call("q355_mmq_qkv_rope", 16, 16, 2048, 1536, 16, 16, 64, 16, 16, 16, 16, 16, 4, 2, 16, 16, 16, 12, 2)
+        call("q355_mmq_qkv_rope", 16, 16, 2048, 1536, 16, 16, 64, 16, 16, 16, 16, 16, 4, 2, 16, 16, 16, None, 12, 2)
 
 
 CFG_S = QM.Config(L=2, V=4096)
@@ -191,7 +191,7 @@ def test_mmq_qkv_rope_equals_finish(cuda, T, seq_stride):
         q = torch.zeros(T, c.NH * 128, dtype=torch.float16, device=cuda)
         if fused:
             call("q355_mmq_qkv_rope", ptr(W.qs), ptr(W.d), N, K, ptr(xq), ptr(xds), T, ptr(bias), ptr(cos), ptr(sin),
-                 ptr(pos), ptr(table), bt_stride, seq_stride, ptr(kc), ptr(vc), ptr(q), c.NH, c.NKV)
+                 ptr(pos), ptr(table), bt_stride, seq_stride, ptr(kc), ptr(vc), ptr(q), None, c.NH, c.NKV)
         else:
             acc = torch.zeros(T, N, dtype=torch.int64, device=cuda)
             call("q355_mmq_q4_0_q8_1", ptr(W.qs), ptr(W.d), N, K, ptr(xq), ptr(xds), T, 6, None, ptr(acc),
