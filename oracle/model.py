@@ -101,12 +101,13 @@ def attn_decode(q: np.ndarray, K: np.ndarray, V: np.ndarray, n_ctx: int, nh: int
     hd = q.shape[-1]
     grp = nh // nkv
     out = np.empty((nh, hd), np.float64)
-    for h in range(nh):
-        k = K[h // grp, :n_ctx].astype(np.float64)
-        v = V[h // grp, :n_ctx].astype(np.float64)
-        s = k @ q[h].astype(np.float64) / math.sqrt(hd)
-        p = np.exp(s - s.max())
-        out[h] = p @ v / p.sum()
+    for g in range(nkv):                                 # K/V widened once per KV head
+        k = K[g, :n_ctx].astype(np.float64)
+        v = V[g, :n_ctx].astype(np.float64)
+        for h in range(g * grp, (g + 1) * grp):
+            s = k @ q[h].astype(np.float64) / math.sqrt(hd)
+            p = np.exp(s - s.max())
+            out[h] = p @ v / p.sum()
     return out.reshape(-1).astype(np.float32)
 
 
@@ -241,6 +242,34 @@ class Model:
         h = self.embed(toks)
         for i in range(len(self.w["layers"])):
             h = self.layer(i, h, pos0, cache)
+        return h
+
+    def decode_batch(self, toks, positions, caches) -> np.ndarray:
+        """One decode token for each of S independent sequences: token toks[s] at position positions[s] of the
+        sequence whose cache is caches[s] (the batched step, scripts/qwen_batched_decode.py:156-187). Each row
+        follows Model.layer's single-token arithmetic (the same rounding points); only the GEMV products of the
+        S rows are evaluated as one matrix product. Writes each sequence's K/V rows; returns h float64 [S, H].
+        pinned by: equality (1e-12) with Model.forward run per sequence (tests/test_oracle.py)."""
+        c = self.cfg
+        S = len(toks)
+        h = self.embed(toks).astype(np.float64)
+        for i, (L, lin) in enumerate(zip(self.w["layers"], self.lin)):
+            x = rmsnorm(h, L["ln1"], c.eps).astype(np.float32)
+            q = lin["q"](x) + L["bq"]
+            k = lin["k"](x) + L["bk"]
+            v = lin["v"](x) + L["bv"]
+            att = np.empty((S, c.NH * c.HD), np.float32)
+            for r in range(S):
+                p, cache = int(positions[r]), caches[r]
+                cs, sn = self.cos[p], self.sin[p]
+                qh = rope(q[r].reshape(c.NH, c.HD), cs, sn).astype(np.float16)
+                cache["K"][i, :, p] = rope(k[r].reshape(c.NKV, c.HD), cs, sn).astype(np.float16)
+                cache["V"][i, :, p] = v[r].reshape(c.NKV, c.HD).astype(np.float16)
+                att[r] = attn_decode(qh, cache["K"][i], cache["V"][i], p + 1, c.NH, c.NKV)
+            h = h + lin["o"](att)
+            x = rmsnorm(h, L["ln2"], c.eps).astype(np.float32)
+            m = silu_mul(lin["g"](x), lin["u"](x)).astype(np.float32)
+            h = h + lin["d"](m)
         return h
 
     def logits(self, h: np.ndarray) -> np.ndarray:

@@ -356,9 +356,10 @@ def test_layer_config1(one_layer):
     cache["K"][0, :, :past] = Kp
     cache["V"][0, :, :past] = Vp
     ref = om.layer(0, h, past, cache)
-    got = dec.h_f32().cpu().numpy()
-    assert relerr(got - h, ref - h) < 5e-3
-    assert relerr(got, ref) < REL
+    got = dec.h_f64().cpu().numpy()
+    # north_star's bound is 1e-3 relative; the f64 layer (fixed-point residual) holds the layer's update to 1e-9
+    assert relerr(got - h, ref - h) < 1e-9
+    assert relerr(got, ref) < 1e-9
 
 
 # --------------------------------------------------------------------------------------------------

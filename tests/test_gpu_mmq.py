@@ -205,10 +205,20 @@ def check_greedy(got, ref, margins, what):
 NEAR_TIE = 1e-2
 
 
-# Largest teacher-forced logit deviation from the oracle in the matching arithmetic, with margin: measured
-# 0.070 (int8 MMQ: its fp16-P attention and fp32 sums move a few Q8_1 codes per layer, each step of one code
-# moving its block by d/2) and 0.014 (fp16 mode) on this model over 10 steps.
-LOGIT_TOL = {"q8": 0.12, "f16": 0.03}
+# Teacher-forced logit bounds against the oracle in the matching arithmetic.
+#  "q8" (BASELINE config 3's int8 MMQ): f64 accumulation and f64 attention like the batch-1 path, so the only
+#  deviation left is the LM head's fp32 accumulation (~1e-7 relative); bound: north_star's 1e-3 relative to the
+#  largest |logit|, and the argmax must match wherever the oracle's top-2 margin is at least NEAR_TIE (measured
+#  deviation on these runs: 0, the fp32 logits are bit-equal).
+#  "f16" (the reference's own fp16 batched arithmetic, gemv_v2_source): fp16 activations and fp16-P attention
+#  round differently from the oracle's f64 values; measured largest deviation 0.014 -> bound 0.03, argmax checked
+#  above twice that.
+def logit_tol(act, ref):
+    return 1e-3 * float(np.abs(ref).max()) if act == "q8" else 0.03
+
+
+def token_margin(act):
+    return NEAR_TIE if act == "q8" else 0.06
 
 
 @pytest.mark.parametrize("act", ["f16", "q8"])
@@ -216,13 +226,12 @@ LOGIT_TOL = {"q8": 0.12, "f16": 0.03}
 def test_batched_greedy_matches_oracle(small, small_f16, B, act):
     """B independent prompts decoded together (paged KV, scattered pages) against the oracle in the matching
     arithmetic, teacher-forced: at every step each checked sequence is fed the oracle's token; its logits must
-    be within LOGIT_TOL of the oracle's, and its argmax must equal the oracle's wherever the oracle's top-2
-    margin exceeds twice that tolerance (below it, either token is a legitimate greedy choice)."""
+    be within logit_tol of the oracle's, and its argmax must equal the oracle's wherever the oracle's top-2
+    margin is at least token_margin (below it, either token is a legitimate greedy choice)."""
     import torch
     w, dm, om = small
     if act == "f16":
         om = small_f16
-    tol = LOGIT_TOL[act]
     rng = np.random.default_rng(B)
     prompts = rng.integers(0, CFG_S.V, (B, 6))
     bd = QB.BatchedDecoder(dm, B=B, max_ctx=256, page_seed=B, act=act, keep_logits=True)
@@ -243,9 +252,9 @@ def test_batched_greedy_matches_oracle(small, small_f16, B, act):
         for s_ in seqs:
             lg = ref[s_][t]
             dev_ = float(np.abs(got[s_] - lg).max())
-            assert dev_ < tol, f"B={B} seq {s_} step {t}: logits off by {dev_:.3g}"
+            assert dev_ <= logit_tol(act, lg), f"B={B} seq {s_} step {t}: logits off by {dev_:.3g}"
             top2 = np.partition(lg, -2)[-2:]
-            if top2[1] - top2[0] > 2 * tol:
+            if top2[1] - top2[0] >= token_margin(act):
                 assert int(toks[s_]) == int(np.argmax(lg)), f"B={B} seq {s_} step {t}"
             toks[s_] = int(np.argmax(lg))                 # teacher forcing
         if t < 9:

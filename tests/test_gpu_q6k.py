@@ -95,14 +95,13 @@ def test_mmq_q6k_logits(cuda, N, K, T):
 @pytest.mark.parametrize("B", [8, 32])
 def test_batched_decode_with_q6k_head(cuda, B):
     """BatchedDecoder with llama.cpp's Q6_K output.weight (int8 MMQ layers, Q6_K MFMA head), teacher-forced
-    against the oracle (oracle.model.LinearQ6K head): logits within the batched int8 mode's tolerance (0.12),
-    argmax equal wherever the oracle's margin exceeds twice that."""
+    against the oracle (oracle.model.LinearQ6K head): logits within the batched int8 mode's bound (1e-3 of the
+    largest |logit|), argmax equal wherever the oracle's margin is at least NEAR_TIE."""
     import torch
     from lab import qwen_batched as QB
     cfg = QM.Config(L=2, V=4096)
     w = QM.random_weights(cfg, seed=31)
-    # d = 2e-5: weights of std ~0.02 like the Q4_0 layers, so the logits have the magnitude the 0.12 bound
-    # (measured on the tied Q4_0 head) was calibrated for
+    # d = 2e-5: weights of std ~0.02 like the Q4_0 layers (logits of the magnitude of the tied Q4_0 head's)
     w["head_q6k"] = random_q6_k(cfg.V * cfg.H // 256, np.random.default_rng(32), d=0.00002)
     dm = QM.DeviceModel(w, cfg, maxlen=256)
     om = OM.Model(OM.Config(L=2, V=4096), w, maxlen=256)
@@ -121,9 +120,9 @@ def test_batched_decode_with_q6k_head(cuda, B):
         for s_ in seqs:
             lg = lgs[s_]
             dev = float(np.abs(got[s_] - lg).max())
-            assert dev < 0.12, f"B={B} seq {s_} step {t}: logits off by {dev:.3g}"
+            assert dev <= 1e-3 * float(np.abs(lg).max()), f"B={B} seq {s_} step {t}: logits off by {dev:.3g}"
             top2 = np.partition(lg, -2)[-2:]
-            if top2[1] - top2[0] > 0.24:
+            if top2[1] - top2[0] >= NEAR_TIE:
                 assert int(toks[s_]) == int(np.argmax(lg))
             toks[s_] = int(np.argmax(lg))
             lgs[s_] = om.logits(om.forward([int(toks[s_])], 5 + t, caches[s_]))[0]

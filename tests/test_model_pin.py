@@ -5,7 +5,9 @@ embed -> per layer [RMSNorm(ln1) -> QKV GEMV + bias -> RoPE(q, k) + K/V write ->
 O GEMV + residual -> RMSNorm(ln2) -> gate/up GEMV -> SwiGLU -> down GEMV + residual] -> RMSNorm(norm) ->
 tied head. It shares no code with oracle/: the Q4_0 decoder, the Q8_1 rounding points (the reference's
 QUANT_Q8 rule, lab/qwen_batched.py:1032-1033, with the fp16 stored scale), RMSNorm, the NeoX RoPE pairing
-(d, d + 64), softmax attention and SiLU are written here in torch from their definitions. A model with a
+(d, d + 64), softmax attention and SiLU are written here in torch from their definitions. Both activation
+modes are pinned: "q8" (Q8_1 layer inputs) and "f16" (the reference's batched arithmetic, gemv_v2_source,
+lab/qwen_batched.py:467-680: fp16 layer inputs times the fp16 weights d (q - 8), the LM head on Q8_1). A model with a
 swapped norm weight, a dropped bias or a misplaced residual gives logits that differ far beyond the
 tolerance (checked by the mutation cases at the end).
 """
@@ -39,20 +41,31 @@ def q8(x: torch.Tensor) -> torch.Tensor:
     return (q.to(torch.float64) * d.to(torch.float16).to(torch.float64)).reshape(x.shape)
 
 
+def f16(x: torch.Tensor) -> torch.Tensor:
+    """fp16 layer input: the fp32 activation rounded to fp16."""
+    return x.to(torch.float32).to(torch.float16).to(torch.float64)
+
+
+def w16(wq: torch.Tensor) -> torch.Tensor:
+    """The fp16 weight of the batched arithmetic: d (q - 8), an exact float64 product, rounded once to fp16."""
+    return wq.to(torch.float16).to(torch.float64)
+
+
 def rms(h, w, eps=1e-6):
     return h / torch.sqrt((h * h).mean(-1, keepdim=True) + eps) * torch.as_tensor(w, dtype=torch.float64)
 
 
 class Ref:
-    def __init__(self, w, maxlen=64, mutate=None):
+    def __init__(self, w, maxlen=64, mutate=None, act="q8"):
         self.w, self.mut = w, mutate or ""
+        self.a = q8 if act == "q8" else f16
         i = torch.arange(0, HD, 2, dtype=torch.float64) / HD
         ang = torch.arange(maxlen, dtype=torch.float64)[:, None] * (1e6 ** -i)[None]
         self.cos, self.sin = torch.cos(ang).to(torch.float32).double(), torch.sin(ang).to(torch.float32).double()
         self.E = dq4(w["embed"], V, H)
         self.L = []
         for L in w["layers"]:
-            self.L.append({k: dq4(L[k], *s) for k, s in
+            self.L.append({k: (dq4(L[k], *s) if act == "q8" else w16(dq4(L[k], *s))) for k, s in
                            (("wq", (NH * HD, H)), ("wk", (NKV * HD, H)), ("wv", (NKV * HD, H)), ("wo", (H, NH * HD)),
                             ("wg", (FFN, H)), ("wu", (FFN, H)), ("wd", (H, FFN)))})
         self.K = [torch.zeros(NKV, maxlen, HD, dtype=torch.float64) for _ in w["layers"]]
@@ -68,7 +81,7 @@ class Ref:
         h = self.E[tok][None].to(torch.float32).double()
         for i, (Lw, Ld) in enumerate(zip(self.w["layers"], self.L)):
             ln1, ln2 = (Lw["ln2"], Lw["ln1"]) if self.mut == "swap_norms" else (Lw["ln1"], Lw["ln2"])
-            x = q8(rms(h, ln1).to(torch.float32))
+            x = self.a(rms(h, ln1).to(torch.float32))
             bq = 0 if self.mut == "no_bias" else torch.as_tensor(Lw["bq"], dtype=torch.float64)
             q = x @ Ld["wq"].T + bq
             k = x @ Ld["wk"].T + torch.as_tensor(Lw["bk"], dtype=torch.float64)
@@ -81,11 +94,11 @@ class Ref:
                 kv = hh // (NH // NKV)
                 s = self.K[i][kv, :p + 1] @ q[hh] / math.sqrt(HD)
                 att[hh] = torch.softmax(s, 0) @ self.V[i][kv, :p + 1]
-            o = q8(att.reshape(1, -1).to(torch.float32)) @ Ld["wo"].T
+            o = self.a(att.reshape(1, -1).to(torch.float32)) @ Ld["wo"].T
             h = o if self.mut == "no_resid" else h + o
-            x = q8(rms(h, ln2).to(torch.float32))
+            x = self.a(rms(h, ln2).to(torch.float32))
             m = torch.nn.functional.silu(x @ Ld["wg"].T) * (x @ Ld["wu"].T)
-            h = h + q8(m.to(torch.float32)) @ Ld["wd"].T
+            h = h + self.a(m.to(torch.float32)) @ Ld["wd"].T
         x = q8(rms(h, self.w["norm"]).to(torch.float32))
         return (x @ self.E.T).to(torch.float32)[0]
 
@@ -95,8 +108,8 @@ def weights():
     return QM.random_weights(QM.Config(L=2, V=V), seed=31)
 
 
-def _oracle_logits(w, toks):
-    m = OM.Model(OM.Config(L=2, V=V), w, maxlen=64)
+def _oracle_logits(w, toks, act="q8"):
+    m = OM.Model(OM.Config(L=2, V=V), w, maxlen=64, act=act)
     cache = m.new_cache()
     out = []
     for p, t in enumerate(toks):
@@ -104,17 +117,18 @@ def _oracle_logits(w, toks):
     return np.stack(out)
 
 
-def _ref_logits(w, toks, mutate=None):
-    r = Ref(w, mutate=mutate)
+def _ref_logits(w, toks, mutate=None, act="q8"):
+    r = Ref(w, mutate=mutate, act=act)
     return np.stack([r.step(t, p).numpy() for p, t in enumerate(toks)])
 
 
 TOKS = [5, 900, 17, 333, 1023, 64]
 
 
-def test_model_matches_independent_forward(weights):
+@pytest.mark.parametrize("act", ["q8", "f16"])
+def test_model_matches_independent_forward(weights, act):
     """2 layers at full width, 6 decode positions: the oracle's logits equal the independent forward's."""
-    a, b = _oracle_logits(weights, TOKS), _ref_logits(weights, TOKS)
+    a, b = _oracle_logits(weights, TOKS, act), _ref_logits(weights, TOKS, act=act)
     err = np.abs(a - b).max() / np.abs(b).max()
     assert err < 1e-6, err
 
@@ -123,4 +137,11 @@ def test_model_matches_independent_forward(weights):
 def test_forward_detects_composition_mistakes(weights, mutate):
     """The comparison above is sensitive: each plausible composition mistake moves the logits by > 1e-3."""
     a, b = _oracle_logits(weights, TOKS[:3]), _ref_logits(weights, TOKS[:3], mutate)
+    assert np.abs(a - b).max() / np.abs(a).max() > 1e-3
+
+
+def test_forward_detects_activation_mode_mistake(weights):
+    """The two modes' rounding points are distinguishable: the "f16" oracle against the "q8" forward (Q8_1
+    inputs instead of fp16, unrounded weights) differs by > 1e-3."""
+    a, b = _oracle_logits(weights, TOKS[:3], "f16"), _ref_logits(weights, TOKS[:3], act="q8")
     assert np.abs(a - b).max() / np.abs(a).max() > 1e-3

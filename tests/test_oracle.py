@@ -282,6 +282,32 @@ def test_model_prefill_equals_decode():
     assert np.allclose(c1["V"][:, :, :5].astype(np.float32), c2["V"][:, :, :5].astype(np.float32), atol=2e-3)
 
 
+def test_model_decode_batch_equals_per_sequence():
+    """decode_batch (the S rows' GEMVs as one product) equals Model.forward run for each sequence alone, for
+    sequences at different positions; a mixed-up row/cache pairing (two caches swapped) fails it."""
+    from lab import qwen_model as QM      # the weight generator (input data), not code under test here
+    cfg = QM.Config(L=2, V=512, FFN=256, H=256, NH=4, NKV=2, HD=64)
+    w = QM.random_weights(cfg, seed=5)
+    ocfg = OM.Config(H=256, NH=4, NKV=2, HD=64, FFN=256, L=2, V=512)
+    m = OM.Model(ocfg, w, maxlen=64)
+    prompts = [[5, 17, 300], [2, 99, 7, 44, 1], [8]]
+    def setup():
+        caches = [m.new_cache() for _ in prompts]
+        for p, c in zip(prompts, caches):
+            m.forward(p, 0, c)
+        return caches
+    toks, pos = [11, 23, 400], [len(p) for p in prompts]
+    ca, cb = setup(), setup()
+    hb = m.decode_batch(toks, pos, ca)
+    for r in range(3):
+        hs = m.forward([toks[r]], pos[r], cb[r])[0]
+        assert np.allclose(hb[r], hs, rtol=1e-12, atol=1e-12)
+        assert np.array_equal(ca[r]["K"], cb[r]["K"]) and np.array_equal(ca[r]["V"], cb[r]["V"])
+    cc = setup()
+    hx = m.decode_batch(toks, pos, [cc[1], cc[0], cc[2]])
+    assert not np.allclose(hx[0], hb[0], rtol=1e-3)
+
+
 def test_q6_k_decode_matches_encoded_values():
     """Q6_K: chosen 6-bit values and scales, scattered into ql/qh bytes by an encoder written from the block
     definition, decode back exactly (and the three independent decoders agree)."""
