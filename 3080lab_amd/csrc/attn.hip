@@ -508,30 +508,23 @@ __global__ void __launch_bounds__(64) k_attn_merge(const AttnArgs a) {
 // A token whose context fits one split is finished here (Q8_1 oq/ods, fp32 o32 if asked); otherwise each
 // split writes its unnormalised (o[G][HD], M[G], L[G]) to part [T][nkv][nsp][G][HD + 2] (nsp =
 // ceil(max_chunks / SPG)) and k_attn_merge_f64 finishes the token in split order.
-// acc += bcast(q, lane i of each 16-lane row) * k_i for i = 0..15: v_fmac_f64 with a DPP row_newbcast source
-// (gfx950's 64-bit DPP), so a row-uniform f64 operand costs no broadcast instruction. s_nop 1: the two wait
-// states a DPP source needs after a VALU write of it.
-__device__ __forceinline__ void fma16_bcast(double& acc, double q, const double (&k)[16]) {
+// acc += bcast(q, lane OFF + i of each 16-lane row) * k_i for i = 0..7: v_fmac_f64 with a DPP row_newbcast
+// source (gfx950's 64-bit DPP), so a row-uniform f64 operand costs no broadcast instruction. s_nop 1: the two
+// wait states a DPP source needs after a VALU write of it.
+template <int OFF>
+__device__ __forceinline__ void fma8_bcast(double& acc, double q, const double (&k)[8]) {
   asm("s_nop 1\n\t"
-      "v_fmac_f64_dpp %0, %1, %2 row_newbcast:0 row_mask:0xf bank_mask:0xf\n\t"
-      "v_fmac_f64_dpp %0, %1, %3 row_newbcast:1 row_mask:0xf bank_mask:0xf\n\t"
-      "v_fmac_f64_dpp %0, %1, %4 row_newbcast:2 row_mask:0xf bank_mask:0xf\n\t"
-      "v_fmac_f64_dpp %0, %1, %5 row_newbcast:3 row_mask:0xf bank_mask:0xf\n\t"
-      "v_fmac_f64_dpp %0, %1, %6 row_newbcast:4 row_mask:0xf bank_mask:0xf\n\t"
-      "v_fmac_f64_dpp %0, %1, %7 row_newbcast:5 row_mask:0xf bank_mask:0xf\n\t"
-      "v_fmac_f64_dpp %0, %1, %8 row_newbcast:6 row_mask:0xf bank_mask:0xf\n\t"
-      "v_fmac_f64_dpp %0, %1, %9 row_newbcast:7 row_mask:0xf bank_mask:0xf\n\t"
-      "v_fmac_f64_dpp %0, %1, %10 row_newbcast:8 row_mask:0xf bank_mask:0xf\n\t"
-      "v_fmac_f64_dpp %0, %1, %11 row_newbcast:9 row_mask:0xf bank_mask:0xf\n\t"
-      "v_fmac_f64_dpp %0, %1, %12 row_newbcast:10 row_mask:0xf bank_mask:0xf\n\t"
-      "v_fmac_f64_dpp %0, %1, %13 row_newbcast:11 row_mask:0xf bank_mask:0xf\n\t"
-      "v_fmac_f64_dpp %0, %1, %14 row_newbcast:12 row_mask:0xf bank_mask:0xf\n\t"
-      "v_fmac_f64_dpp %0, %1, %15 row_newbcast:13 row_mask:0xf bank_mask:0xf\n\t"
-      "v_fmac_f64_dpp %0, %1, %16 row_newbcast:14 row_mask:0xf bank_mask:0xf\n\t"
-      "v_fmac_f64_dpp %0, %1, %17 row_newbcast:15 row_mask:0xf bank_mask:0xf"
+      "v_fmac_f64_dpp %0, %1, %2 row_newbcast:%10 row_mask:0xf bank_mask:0xf\n\t"
+      "v_fmac_f64_dpp %0, %1, %3 row_newbcast:%11 row_mask:0xf bank_mask:0xf\n\t"
+      "v_fmac_f64_dpp %0, %1, %4 row_newbcast:%12 row_mask:0xf bank_mask:0xf\n\t"
+      "v_fmac_f64_dpp %0, %1, %5 row_newbcast:%13 row_mask:0xf bank_mask:0xf\n\t"
+      "v_fmac_f64_dpp %0, %1, %6 row_newbcast:%14 row_mask:0xf bank_mask:0xf\n\t"
+      "v_fmac_f64_dpp %0, %1, %7 row_newbcast:%15 row_mask:0xf bank_mask:0xf\n\t"
+      "v_fmac_f64_dpp %0, %1, %8 row_newbcast:%16 row_mask:0xf bank_mask:0xf\n\t"
+      "v_fmac_f64_dpp %0, %1, %9 row_newbcast:%17 row_mask:0xf bank_mask:0xf"
       : "+v"(acc)
-      : "v"(q), "v"(k[0]), "v"(k[1]), "v"(k[2]), "v"(k[3]), "v"(k[4]), "v"(k[5]), "v"(k[6]), "v"(k[7]), "v"(k[8]),
-        "v"(k[9]), "v"(k[10]), "v"(k[11]), "v"(k[12]), "v"(k[13]), "v"(k[14]), "v"(k[15]));
+      : "v"(q), "v"(k[0]), "v"(k[1]), "v"(k[2]), "v"(k[3]), "v"(k[4]), "v"(k[5]), "v"(k[6]), "v"(k[7]),
+        "n"(OFF), "n"(OFF + 1), "n"(OFF + 2), "n"(OFF + 3), "n"(OFF + 4), "n"(OFF + 5), "n"(OFF + 6), "n"(OFF + 7));
 }
 // o[h][u], o[h + 1][u] += bcast(p[h], p[h + 1]: lane T of each row) * v_u (two heads of one P.V key)
 template <int T>
@@ -553,6 +546,7 @@ __device__ __forceinline__ void pv_key(double (&o)[G][2], const double (&pr)[G],
   const double v0 = (double)vf.x, v1 = (double)vf.y;
 #pragma unroll
   for (int h = 0; h < G; h += 2) fma_pv2<T>(o[h][0], o[h][1], o[h + 1][0], o[h + 1][1], pr[h], pr[h + 1], v0, v1);
+  __builtin_amdgcn_sched_barrier(0);                    // one key's conversions live at a time
 }
 template <int G, int... T>
 __device__ __forceinline__ void pv_keys(double (&o)[G][2], const double (&pr)[G], const unsigned (&vr)[16], int kg,
@@ -562,7 +556,7 @@ __device__ __forceinline__ void pv_keys(double (&o)[G][2], const double (&pr)[G]
 
 template <int G, int SPG>
 __global__ void __launch_bounds__(SPG * 256) k_attn_batch_f64(const AttnArgs a) {
-  static_assert(G % 2 == 0 && G <= 8 && G <= 4 * SPG, "heads per KV group");
+  static_assert(G % 2 == 0 && G <= 8, "heads per KV group");
   constexpr int KEYS = SPG * PAGE;
   __shared__ __align__(16) double sq[4][G][KEYS];      // score partials per dim quarter
   __shared__ __align__(16) double ps[KEYS][G];         // p per key (16-byte reads give two heads)
@@ -597,10 +591,6 @@ __global__ void __launch_bounds__(SPG * 256) k_attn_batch_f64(const AttnArgs a) 
       qd[h][0] = q[h * HD];
       qd[h][1] = q[h * HD + 16];
     }
-    // V operands of phase 3 (in flight during the scores): keys 4 t + l / 16, dims 32 dq + 2 (l % 16)
-#pragma unroll
-    for (int t = 0; t < 16; ++t)
-      vr[t] = ld_stream4(a.vcache + base + (size_t)(4 * t + kg) * HD + 32 * dq + 2 * dp);
   }
   // 1. scores of this wave's dim quarter
   if (live) {
@@ -611,31 +601,34 @@ __global__ void __launch_bounds__(SPG * 256) k_attn_batch_f64(const AttnArgs a) 
 #pragma unroll
     for (int h = 0; h < G; ++h) acc[h] = 0.0;
 #pragma unroll
-    for (int hf = 0; hf < 2; ++hf) {                    // 16 dims at a time (fewer live registers)
-      double kd[16];
+    for (int c = 0; c < 4; ++c) {                       // 8 dims at a time (fewer live registers)
+      double kd[8];
+      const __half2* k2 = (const __half2*)&kr[c];
 #pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        const __half2* k2 = (const __half2*)&kr[2 * hf + i];
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          const float2 kf = __half22float2(k2[u]);
-          kd[8 * i + 2 * u] = (double)kf.x;
-          kd[8 * i + 2 * u + 1] = (double)kf.y;
-        }
+      for (int u = 0; u < 4; ++u) {
+        const float2 kf = __half22float2(k2[u]);
+        kd[2 * u] = (double)kf.x;
+        kd[2 * u + 1] = (double)kf.y;
       }
 #pragma unroll
-      for (int h = 0; h < G; ++h) fma16_bcast(acc[h], qd[h][hf], kd);
+      for (int h = 0; h < G; ++h) {
+        if (c & 1) fma8_bcast<8>(acc[h], qd[h][c >> 1], kd);
+        else fma8_bcast<0>(acc[h], qd[h][c >> 1], kd);
+      }
     }
 #pragma unroll
     for (int h = 0; h < G; ++h) sq[dq][h][pg * PAGE + lane] = acc[h];
+    // V operands of phase 3, in flight during the softmax: keys 4 t + l / 16, dims 32 dq + 2 (l % 16)
+#pragma unroll
+    for (int t = 0; t < 16; ++t)
+      vr[t] = ld_stream4(a.vcache + base + (size_t)(4 * t + kg) * HD + 32 * dq + 2 * dp);
   } else {
 #pragma unroll
     for (int h = 0; h < G; ++h) sq[dq][h][pg * PAGE + lane] = 0.0;
   }
   __syncthreads();
-  // 2. softmax: wave h < G takes head h over the split's keys (SPG per lane)
-  if (wv < G) {
-    const int h = wv;
+  // 2. softmax: wave w takes heads w, w + 4 SPG, ... over the split's keys (SPG per lane)
+  for (int h = wv; h < G; h += 4 * SPG) {
     double sv[SPG], m = -INFINITY;
 #pragma unroll
     for (int g = 0; g < SPG; ++g) {
