@@ -141,7 +141,7 @@ class Kern:
     def launch(self, grid=None, block=None, args=()):
         if getattr(self.spec, "ref", ""):
             from .refcall import LAUNCHERS
-            return LAUNCHERS[self.spec.ref](self.spec, list(args))
+            return LAUNCHERS[self.spec.ref](self.spec, list(args), grid)
         conv = []
         for a in args:
             if hasattr(a, "data_ptr"):

@@ -29,11 +29,29 @@ from .qwen_model import FIX_SCALE, PAGE, Config, DeviceModel
 
 # reference generator names (lab/qwen_batched.py) -> the C-ABI entry points that replace them
 def gemv_v2_source(WM=1, WK=1, MT=1, B=8, epi="store", PF=1, KS=1, ACC16=False) -> KernelSpec:
-    """Batched decode GEMV (lab/qwen_batched.py:467-641) -> q355_gemm_q4_0_f16 (the same fp16 weight
-    dequantization, fp16 MFMA); epi store / logits / resid (fixed-point residual) / swiglu (fp16 out) /
-    biasf (-> resid_fix + q355_qkv_finish)."""
+    """Batched decode GEMV (lab/qwen_batched.py:467-641) -> the fp16-weight products of the same arithmetic (fp16
+    weight dequantization, fp16 MFMA, fp32 accumulation into the fixed-point residual). Launched with the
+    reference's (W, S, X, Y, aux, N, K, ws, cnt) (lab/refcall.py:launch_gemv_v2): biasf on the qkv buffer ->
+    q355_gemm_f16_qkv_rope at the ATTN launch; resid on the attention output -> the O product (split merge in
+    its staging up to 16 tokens); swiglu -> q355_gemm_q4_0_f16 epi 8; resid -> epi 6. The tile shape (WM, WK,
+    MT, KS, PF, ACC16) is the library's choice per shape and batch, so those arguments have no counterpart."""
+    if epi not in ("store", "logits", "resid", "biasf", "swiglu"):
+        raise ValueError(f"epilogue {epi!r}: store, logits, resid, biasf or swiglu")
     code = {"store": 0, "logits": 5, "resid": 6, "biasf": 6, "swiglu": 8}[epi]
-    return KernelSpec("q355_gemm_q4_0_f16", {"epi": code})
+    return KernelSpec("q355_gemm_q4_0_f16", {"epi": code, "epi_name": epi, "B": int(B)}, ref="gemv_v2")
+
+
+def head_v2_source(WM=8, WK=1, MT=1, B=8, PF=1) -> KernelSpec:
+    """Batched LM head (lab/qwen_batched.py:681-833), launched with (*head, x, logits, V, H): the final RMSNorm's
+    Q8_1 times the head on int8 MFMA (the tied Q4_0 matrix, or llama.cpp's Q6_K output.weight) -> fp32 logits and
+    argmax partials (lab/refcall.py:launch_head_v2)."""
+    return KernelSpec("q355_mmq_q4_0_q8_1", {"B": int(B)}, ref="head_v2")
+
+
+def batchify(spec: KernelSpec, lines: str = "") -> KernelSpec:
+    """The reference's batchify (scripts/qwen_batched_decode.py:74-86) edits kernel source to offset each pointer by
+    blockIdx.y; the library's entry points take the batch size, which Kern.launch reads from grid.y."""
+    return KernelSpec(spec.symbol, {**spec.params, "batched": True}, spec.ref)
 
 
 def gemm_q4i8_ms_source(WM=4, WN=2, MT=2, NT=4, epi="store", KB=4, NSTG=2, MINB=1, ABL=None) -> KernelSpec:
@@ -50,6 +68,12 @@ QUANT_Q8 = KernelSpec("q355_quant_q8_1")
 def rmsnorm_q8_source(H: int) -> KernelSpec:
     """RMSNorm + Q8 quantizer (lab/qwen_batched.py:1044-1091) over the fixed-point residual stream."""
     return KernelSpec("q355_rmsnorm_fix_q8_1", {"H": H})
+
+
+def pack_q6_mma(*head):
+    """The reference repacks the Q6_K head into mma fragment order (lab/qwen_batched.py:439-466); the library's
+    Q6_K planes (lab.gguf.tile_q6_k) already are its MFMA operand order, so this is the identity."""
+    return head
 
 
 def pack_q4_i8(W, S):

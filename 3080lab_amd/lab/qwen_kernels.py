@@ -39,8 +39,11 @@ def gemv_source(S_: int = 1, epi: str = "store", quant: str = "q8_1", G: int = 1
         if epi not in _EPI_CODE:
             raise ValueError(f"epilogue {epi!r} not in {EPILOGUES}")
         return KernelSpec("q355_gemv_q4_0_bf16", {"epi": _EPI_CODE[epi]})
-    if quant != "q8_1":
-        raise ValueError(f"quant={quant!r}: this build's GEMV consumes Q8_1 (or bf16) activations")
+    # "g32f16" is how scripts/qwen_gguf.py:126 names GGUF's Q4_0 weights (groups of 32, fp16 scale): the
+    # library's weight format, with Q8_1 activations
+    if quant not in ("q8_1", "g32f16"):
+        raise ValueError(f"quant={quant!r}: this build's GEMV takes Q4_0 weights ('g32f16') with Q8_1 (or bf16) "
+                         "activations")
     if epi in ("biasf_kv", "qkv"):          # the fused QKV entry point, called in its own argument order
         return KernelSpec("q355_qkv_rope_kv")
     if epi not in EPILOGUES:

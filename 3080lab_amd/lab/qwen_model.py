@@ -135,10 +135,15 @@ class Q6KMat:
         self.hi = torch.from_numpy(hi.reshape(-1)).to(device)
         self.sc = torch.from_numpy(sc.reshape(-1).view(np.uint8)).to(device)
         self.d = torch.from_numpy(d.reshape(-1).view(np.int16)).to(device)
+        from .refcall import register
+        register(self.lo, self)           # the head pointer of reference-order launches resolves to this matrix
 
     @property
     def nbytes(self):
         return self.lo.numel() + self.hi.numel() + self.sc.numel() + 2 * self.d.numel()
+
+    def data_ptr(self):
+        return self.lo.data_ptr()
 
 
 def weights_from_gguf(path) -> tuple:
