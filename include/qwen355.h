@@ -144,8 +144,9 @@ int q355_attn_decode(const void* q, const void* kcache, const void* vcache, cons
  * reference. The fp32 split partials go to a fixed device array inside the library (one per GPU, held until the
  * process ends) instead of a caller buffer; it calls no hipMalloc/hipFree. Limit:
  * T * nh * ceil(max_chunks / 4) * 130 * 4 bytes <= q355_attn_decode_noalloc_max_bytes() (4 MiB), else
- * Q355_EINVAL. Calls that overlap on one GPU share the array and race. Outputs and the other arguments as
- * q355_attn_decode; GQA group nh/nkv <= 16. */
+ * Q355_EINVAL. Every call on one GPU shares the array: serialise all calls on a device through one stream
+ * (graphs or decoders replayed on different streams race and give wrong outputs with no error). Outputs and the
+ * other arguments as q355_attn_decode; GQA group nh/nkv <= 16. */
 int64_t q355_attn_decode_noalloc_max_bytes(void);
 int q355_attn_decode_noalloc(const void* q, const void* kcache, const void* vcache, const int32_t* pos,
                              const int32_t* block_table, int bt_stride, int nh, int nkv, int max_chunks,

@@ -73,6 +73,7 @@ def test_quant_q8_1_bitexact(cuda):
     x[0, :32] = 0.0                                   # d = 0 block
     x[1, 32:64] = np.float32(0.5) * np.arange(32)     # exact halves after scaling
     x[2, 64:96] = -x[2, 64:96] * 1e-30                # tiny values (fp16 d underflow)
+    x[2, 96:128] = x[2, 96:128] * 1e-4                # small values (fp16-subnormal d)
     xq = torch.zeros(T, K, dtype=torch.int8, device=cuda)
     xds = torch.zeros(T, K // 32, 2, dtype=torch.float16, device=cuda)
     call("q355_quant_q8_1", ptr(to_dev(x)), ptr(xq), ptr(xds), T, K)

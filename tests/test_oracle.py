@@ -122,6 +122,19 @@ def test_q8_1_known_blocks():
         assert s[0, b] == np.float16(np.float32(float(d32)) * np.float32(sum(want)))
 
 
+def test_q8_1_fp16_subnormal_scale():
+    """A block of small values (amax 1e-4): d = amax / 127 = 7.9e-7 is an fp16 subnormal. The codes follow the
+    reference's QUANT_Q8 (divisor = the fp32 d, so the amax element is +-127); the stored scale is BASELINE's fp16
+    d, here a subnormal whose relative error (~1e-2) exceeds fp16's 2^-11 -- where this build's products differ
+    from the reference's (which keeps the fp32 d). The GPU quantizer writes the same bytes (test_gpu_kernels)."""
+    x = (np.linspace(-1.0, 1.0, 32, dtype=np.float32) * np.float32(1e-4))[None]
+    q, d, _ = OQ.quantize_q8_1(x)
+    want, d32 = _q8_expect(x[0])
+    assert q[0].tolist() == want and abs(q[0]).max() == 127
+    assert 0 < float(d[0, 0]) < 6.1e-5                              # fp16 subnormal
+    assert abs(float(d[0, 0]) - float(d32)) > float(d32) * 2.0 ** -11
+
+
 def test_q8_1_bruteforce_random():
     rng = np.random.default_rng(5)
     x = (rng.standard_normal((3, 96)) * rng.choice([1e-3, 1.0, 40.0], (3, 1))).astype(np.float32)

@@ -44,6 +44,12 @@ def test_attn_decode_noalloc_matches_allocating_entry(cuda):
         assert torch.equal(o32_a.view(torch.int32), o32_b.view(torch.int32)), T
     # beyond the fixed scratch: rejected before any launch
     # (100 tokens x 12 heads x 8 splits x 520 B = 4.99 MB > 4 MiB; the size check precedes every launch)
+    # (its own buffers sized for 100 tokens, so the call stays in bounds whatever order the checks run in)
+    T = 100
+    qT = torch.zeros(T, nh * 128, dtype=torch.float16, device=cuda)
+    posT = torch.zeros(T, dtype=torch.int32, device=cuda)
+    btT = torch.zeros(T, mc, dtype=torch.int32, device=cuda)
+    oq_c, ods_c, o32_c = _outs(torch, cuda, T, nh)
     with pytest.raises(HipError, match="scratch"):
-        call("q355_attn_decode_noalloc", ptr(q), ptr(kc), ptr(vc), ptr(pos), ptr(bt), mc, nh, nkv, mc, scale,
-             ptr(oq_b), ptr(ods_b), ptr(o32_b), 100)
+        call("q355_attn_decode_noalloc", ptr(qT), ptr(kc), ptr(vc), ptr(posT), ptr(btT), mc, nh, nkv, mc, scale,
+             ptr(oq_c), ptr(ods_c), ptr(o32_c), T)
