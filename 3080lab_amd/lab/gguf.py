@@ -146,13 +146,14 @@ def q4_0_blocks(b: np.ndarray):
 
 
 def q6_k_blocks(b: np.ndarray):
-    """-> q int8 [nblk, 256] in [-32, 31], s float32 [nblk, 16] (= d * scale of each 16 weights)."""
+    """Q6_K super-blocks (210 bytes each) decoded: the 256 signed 6-bit values of every block, and one float32
+    factor per 16 of them, the super-block scale times that group's int8 scale."""
     q, sc, d = _q6_k_fields(b)
     return q, d.astype(np.float32)[:, None] * sc.astype(np.float32)
 
 
 def q6_k_parts(b: np.ndarray):
-    """-> q int8 [nblk, 256] in [-32, 31], sc int8 [nblk, 16], d fp16 [nblk] (Q6_K's raw fields)."""
+    """The same values, with the scales left as stored: 16 int8 group scales and the fp16 super-block scale."""
     return _q6_k_fields(b)
 
 
