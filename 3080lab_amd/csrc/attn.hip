@@ -555,7 +555,7 @@ __device__ __forceinline__ void pv_keys(double (&o)[G][2], const double (&pr)[G]
 }
 
 template <int G, int SPG>
-__global__ void __launch_bounds__(SPG * 256) k_attn_batch_f64(const AttnArgs a) {
+__global__ void __launch_bounds__(SPG * 256) __attribute__((amdgpu_waves_per_eu(6))) k_attn_batch_f64(const AttnArgs a) {
   static_assert(G % 2 == 0 && G <= 8, "heads per KV group");
   constexpr int KEYS = SPG * PAGE;
   __shared__ __align__(16) double sq[4][G][KEYS];      // score partials per dim quarter
