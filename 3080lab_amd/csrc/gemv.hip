@@ -674,20 +674,31 @@ __global__ void __launch_bounds__(256) k_rmsnorm_fix_q8_1(const long long* __res
   const int tok = blockIdx.x;
   const int g = threadIdx.x;                       // 8 consecutive values per thread, H / 8 <= 256
   const bool act = g < H / 8;
+  // every load first (h as four 16-byte pieces, the norm weights beside them): one memory latency
+  longlong2 hr[4] = {};
+  float4 w0 = make_float4(0.f, 0.f, 0.f, 0.f), w1 = w0;
+  if (act) {
+    const longlong2* hp = (const longlong2*)(h + (size_t)tok * H + 8 * g);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) hr[u] = hp[u];
+    w0 = ((const float4*)w)[2 * g];
+    w1 = ((const float4*)w)[2 * g + 1];
+  }
   double hv[8];
   double ss = 0.0;
 #pragma unroll
-  for (int u = 0; u < 8; ++u) {
-    hv[u] = act ? from_fix(h[(size_t)tok * H + 8 * g + u]) : 0.0;
-    ss = fma(hv[u], hv[u], ss);
+  for (int u = 0; u < 4; ++u) {
+    hv[2 * u] = from_fix(hr[u].x);
+    hv[2 * u + 1] = from_fix(hr[u].y);
   }
+#pragma unroll
+  for (int u = 0; u < 8; ++u) ss = fma(hv[u], hv[u], ss);
   ss = wave_sum_d(ss);
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
   __syncthreads();
   const double r = 1.0 / sqrt((red[0] + red[1] + red[2] + red[3]) / (double)H + eps);
   float x[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   if (act) {
-    const float4 w0 = ((const float4*)w)[2 * g], w1 = ((const float4*)w)[2 * g + 1];
     const float wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
 #pragma unroll
     for (int u = 0; u < 8; ++u) x[u] = (float)(hv[u] * r * (double)wv[u]);
@@ -708,19 +719,30 @@ __global__ void __launch_bounds__(256) k_rmsnorm_fix_f16(const long long* __rest
   const int tok = blockIdx.x;
   const int g = threadIdx.x;                       // 8 consecutive values per thread, H / 8 <= 256
   const bool act = g < H / 8;
+  // every load first (h as four 16-byte pieces, the norm weights beside them): one memory latency
+  longlong2 hr[4] = {};
+  float4 w0 = make_float4(0.f, 0.f, 0.f, 0.f), w1 = w0;
+  if (act) {
+    const longlong2* hp = (const longlong2*)(h + (size_t)tok * H + 8 * g);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) hr[u] = hp[u];
+    w0 = ((const float4*)w)[2 * g];
+    w1 = ((const float4*)w)[2 * g + 1];
+  }
   double hv[8];
   double ss = 0.0;
 #pragma unroll
-  for (int u = 0; u < 8; ++u) {
-    hv[u] = act ? from_fix(h[(size_t)tok * H + 8 * g + u]) : 0.0;
-    ss = fma(hv[u], hv[u], ss);
+  for (int u = 0; u < 4; ++u) {
+    hv[2 * u] = from_fix(hr[u].x);
+    hv[2 * u + 1] = from_fix(hr[u].y);
   }
+#pragma unroll
+  for (int u = 0; u < 8; ++u) ss = fma(hv[u], hv[u], ss);
   ss = wave_sum_d(ss);
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
   __syncthreads();
   const double r = 1.0 / sqrt((red[0] + red[1] + red[2] + red[3]) / (double)H + eps);
   if (act) {
-    const float4 w0 = ((const float4*)w)[2 * g], w1 = ((const float4*)w)[2 * g + 1];
     const float wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
     __half o[8];
 #pragma unroll
