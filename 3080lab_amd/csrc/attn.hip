@@ -566,13 +566,30 @@ __global__ void __launch_bounds__(SPG * 256) __attribute__((amdgpu_waves_per_eu(
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int pg = wv >> 2, dq = wv & 3;
   const int nsp = (a.max_chunks + SPG - 1) / SPG;
-  // split-major order over the grid (nkv * nsp, T): the first splits of every token are dispatched first
-  const int wid = blockIdx.x + gridDim.x * blockIdx.y, per = gridDim.y * a.nkv;
-  const int sp = wid / per, j = (wid % per) / a.nkv, kvh = wid % a.nkv;
+  const int wid = blockIdx.x + gridDim.x * blockIdx.y;
+  int sp, j, kvh, pgid, pos;
+  if (a.work) {
+    // the step's live items, packed at the front of the grid: one load gives the item, its position and its
+    // page ids, so the K loads follow after one memory latency, and the empty slots at the end exit at once
+    static_assert(SPG <= 2, "a work item carries two page ids");
+    const int4 it = a.work[wid];
+    if (it.x < 0) return;                               // uniform per workgroup
+    j = it.x & 0xffff;
+    kvh = (it.x >> 16) & 0xff;
+    sp = it.x >> 24;
+    pos = it.y;
+    pgid = pg == 0 ? it.z : it.w;
+  } else {
+    // split-major order over the grid (nkv * nsp, T): the first splits of every token are dispatched first
+    const int per = gridDim.y * a.nkv;
+    sp = wid / per;
+    j = (wid % per) / a.nkv;
+    kvh = wid % a.nkv;
+    // the page id does not depend on the position: both loads are in flight together
+    pgid = a.block_table[(size_t)j * a.bt_stride + min(sp * SPG + pg, a.max_chunks - 1)];
+    pos = a.pos[j];
+  }
   const int c = sp * SPG + pg;
-  // the page id does not depend on the position: both loads are in flight together
-  const int pgid = a.block_table[(size_t)j * a.bt_stride + min(c, a.max_chunks - 1)];
-  const int pos = a.pos[j];
   const int nch = pos / PAGE + 1, nsplit = (nch + SPG - 1) / SPG;
   if (sp >= nsplit) return;                             // uniform per workgroup
   const bool live = c < nch;                            // uniform per wave; page 0 of the split is always live
@@ -716,6 +733,48 @@ __global__ void __launch_bounds__(SPG * 256) __attribute__((amdgpu_waves_per_eu(
 #pragma unroll
   for (int i = 0; i < 8; i += 2) *(double2*)(P + 8 * dg + i) = make_double2(od[i], od[i + 1]);
   if (dg == 0) *(double2*)(P + HD) = make_double2(xm[h], xl[h]);
+}
+
+// The live work items of k_attn_batch_f64 for one step (one workgroup of up to 1024 threads, thread t = token t):
+// split-major, then token, then KV head -- the order of the plain grid with the dead splits left out -- followed
+// by empty items (-1) up to cap, the grid size. Each item carries the token's position and the page ids of the
+// split's (up to) two pages. The positions do not change within a step, so one list serves all layers.
+template <int SPG>
+__global__ void __launch_bounds__(1024) k_attn_worklist(const int* __restrict__ pos, const int* __restrict__ bt,
+                                                        int bt_stride, int T, int nkv, int max_chunks,
+                                                        int4* __restrict__ work, int cap) {
+  __shared__ int wsum[16];
+  const int t = threadIdx.x, lane = t & 63, wv = t >> 6, nw = (int)(blockDim.x >> 6);
+  const int nsp = (max_chunks + SPG - 1) / SPG;
+  int ns = 0, p = 0;
+  if (t < T) {
+    p = pos[t];
+    ns = min(nsp, (p / PAGE + 1 + SPG - 1) / SPG);
+  }
+  int base = 0;
+  for (int sp = 0; sp < nsp; ++sp) {
+    const bool live = sp < ns;
+    const unsigned long long m = __ballot(live);
+    const int below = __popcll(m & ((1ull << lane) - 1ull));
+    if (lane == 0) wsum[wv] = __popcll(m);
+    __syncthreads();
+    int off = 0, tot = 0;
+    for (int w = 0; w < nw; ++w) {
+      const int cw = wsum[w];
+      off += w < wv ? cw : 0;
+      tot += cw;
+    }
+    __syncthreads();                                    // wsum is rewritten next split
+    if (live) {
+      const int* row = bt + (size_t)t * bt_stride;
+      int4 it = make_int4(t | (sp << 24), p, row[min(sp * SPG, max_chunks - 1)],
+                          row[min(sp * SPG + 1, max_chunks - 1)]);
+      const size_t idx = (size_t)(base + off + below) * nkv;
+      for (int k = 0; k < nkv; ++k, it.x += 1 << 16) work[idx + k] = it;
+    }
+    base += tot;
+  }
+  for (int i = base * nkv + t; i < cap; i += blockDim.x) work[i] = make_int4(-1, 0, 0, 0);
 }
 
 // Merge of k_attn_batch_f64's split partials, f64, in split order: o = sum_s e^(M_s - M) o_s / sum_s

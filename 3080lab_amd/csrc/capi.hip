@@ -665,10 +665,9 @@ static int launch_attn_f64(const AttnArgs& a, int T, hipStream_t s) {
   return launched("attn_merge_f64");
 }
 
-extern "C" int q355_attn_decode_f64(const double* q64, const void* kcache, const void* vcache, const int32_t* pos,
-                                    const int32_t* block_table, int bt_stride, int nh, int nkv, int max_chunks,
-                                    double scale, double* part, int8_t* oq, void* ods, float* o32, int T,
-                                    void* stream) {
+static int attn_decode_f64(const double* q64, const void* kcache, const void* vcache, const int32_t* pos,
+                           const int32_t* block_table, int bt_stride, int nh, int nkv, int max_chunks, double scale,
+                           double* part, int8_t* oq, void* ods, float* o32, int T, const void* work, void* stream) {
   REQUIRE(q64 && kcache && vcache && pos && block_table && part && oq && ods, "attn_decode_f64: null pointer");
   REQUIRE(nh > 0 && nkv > 0 && nh % nkv == 0, "attn_decode_f64: nh=%d nkv=%d", nh, nkv);
   REQUIRE(nh / nkv == 6 || nh / nkv == 4 || nh / nkv == 8, "attn_decode_f64: GQA group %d (4, 6 or 8 supported)",
@@ -680,12 +679,50 @@ extern "C" int q355_attn_decode_f64(const double* q64, const void* kcache, const
   a.q64 = q64; a.kcache = (const __half*)kcache; a.vcache = (const __half*)vcache;
   a.pos = pos; a.block_table = block_table; a.bt_stride = bt_stride; a.nh = nh; a.nkv = nkv;
   a.max_chunks = max_chunks; a.scale = scale; a.part = part; a.oq = oq; a.ods = (half2*)ods; a.o32 = o32;
+  a.work = (const int4*)work;
   hipStream_t s = (hipStream_t)stream;
   switch (nh / nkv) {
     case 4: return launch_attn_f64<4>(a, T, s);
     case 6: return launch_attn_f64<6>(a, T, s);
     default: return launch_attn_f64<8>(a, T, s);
   }
+}
+
+extern "C" int q355_attn_decode_f64(const double* q64, const void* kcache, const void* vcache, const int32_t* pos,
+                                    const int32_t* block_table, int bt_stride, int nh, int nkv, int max_chunks,
+                                    double scale, double* part, int8_t* oq, void* ods, float* o32, int T,
+                                    void* stream) {
+  return attn_decode_f64(q64, kcache, vcache, pos, block_table, bt_stride, nh, nkv, max_chunks, scale, part, oq, ods,
+                         o32, T, nullptr, stream);
+}
+
+// The step's live-item list of q355_attn_decode_f64_wl: 16 B per item, nkv * ceil(max_chunks / 2) * T items.
+extern "C" int64_t q355_attn_f64_worklist_bytes(int T, int nkv, int max_chunks) {
+  return (int64_t)16 * nkv * ((max_chunks + ATTN64_SPG - 1) / ATTN64_SPG) * T;
+}
+
+extern "C" int q355_attn_f64_worklist(const int32_t* pos, const int32_t* block_table, int bt_stride, int nkv,
+                                      int max_chunks, int T, void* work, void* stream) {
+  REQUIRE(pos && block_table && work, "attn_f64_worklist: null pointer");
+  REQUIRE(nkv > 0 && nkv <= 255 && max_chunks > 0 && max_chunks <= bt_stride && max_chunks <= 64,
+          "attn_f64_worklist: nkv=%d max_chunks=%d bt_stride=%d", nkv, max_chunks, bt_stride);
+  REQUIRE(T > 0 && T <= 1024, "attn_f64_worklist: T=%d (1..1024)", T);
+  const int cap = nkv * ((max_chunks + ATTN64_SPG - 1) / ATTN64_SPG) * T;
+  hipLaunchKernelGGL(k_attn_worklist<ATTN64_SPG>, dim3(1), dim3(1024), 0, (hipStream_t)stream, pos, block_table,
+                     bt_stride, T, nkv, max_chunks, (int4*)work, cap);
+  return launched("attn_f64_worklist");
+}
+
+// q355_attn_decode_f64 over the step's live-item list (q355_attn_f64_worklist, built from the same pos,
+// block_table, nkv, max_chunks and T after the positions were last changed): bit-identical outputs.
+extern "C" int q355_attn_decode_f64_wl(const double* q64, const void* kcache, const void* vcache, const int32_t* pos,
+                                       const int32_t* block_table, int bt_stride, int nh, int nkv, int max_chunks,
+                                       double scale, double* part, int8_t* oq, void* ods, float* o32, int T,
+                                       const void* work, void* stream) {
+  REQUIRE(work, "attn_decode_f64_wl: null work list");
+  REQUIRE(T <= 1024, "attn_decode_f64_wl: T=%d (the work list holds up to 1024 tokens)", T);
+  return attn_decode_f64(q64, kcache, vcache, pos, block_table, bt_stride, nh, nkv, max_chunks, scale, part, oq, ods,
+                         o32, T, work, stream);
 }
 
 extern "C" int q355_attn_decode_partials_f16(const void* q, const void* kcache, const void* vcache, const int32_t* pos,

@@ -135,6 +135,9 @@ struct AttnArgs {
   half2* ods;                  // [T][nh*HD/32]
   float* o32;                  // optional fp32 output [T][nh*HD] (tests), may be null
   __half* oh;                  // fp16 merged output [T][nh*HD] (the fp16 batched path), instead of oq/ods
+  // k_attn_batch_f64: optional list of the live (token, KV head, split) items of this step, one per workgroup in
+  // grid order (k_attn_worklist): {token | kvh << 16 | split << 24 (-1: none), pos, page ids of the split's 2 pages}
+  const int4* work;
 };
 
 template <int T, int NT, int NW, int KPL, int PRO, int EPI, int WF>

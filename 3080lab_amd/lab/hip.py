@@ -64,12 +64,16 @@ _SIGS = {
     "q355_mmq_qkv_rope": [_P, _P, c_int, c_int, _P, _P, c_int, _P, _P, _P, _P, _P, c_int, c_int, _P, _P, _P, _P,
                           c_int, c_int, _P],
     "q355_attn_decode_f64": [_P, _P, _P, _P, _P, c_int, c_int, c_int, c_int, c_double, _P, _P, _P, _P, c_int, _P],
+    "q355_attn_decode_f64_wl": [_P, _P, _P, _P, _P, c_int, c_int, c_int, c_int, c_double, _P, _P, _P, _P, c_int, _P,
+                                _P],
+    "q355_attn_f64_worklist_bytes": [c_int, c_int, c_int],
+    "q355_attn_f64_worklist": [_P, _P, c_int, c_int, c_int, c_int, _P, _P],
     "q355_gemm_f16_qkv_rope": [_P, _P, c_int, c_int, _P, c_int, _P, _P, _P, _P, _P, c_int, c_int, _P, _P, _P,
                                c_int, c_int, _P],
 }
 # entry points returning something other than an int status
 _VALUE_FUNCS = {"q355_attn_decode_noalloc_max_bytes", "q355_head_nparts", "q355_mmq_nparts", "q355_mega_ws_bytes", "q355_mega_layer_bytes",
-                "q355_attn_prefill_ws_bytes"}
+                "q355_attn_prefill_ws_bytes", "q355_attn_f64_worklist_bytes"}
 
 _lib = None
 
@@ -92,7 +96,7 @@ def lib():
         for name, args in _SIGS.items():
             f = getattr(L, name)
             f.argtypes = args
-            f.restype = ctypes.c_int64 if name.endswith(("_ws_bytes", "_max_bytes")) else c_int
+            f.restype = ctypes.c_int64 if name.endswith(("_ws_bytes", "_max_bytes", "_worklist_bytes")) else c_int
         _lib = L
     return _lib
 

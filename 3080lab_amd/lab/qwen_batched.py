@@ -140,6 +140,9 @@ class BatchedDecoder:
         self.tok = torch.zeros(B, dtype=torch.int32, device=dev)
         self.pos = torch.zeros(B, dtype=torch.int32, device=dev)
         self.scale = 1.0 / math.sqrt(c.HD)
+        # the step's live (token, KV head, split) items of the f64 attention, rebuilt by layer 0 of every step
+        nb = call("q355_attn_f64_worklist_bytes", B, c.NKV, self.max_chunks)
+        self.work = torch.zeros(nb // 4, dtype=torch.int32, device=dev) if B <= 1024 else None
 
     def h_f32(self):
         import torch
@@ -197,9 +200,16 @@ class BatchedDecoder:
              ptr(m.cos), ptr(m.sin), ptr(self.pos), ptr(self.block_table), self.max_chunks, 1, ptr(self.kc[i]),
              ptr(self.vc[i]), ptr(self.q), ptr(self.q64), c.NH, c.NKV)
         # f64 attention (the batch-1 arithmetic), split merge in f64 -> Q8_1
-        call("q355_attn_decode_f64", ptr(self.q64), ptr(self.kc[i]), ptr(self.vc[i]), ptr(self.pos),
-             ptr(self.block_table), self.max_chunks, c.NH, c.NKV, self.max_chunks, self.scale, ptr(self.part),
-             ptr(self.aq), ptr(self.ads), None, B)
+        args = (ptr(self.q64), ptr(self.kc[i]), ptr(self.vc[i]), ptr(self.pos), ptr(self.block_table),
+                self.max_chunks, c.NH, c.NKV, self.max_chunks, self.scale, ptr(self.part), ptr(self.aq),
+                ptr(self.ads), None, B)
+        if self.work is None:
+            call("q355_attn_decode_f64", *args)
+        else:
+            if i == 0:                       # positions are fixed for the rest of the step
+                call("q355_attn_f64_worklist", ptr(self.pos), ptr(self.block_table), self.max_chunks, c.NKV,
+                     self.max_chunks, B, ptr(self.work))
+            call("q355_attn_decode_f64_wl", *args, ptr(self.work))
         self._mmq(L["o"], self.aq, self.ads, 6, yfix=self.h)
         self._norm(L["ln2"])
         if B <= 16:

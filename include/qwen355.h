@@ -284,6 +284,19 @@ int q355_attn_decode_f64(const double* q64, const void* kcache, const void* vcac
                          const int32_t* block_table, int bt_stride, int nh, int nkv, int max_chunks, double scale,
                          double* part, int8_t* oq, void* ods, float* o32, int T, void* stream);
 
+/* The same attention over a list of the step's live (token, KV head, two-page split) items, built by
+ * q355_attn_f64_worklist from pos / block_table after the positions last changed (once per step: every layer
+ * reuses it). The list puts the live work first in grid order and carries each item's position and page ids,
+ * so no workgroup waits on a dead split or a dependent block-table load. Bit-identical to q355_attn_decode_f64.
+ * work: q355_attn_f64_worklist_bytes(T, nkv, max_chunks) bytes; T <= 1024.
+ * No counterpart in the reference: ATTN4 (lab/qwen_kernels.py:517-605) launches one block per (token, head). */
+int64_t q355_attn_f64_worklist_bytes(int T, int nkv, int max_chunks);
+int q355_attn_f64_worklist(const int32_t* pos, const int32_t* block_table, int bt_stride, int nkv, int max_chunks,
+                           int T, void* work, void* stream);
+int q355_attn_decode_f64_wl(const double* q64, const void* kcache, const void* vcache, const int32_t* pos,
+                            const int32_t* block_table, int bt_stride, int nh, int nkv, int max_chunks, double scale,
+                            double* part, int8_t* oq, void* ods, float* o32, int T, const void* work, void* stream);
+
 /* Causal GQA prefill attention (fp16 MFMA, fp32 accumulation) for one sequence: queries q fp16
  * [P][nh*128] at positions pos0 .. pos0 + P - 1 attend to keys 0 .. their own position in the paged cache
  * (block_table = the sequence's page ids, >= (pos0 + P - 1) / 64 + 1 of them; K/V of every attended

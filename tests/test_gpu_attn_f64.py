@@ -37,6 +37,23 @@ def _run(cuda, nh, nkv, pos, mc, seed):
          ptr(ods), ptr(o32), T)
     torch.cuda.synchronize()
     got, gq, gds = o32.cpu().numpy(), oq.cpu().numpy(), ods.cpu().numpy()
+    # the same launch over the live-item list: bit-identical
+    work = torch.zeros(call("q355_attn_f64_worklist_bytes", T, nkv, mc) // 4, dtype=torch.int32, device=cuda) - 7
+    call("q355_attn_f64_worklist", ptr(keep[3]), ptr(keep[4]), mc, nkv, mc, T, ptr(work))
+    for t in (part, oq, ods, o32):
+        t.zero_()
+    call("q355_attn_decode_f64_wl", *[ptr(t) for t in keep], mc, nh, nkv, mc, 1 / math.sqrt(128), ptr(part), ptr(oq),
+         ptr(ods), ptr(o32), T, ptr(work))
+    torch.cuda.synchronize()
+    assert np.array_equal(o32.cpu().numpy().view(np.uint32), got.view(np.uint32))
+    assert np.array_equal(oq.cpu().numpy(), gq) and np.array_equal(ods.cpu().numpy().view(np.uint16), gds.view(np.uint16))
+    w = work.cpu().numpy().reshape(-1, 4)
+    nsp = (mc + 1) // 2
+    live = [(j, k, sp) for sp in range(nsp) for j in range(T) for k in range(nkv) if sp <= int(pos[j]) // 128]
+    assert len(w) == nkv * nsp * T and (w[len(live):, 0] == -1).all()
+    assert [(x & 0xffff, (x >> 16) & 0xff, x >> 24) for x in w[:len(live), 0]] == live
+    assert all(w[i, 1] == pos[j] and w[i, 2] == bt[j, min(2 * sp, mc - 1)] and w[i, 3] == bt[j, min(2 * sp + 1, mc - 1)]
+               for i, (j, _, sp) in enumerate(live))
     for j in range(T):
         K = np.concatenate([kc[bt[j, p]] for p in range(mc)], axis=1)
         V = np.concatenate([vc[bt[j, p]] for p in range(mc)], axis=1)
