@@ -492,6 +492,70 @@ __global__ void __launch_bounds__(64) k_attn_merge(const AttnArgs a) {
   }
 }
 
+// Merge of k_attn_batch_f64's split partials, f64, in split order: o = sum_s e^(M_s - M) o_s / sum_s
+// e^(M_s - M) L_s (M = max_s M_s). Workgroup (KV head, token), thread (head t / 64, dims 2 (t % 64), + 1):
+// the splits' (M, L) and two values are loaded in batches of up to SB splits (one memory latency each; a
+// later batch rescales the earlier sums to its maximum), then Q8_1 per 16-lane row (one 32-value block).
+// COH: the partials were written by other workgroups of the same launch (device-scope stores), so they are read
+// with device-scope loads; otherwise by an earlier launch, read with ordinary loads.
+template <int G, int SPG, int SB, bool COH>
+__device__ __forceinline__ void merge_f64(const AttnArgs& a, const int kvh, const int j, const int nsplit,
+                                          const int tid) {
+  const int nsp = (a.max_chunks + SPG - 1) / SPG;
+  const int h = tid >> 6, dp = tid & 63;
+  const double* P0 = a.part + (((size_t)j * a.nkv + kvh) * nsp * G + h) * (HD + 2);
+  const size_t st = (size_t)G * (HD + 2);
+  const Coh16 coh(P0, (unsigned)(nsp * st * 8));      // P0 is uniform per wave (one head per wave)
+  auto ld2 = [&](size_t e) {                          // the double2 at P0 + e
+    return COH ? __builtin_bit_cast(double2, coh.ld((unsigned)(e * 8))) : *(const double2*)(P0 + e);
+  };
+  double M = -INFINITY, o0 = 0.0, o1 = 0.0, L = 0.0;
+  for (int s0 = 0; s0 < nsplit; s0 += SB) {             // one batch (one memory latency) up to SB splits
+    double2 ml[SB], x[SB];
+#pragma unroll
+    for (int s = 0; s < SB; ++s)
+      if (s0 + s < nsplit) {
+        ml[s] = ld2((s0 + s) * st + HD);
+        x[s] = ld2((s0 + s) * st + 2 * dp);
+      }
+    double Mb = M;
+#pragma unroll
+    for (int s = 0; s < SB; ++s)
+      if (s0 + s < nsplit) Mb = fmax(Mb, ml[s].x);
+    if (s0) {                                           // rescale the earlier batches to the new maximum
+      const double r = exp(M - Mb);
+      o0 *= r; o1 *= r; L *= r;
+    }
+    M = Mb;
+#pragma unroll
+    for (int s = 0; s < SB; ++s)
+      if (s0 + s < nsplit) {
+        const double f = exp(ml[s].x - M);
+        L = fma(f, ml[s].y, L);
+        o0 = fma(f, x[s].x, o0);
+        o1 = fma(f, x[s].y, o1);
+      }
+  }
+  const float v0 = (float)(o0 / L), v1 = (float)(o1 / L);
+  const size_t n = (size_t)a.nh * HD, e = (size_t)j * n + (size_t)(kvh * G + h) * HD + 2 * dp;
+  if (a.o32) *(float2*)(a.o32 + e) = make_float2(v0, v1);
+  // Q8_1 of the row's 32 values (16 lanes x 2), the rule of q8_code
+  float amax = fmaxf(fabsf(v0), fabsf(v1));
+  amax = fmaxf(amax, dpp<DPP_XOR1>(amax));
+  amax = fmaxf(amax, dpp<DPP_XOR2>(amax));
+  amax = fmaxf(amax, dpp<DPP_HALF_MIRROR>(amax));
+  amax = fmaxf(amax, dpp<DPP_MIRROR>(amax));
+  const float d32 = q8_scale(amax);
+  const int q0 = q8_code(v0, d32), q1 = q8_code(v1, d32);
+  int sq = q0 + q1;
+  sq += dpp<DPP_XOR1>(sq);
+  sq += dpp<DPP_XOR2>(sq);
+  sq += dpp<DPP_HALF_MIRROR>(sq);
+  sq += dpp<DPP_MIRROR>(sq);
+  *(short*)(a.oq + e) = (short)((q0 & 255) | ((q1 & 255) << 8));
+  if ((dp & 15) == 0) a.ods[e / 32] = __halves2half2(__float2half_rn(d32), q8_s16(d32, sq));
+}
+
 // ---------------------------------------------------------------------------------------------
 // f64 batched decode attention (the int8 batched path): the arithmetic of the batch-1 kernel above -- f64
 // scores, softmax and P.V from fp16 q/K/V widened exactly -- at the throughput of a batch. Workgroup
@@ -713,129 +777,91 @@ __global__ void __launch_bounds__(SPG * 256) __attribute__((amdgpu_waves_per_eu(
   __syncthreads();
   // 4. thread (head h, dims 8 dg .. 8 dg + 7): the split's live pages in page order
   const int t = threadIdx.x;
-  if (t >= G * 16) return;                              // whole quads (Q8_1 blocks) stay together
-  const int h = t >> 4, dg = t & 15;
-  const int nlive = min(SPG, nch - sp * SPG);
-  double od[8];
+  if (t < G * 16) {                                     // whole quads (Q8_1 blocks) stay together
+    const int h = t >> 4, dg = t & 15;
+    const int nlive = min(SPG, nch - sp * SPG);
+    double od[8];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) od[i] = po[0][h][8 * dg + i];
-  for (int g = 1; g < nlive; ++g)
+    for (int i = 0; i < 8; ++i) od[i] = po[0][h][8 * dg + i];
+    for (int g = 1; g < nlive; ++g)
 #pragma unroll
-    for (int i = 0; i < 8; ++i) od[i] += po[g][h][8 * dg + i];
-  if (nsplit == 1) {
-    float of[8];
+      for (int i = 0; i < 8; ++i) od[i] += po[g][h][8 * dg + i];
+    if (nsplit == 1) {
+      float of[8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) of[i] = (float)(od[i] / xl[h]);
-    attn_out8(a, j, kvh * G + h, dg, of, true);
-    return;
+      for (int i = 0; i < 8; ++i) of[i] = (float)(od[i] / xl[h]);
+      attn_out8(a, j, kvh * G + h, dg, of, true);
+    } else if (a.arrivals) {
+      // device-scope stores (written through to the memory every XCD reads): the merging workgroup may run on
+      // another XCD and reads them with device-scope loads, so no cache writeback or invalidate is needed
+      const Coh16 P(a.part + (((size_t)j * a.nkv + kvh) * nsp + sp) * G * (HD + 2), G * (HD + 2) * 8);
+      const unsigned e = (unsigned)(h * (HD + 2) + 8 * dg) * 8;
+#pragma unroll
+      for (int i = 0; i < 8; i += 2) P.st16(e + i * 8, __builtin_bit_cast(int4, make_double2(od[i], od[i + 1])));
+      if (dg == 0) P.st16((unsigned)(h * (HD + 2) + HD) * 8, __builtin_bit_cast(int4, make_double2(xm[h], xl[h])));
+    } else {                                            // merged by a later launch
+      double* P = a.part + ((((size_t)j * a.nkv + kvh) * nsp + sp) * G + h) * (HD + 2);
+#pragma unroll
+      for (int i = 0; i < 8; i += 2) *(double2*)(P + 8 * dg + i) = make_double2(od[i], od[i + 1]);
+      if (dg == 0) *(double2*)(P + HD) = make_double2(xm[h], xl[h]);
+    }
   }
-  double* P = a.part + ((((size_t)j * a.nkv + kvh) * nsp + sp) * G + h) * (HD + 2);
-#pragma unroll
-  for (int i = 0; i < 8; i += 2) *(double2*)(P + 8 * dg + i) = make_double2(od[i], od[i + 1]);
-  if (dg == 0) *(double2*)(P + HD) = make_double2(xm[h], xl[h]);
+  if (nsplit == 1 || !a.arrivals) return;             // uniform per workgroup
+  // 5. the last split of this (token, KV head) to finish merges all of them (no separate merge launch): every
+  // thread's partial stores are acknowledged before the workgroup counts itself, so the last to count finds
+  // every split's partials; it resets the counter for the next launch
+  __shared__ int last;
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (t == 0) {
+    int* cnt = a.arrivals + (size_t)j * a.nkv + kvh;
+    last = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == nsplit - 1;
+    if (last) stc(cnt, 0);
+  }
+  __syncthreads();
+  if (!last) return;
+  if (t < G * 64) merge_f64<G, SPG, 4, true>(a, kvh, j, nsplit, t);   // 4 splits per load batch: VGPR budget
 }
 
-// The live work items of k_attn_batch_f64 for one step (one workgroup of up to 1024 threads, thread t = token t):
+// The live work items of k_attn_batch_f64 for one step, built by one wave (T <= 64 tokens, lane t = token t):
 // split-major, then token, then KV head -- the order of the plain grid with the dead splits left out -- followed
 // by empty items (-1) up to cap, the grid size. Each item carries the token's position and the page ids of the
-// split's (up to) two pages. The positions do not change within a step, so one list serves all layers.
+// split's (up to) two pages. Item index of (t, sp) = the live (token, split) pairs of earlier splits + the live
+// tokens before t in split sp, from one ballot per split (no barriers). The positions do not change within a
+// step, so one list serves all layers.
 template <int SPG>
-__global__ void __launch_bounds__(1024) k_attn_worklist(const int* __restrict__ pos, const int* __restrict__ bt,
-                                                        int bt_stride, int T, int nkv, int max_chunks,
-                                                        int4* __restrict__ work, int cap) {
-  __shared__ int wsum[16];
-  const int t = threadIdx.x, lane = t & 63, wv = t >> 6, nw = (int)(blockDim.x >> 6);
+__global__ void __launch_bounds__(64) k_attn_worklist(const int* __restrict__ pos, const int* __restrict__ bt,
+                                                      int bt_stride, int T, int nkv, int max_chunks,
+                                                      int4* __restrict__ work, int cap) {
+  const int t = threadIdx.x;
   const int nsp = (max_chunks + SPG - 1) / SPG;
   int ns = 0, p = 0;
   if (t < T) {
     p = pos[t];
     ns = min(nsp, (p / PAGE + 1 + SPG - 1) / SPG);
   }
+  const int* row = bt + (size_t)min(t, T - 1) * bt_stride;
   int base = 0;
   for (int sp = 0; sp < nsp; ++sp) {
-    const bool live = sp < ns;
-    const unsigned long long m = __ballot(live);
-    const int below = __popcll(m & ((1ull << lane) - 1ull));
-    if (lane == 0) wsum[wv] = __popcll(m);
-    __syncthreads();
-    int off = 0, tot = 0;
-    for (int w = 0; w < nw; ++w) {
-      const int cw = wsum[w];
-      off += w < wv ? cw : 0;
-      tot += cw;
-    }
-    __syncthreads();                                    // wsum is rewritten next split
-    if (live) {
-      const int* row = bt + (size_t)t * bt_stride;
-      int4 it = make_int4(t | (sp << 24), p, row[min(sp * SPG, max_chunks - 1)],
-                          row[min(sp * SPG + 1, max_chunks - 1)]);
-      const size_t idx = (size_t)(base + off + below) * nkv;
+    const unsigned long long m = __ballot(sp < ns);
+    if (m == 0ull) break;                               // no token has this split, nor any later one
+    if (sp < ns) {
+      int4 it = make_int4(t | (sp << 24), p, row[min(sp * SPG, max_chunks - 1)], row[min(sp * SPG + 1, max_chunks - 1)]);
+      const size_t idx = (size_t)(base + __popcll(m & ((1ull << t) - 1ull))) * nkv;
       for (int k = 0; k < nkv; ++k, it.x += 1 << 16) work[idx + k] = it;
     }
-    base += tot;
+    base += __popcll(m);
   }
-  for (int i = base * nkv + t; i < cap; i += blockDim.x) work[i] = make_int4(-1, 0, 0, 0);
+  for (int i = base * nkv + t; i < cap; i += 64) work[i] = make_int4(-1, 0, 0, 0);
 }
 
-// Merge of k_attn_batch_f64's split partials, f64, in split order: o = sum_s e^(M_s - M) o_s / sum_s
-// e^(M_s - M) L_s (M = max_s M_s). Workgroup (KV head, token), thread (head t / 64, dims 2 (t % 64), + 1):
-// the splits' (M, L) and two values are loaded in batches of up to 20 splits (one memory latency each; a
-// later batch rescales the earlier sums to its maximum), then Q8_1 per 16-lane row (one 32-value block).
+// The merge as its own launch: workgroup (KV head, token).
 template <int G, int SPG>
 __global__ void __launch_bounds__(G * 64) k_attn_merge_f64(const AttnArgs a) {
-  constexpr int SB = 20;                                // splits per load batch (2 KB of context per split)
-  const int nsp = (a.max_chunks + SPG - 1) / SPG;
   const int kvh = blockIdx.x, j = blockIdx.y;
   const int nsplit = (a.pos[j] / PAGE + 1 + SPG - 1) / SPG;
   if (nsplit == 1) return;                              // finished by the attention kernel
-  const int h = threadIdx.x >> 6, dp = threadIdx.x & 63;
-  const double* P0 = a.part + (((size_t)j * a.nkv + kvh) * nsp * G + h) * (HD + 2);
-  const size_t st = (size_t)G * (HD + 2);
-  double M = -INFINITY, o0 = 0.0, o1 = 0.0, L = 0.0;
-  for (int s0 = 0; s0 < nsplit; s0 += SB) {             // one batch (one memory latency) up to SB splits
-    double2 ml[SB], x[SB];
-#pragma unroll
-    for (int s = 0; s < SB; ++s)
-      if (s0 + s < nsplit) {
-        ml[s] = *(const double2*)(P0 + (s0 + s) * st + HD);
-        x[s] = *(const double2*)(P0 + (s0 + s) * st + 2 * dp);
-      }
-    double Mb = M;
-#pragma unroll
-    for (int s = 0; s < SB; ++s)
-      if (s0 + s < nsplit) Mb = fmax(Mb, ml[s].x);
-    if (s0) {                                           // rescale the earlier batches to the new maximum
-      const double r = exp(M - Mb);
-      o0 *= r; o1 *= r; L *= r;
-    }
-    M = Mb;
-#pragma unroll
-    for (int s = 0; s < SB; ++s)
-      if (s0 + s < nsplit) {
-        const double f = exp(ml[s].x - M);
-        L = fma(f, ml[s].y, L);
-        o0 = fma(f, x[s].x, o0);
-        o1 = fma(f, x[s].y, o1);
-      }
-  }
-  const float v0 = (float)(o0 / L), v1 = (float)(o1 / L);
-  const size_t n = (size_t)a.nh * HD, e = (size_t)j * n + (size_t)(kvh * G + h) * HD + 2 * dp;
-  if (a.o32) *(float2*)(a.o32 + e) = make_float2(v0, v1);
-  // Q8_1 of the row's 32 values (16 lanes x 2), the rule of q8_code
-  float amax = fmaxf(fabsf(v0), fabsf(v1));
-  amax = fmaxf(amax, dpp<DPP_XOR1>(amax));
-  amax = fmaxf(amax, dpp<DPP_XOR2>(amax));
-  amax = fmaxf(amax, dpp<DPP_HALF_MIRROR>(amax));
-  amax = fmaxf(amax, dpp<DPP_MIRROR>(amax));
-  const float d32 = q8_scale(amax);
-  const int q0 = q8_code(v0, d32), q1 = q8_code(v1, d32);
-  int sq = q0 + q1;
-  sq += dpp<DPP_XOR1>(sq);
-  sq += dpp<DPP_XOR2>(sq);
-  sq += dpp<DPP_HALF_MIRROR>(sq);
-  sq += dpp<DPP_MIRROR>(sq);
-  *(short*)(a.oq + e) = (short)((q0 & 255) | ((q1 & 255) << 8));
-  if ((dp & 15) == 0) a.ods[e / 32] = __halves2half2(__float2half_rn(d32), q8_s16(d32, sq));
+  merge_f64<G, SPG, 20, false>(a, kvh, j, nsplit, threadIdx.x);   // 20 splits (2 KB of context each) per load batch
 }
 
 }  // namespace q355

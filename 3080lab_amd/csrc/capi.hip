@@ -654,13 +654,14 @@ extern "C" int q355_attn_decode_partials(const void* q, const void* kcache, cons
 // Batched decode attention of the int8 path in f64 (k_attn_batch_f64, 4 pages per split) + the f64 split merge
 // -> Q8_1 oq/ods (and fp32 o32 if asked). q64: the f64 queries the QKV epilogue writes.
 constexpr int ATTN64_SPG = 2;                         // pages per split (4 waves per page)
+constexpr int ATTN64_FUSED_MERGE_T = 16;              // work-list launches of up to this many tokens merge in-kernel
 
 template <int G>
 static int launch_attn_f64(const AttnArgs& a, int T, hipStream_t s) {
   const int nsp = (a.max_chunks + ATTN64_SPG - 1) / ATTN64_SPG;
   hipLaunchKernelGGL((k_attn_batch_f64<G, ATTN64_SPG>), dim3(a.nkv * nsp, T), dim3(ATTN64_SPG * 256), 0, s, a);
   if (int e = launched("attn_decode_f64")) return e;
-  if (nsp == 1) return Q355_OK;                         // every token fits one split: finished above
+  if (nsp == 1 || a.arrivals) return Q355_OK;          // every token fits one split, or merged by its last split
   hipLaunchKernelGGL((k_attn_merge_f64<G, ATTN64_SPG>), dim3(a.nkv, T), dim3(G * 64), 0, s, a);
   return launched("attn_merge_f64");
 }
@@ -680,6 +681,11 @@ static int attn_decode_f64(const double* q64, const void* kcache, const void* vc
   a.pos = pos; a.block_table = block_table; a.bt_stride = bt_stride; a.nh = nh; a.nkv = nkv;
   a.max_chunks = max_chunks; a.scale = scale; a.part = part; a.oq = oq; a.ods = (half2*)ods; a.o32 = o32;
   a.work = (const int4*)work;
+  // the arrival counters follow the items in the work buffer. Up to 16 tokens the last split of each (token, KV
+  // head) merges it (B = 8: 1.567 -> 1.533 ms per step); at 32 the merging workgroups' 4-split load rounds
+  // outlast the separate merge launch (2.39 -> 2.44 ms), so that keeps it
+  if (work && T <= ATTN64_FUSED_MERGE_T)
+    a.arrivals = (int*)((char*)work + (size_t)16 * a.nkv * ((max_chunks + ATTN64_SPG - 1) / ATTN64_SPG) * T);
   hipStream_t s = (hipStream_t)stream;
   switch (nh / nkv) {
     case 4: return launch_attn_f64<4>(a, T, s);
@@ -696,9 +702,10 @@ extern "C" int q355_attn_decode_f64(const double* q64, const void* kcache, const
                          o32, T, nullptr, stream);
 }
 
-// The step's live-item list of q355_attn_decode_f64_wl: 16 B per item, nkv * ceil(max_chunks / 2) * T items.
+// The step's live-item list of q355_attn_decode_f64_wl: 16 B per item, nkv * ceil(max_chunks / 2) * T items,
+// then one int arrival counter per (token, KV head).
 extern "C" int64_t q355_attn_f64_worklist_bytes(int T, int nkv, int max_chunks) {
-  return (int64_t)16 * nkv * ((max_chunks + ATTN64_SPG - 1) / ATTN64_SPG) * T;
+  return (int64_t)16 * nkv * ((max_chunks + ATTN64_SPG - 1) / ATTN64_SPG) * T + (int64_t)4 * T * nkv;
 }
 
 extern "C" int q355_attn_f64_worklist(const int32_t* pos, const int32_t* block_table, int bt_stride, int nkv,
@@ -706,9 +713,9 @@ extern "C" int q355_attn_f64_worklist(const int32_t* pos, const int32_t* block_t
   REQUIRE(pos && block_table && work, "attn_f64_worklist: null pointer");
   REQUIRE(nkv > 0 && nkv <= 255 && max_chunks > 0 && max_chunks <= bt_stride && max_chunks <= 64,
           "attn_f64_worklist: nkv=%d max_chunks=%d bt_stride=%d", nkv, max_chunks, bt_stride);
-  REQUIRE(T > 0 && T <= 1024, "attn_f64_worklist: T=%d (1..1024)", T);
+  REQUIRE(T > 0 && T <= 64, "attn_f64_worklist: T=%d (1..64)", T);
   const int cap = nkv * ((max_chunks + ATTN64_SPG - 1) / ATTN64_SPG) * T;
-  hipLaunchKernelGGL(k_attn_worklist<ATTN64_SPG>, dim3(1), dim3(1024), 0, (hipStream_t)stream, pos, block_table,
+  hipLaunchKernelGGL(k_attn_worklist<ATTN64_SPG>, dim3(1), dim3(64), 0, (hipStream_t)stream, pos, block_table,
                      bt_stride, T, nkv, max_chunks, (int4*)work, cap);
   return launched("attn_f64_worklist");
 }
@@ -720,7 +727,7 @@ extern "C" int q355_attn_decode_f64_wl(const double* q64, const void* kcache, co
                                        double scale, double* part, int8_t* oq, void* ods, float* o32, int T,
                                        const void* work, void* stream) {
   REQUIRE(work, "attn_decode_f64_wl: null work list");
-  REQUIRE(T <= 1024, "attn_decode_f64_wl: T=%d (the work list holds up to 1024 tokens)", T);
+  REQUIRE(T <= 64, "attn_decode_f64_wl: T=%d (the work list holds up to 64 tokens)", T);
   return attn_decode_f64(q64, kcache, vcache, pos, block_table, bt_stride, nh, nkv, max_chunks, scale, part, oq, ods,
                          o32, T, work, stream);
 }

@@ -333,4 +333,34 @@ __device__ __forceinline__ T ldc(const T* p) { return __hip_atomic_load(p, __ATO
 template <typename T>
 __device__ __forceinline__ void stc(T* p, T v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
 
+
+// 16-byte device-scope loads (buffer loads with the sc1 policy, as the relaxed agent-scope atomic loads use):
+// coherent with other CUs' device-scope stores, four times the width of ldc, ordinary wait-count tracking
+// The base address must be the same in every lane of the wave (it is moved to scalar registers; a per-lane
+// base would make the compiler loop over the distinct values one load at a time).
+struct Coh16 {
+  __amdgpu_buffer_rsrc_t r;
+  __device__ __forceinline__ static void* uniform(const void* p) {
+    const unsigned long long v = (unsigned long long)p;
+    const unsigned lo = __builtin_amdgcn_readfirstlane((unsigned)v), hi = __builtin_amdgcn_readfirstlane((unsigned)(v >> 32));
+    return (void*)(((unsigned long long)hi << 32) | lo);
+  }
+  __device__ __forceinline__ Coh16(const void* p, unsigned bytes)
+      : r(__builtin_amdgcn_make_buffer_rsrc(uniform(p), 0, (int)bytes, 0x00020000)) {}
+  __device__ __forceinline__ int4 ld(unsigned byte_off) const {
+    return __builtin_bit_cast(int4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)byte_off, 0, 16));
+  }
+  __device__ __forceinline__ unsigned ld4(unsigned byte_off) const {
+    return __builtin_amdgcn_raw_buffer_load_b32(r, (int)byte_off, 0, 16);
+  }
+  // 2- and 16-byte device-scope stores (the sc1 policy of the relaxed agent-scope atomic stores)
+  __device__ __forceinline__ void st2(unsigned byte_off, unsigned short v) const {
+    __builtin_amdgcn_raw_buffer_store_b16(v, r, (int)byte_off, 0, 16);
+  }
+  __device__ __forceinline__ void st16(unsigned byte_off, int4 v) const {
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(__attribute__((ext_vector_type(4))) unsigned, v), r,
+                                           (int)byte_off, 0, 16);
+  }
+};
+
 }  // namespace q355

@@ -106,31 +106,6 @@ __device__ __forceinline__ MegaWs mega_ws(char* p, int max_chunks, int L) {
 
 __device__ __forceinline__ bool seq_reached(unsigned v, unsigned seq) { return (int)(v - seq) >= 0; }
 
-// 16-byte device-scope loads (buffer loads with the sc1 policy, as the relaxed agent-scope atomic loads use):
-// coherent with other CUs' device-scope stores, four times the width of ldc, ordinary wait-count tracking
-// The base address must be the same in every lane of the wave (it is moved to scalar registers; a per-lane
-// base would make the compiler loop over the distinct values one load at a time).
-struct Coh16 {
-  __amdgpu_buffer_rsrc_t r;
-  __device__ __forceinline__ static void* uniform(const void* p) {
-    const unsigned long long v = (unsigned long long)p;
-    const unsigned lo = __builtin_amdgcn_readfirstlane((unsigned)v), hi = __builtin_amdgcn_readfirstlane((unsigned)(v >> 32));
-    return (void*)(((unsigned long long)hi << 32) | lo);
-  }
-  __device__ __forceinline__ Coh16(const void* p, unsigned bytes)
-      : r(__builtin_amdgcn_make_buffer_rsrc(uniform(p), 0, (int)bytes, 0x00020000)) {}
-  __device__ __forceinline__ int4 ld(unsigned byte_off) const {
-    return __builtin_bit_cast(int4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)byte_off, 0, 16));
-  }
-  __device__ __forceinline__ unsigned ld4(unsigned byte_off) const {
-    return __builtin_amdgcn_raw_buffer_load_b32(r, (int)byte_off, 0, 16);
-  }
-  // 2-byte device-scope store (the sc1 policy of the relaxed agent-scope atomic stores)
-  __device__ __forceinline__ void st2(unsigned byte_off, unsigned short v) const {
-    __builtin_amdgcn_raw_buffer_store_b16(v, r, (int)byte_off, 0, 16);
-  }
-};
-
 // ---------------------------------------------------------------------------------------------
 // Synchronisation.
 struct MgSync {

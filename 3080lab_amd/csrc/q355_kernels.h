@@ -138,6 +138,9 @@ struct AttnArgs {
   // k_attn_batch_f64: optional list of the live (token, KV head, split) items of this step, one per workgroup in
   // grid order (k_attn_worklist): {token | kvh << 16 | split << 24 (-1: none), pos, page ids of the split's 2 pages}
   const int4* work;
+  // with work: one arrival counter per (token, KV head) [T][nkv], zero before the first launch (they reset
+  // themselves): the last split to finish merges the token's splits itself (no k_attn_merge_f64 launch)
+  int* arrivals;
 };
 
 template <int T, int NT, int NW, int KPL, int PRO, int EPI, int WF>

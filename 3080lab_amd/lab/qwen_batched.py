@@ -142,7 +142,7 @@ class BatchedDecoder:
         self.scale = 1.0 / math.sqrt(c.HD)
         # the step's live (token, KV head, split) items of the f64 attention, rebuilt by layer 0 of every step
         nb = call("q355_attn_f64_worklist_bytes", B, c.NKV, self.max_chunks)
-        self.work = torch.zeros(nb // 4, dtype=torch.int32, device=dev) if B <= 1024 else None
+        self.work = torch.zeros(nb // 4, dtype=torch.int32, device=dev) if B <= 64 else None
 
     def h_f32(self):
         import torch

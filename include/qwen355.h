@@ -287,8 +287,11 @@ int q355_attn_decode_f64(const double* q64, const void* kcache, const void* vcac
 /* The same attention over a list of the step's live (token, KV head, two-page split) items, built by
  * q355_attn_f64_worklist from pos / block_table after the positions last changed (once per step: every layer
  * reuses it). The list puts the live work first in grid order and carries each item's position and page ids,
- * so no workgroup waits on a dead split or a dependent block-table load. Bit-identical to q355_attn_decode_f64.
- * work: q355_attn_f64_worklist_bytes(T, nkv, max_chunks) bytes; T <= 1024.
+ * so no workgroup waits on a dead split or a dependent block-table load. Up to 16 tokens the last split of each
+ * (token, KV head) to finish merges that token's splits itself (arrival counters at the end of the work buffer),
+ * so there is no merge launch. Bit-identical to q355_attn_decode_f64.
+ * work: q355_attn_f64_worklist_bytes(T, nkv, max_chunks) bytes, zero-filled once before its first use (the
+ * counters reset themselves; concurrent launches on one work buffer race); T <= 64 (decode batches).
  * No counterpart in the reference: ATTN4 (lab/qwen_kernels.py:517-605) launches one block per (token, head). */
 int64_t q355_attn_f64_worklist_bytes(int T, int nkv, int max_chunks);
 int q355_attn_f64_worklist(const int32_t* pos, const int32_t* block_table, int bt_stride, int nkv, int max_chunks,

@@ -38,17 +38,23 @@ def _run(cuda, nh, nkv, pos, mc, seed):
     torch.cuda.synchronize()
     got, gq, gds = o32.cpu().numpy(), oq.cpu().numpy(), ods.cpu().numpy()
     # the same launch over the live-item list: bit-identical
-    work = torch.zeros(call("q355_attn_f64_worklist_bytes", T, nkv, mc) // 4, dtype=torch.int32, device=cuda) - 7
+    nsp = (mc + 1) // 2
+    work = torch.zeros(call("q355_attn_f64_worklist_bytes", T, nkv, mc) // 4, dtype=torch.int32, device=cuda)
+    assert work.numel() == nkv * nsp * T * 4 + T * nkv          # the items, then the arrival counters
+    work[:nkv * nsp * T * 4] = -7                               # every item slot is rewritten
     call("q355_attn_f64_worklist", ptr(keep[3]), ptr(keep[4]), mc, nkv, mc, T, ptr(work))
     for t in (part, oq, ods, o32):
         t.zero_()
-    call("q355_attn_decode_f64_wl", *[ptr(t) for t in keep], mc, nh, nkv, mc, 1 / math.sqrt(128), ptr(part), ptr(oq),
-         ptr(ods), ptr(o32), T, ptr(work))
-    torch.cuda.synchronize()
-    assert np.array_equal(o32.cpu().numpy().view(np.uint32), got.view(np.uint32))
-    assert np.array_equal(oq.cpu().numpy(), gq) and np.array_equal(ods.cpu().numpy().view(np.uint16), gds.view(np.uint16))
-    w = work.cpu().numpy().reshape(-1, 4)
-    nsp = (mc + 1) // 2
+    for rep in range(2):                # up to 16 tokens the merge by the last split: its counters reset themselves
+        call("q355_attn_decode_f64_wl", *[ptr(t) for t in keep], mc, nh, nkv, mc, 1 / math.sqrt(128), ptr(part),
+             ptr(oq), ptr(ods), ptr(o32), T, ptr(work))
+        torch.cuda.synchronize()
+        assert np.array_equal(o32.cpu().numpy().view(np.uint32), got.view(np.uint32)), rep
+        assert np.array_equal(oq.cpu().numpy(), gq), rep
+        assert np.array_equal(ods.cpu().numpy().view(np.uint16), gds.view(np.uint16)), rep
+        assert int(work[nkv * nsp * T * 4:].abs().sum()) == 0
+        o32.zero_()
+    w = work[:nkv * nsp * T * 4].cpu().numpy().reshape(-1, 4)
     live = [(j, k, sp) for sp in range(nsp) for j in range(T) for k in range(nkv) if sp <= int(pos[j]) // 128]
     assert len(w) == nkv * nsp * T and (w[len(live):, 0] == -1).all()
     assert [(x & 0xffff, (x >> 16) & 0xff, x >> 24) for x in w[:len(live), 0]] == live
@@ -63,6 +69,11 @@ def _run(cuda, nh, nkv, pos, mc, seed):
         rq, rd, _ = OQ.quantize_q8_1(ref[None])
         assert (gq[j] == rq.reshape(-1)).mean() >= 0.999, j
         assert (gds[j][:, 0] == rd.reshape(-1)).mean() >= 0.99, j
+
+
+def test_attn_f64_merge_launch_above_16_tokens(cuda):
+    """20 tokens: the work-list launch merges in a separate launch (bit-identical all the same)."""
+    _run(cuda, 12, 2, [(37 * j) % 900 for j in range(20)], 16, 77)
 
 
 @pytest.mark.parametrize("nh,nkv", [(12, 2), (8, 2), (16, 2), (12, 3)])
