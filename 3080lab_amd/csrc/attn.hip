@@ -75,9 +75,10 @@ __global__ void __launch_bounds__(G / HS * W * 64) k_attn_decode(const AttnArgs 
   const int kvh = r / HS, hs = r % HS;
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int hh = wv / W, part = wv % W;
+  // the page id does not depend on the position: both loads are in flight together
+  const int pg = a.block_table[(size_t)j * a.bt_stride + min(c, a.max_chunks - 1)];
   const int pos = a.pos[j];
   if (c >= a.max_chunks || c * PAGE > pos) return;  // chunk slot beyond the table or the context: nothing to do
-  const int pg = a.block_table[(size_t)j * a.bt_stride + c];
   const int hq = kvh * G + hs * GH + hh;
   const int nvalid = min(PAGE, pos + 1 - c * PAGE);
 
@@ -433,13 +434,15 @@ __global__ void __launch_bounds__(256) k_attn_merge_split(const AttnArgs a) {
 // (m_c, l_c) and forms w_c = e^(m_c - M) (M = max_c m_c); lane l then sums dims 2l, 2l+1 of
 // sum_c w_c o_c in fixed chunk order (w_c broadcast from lane c) and divides by L = sum_c w_c l_c.
 // All loads of a group of 8 chunks are issued before their first use. nch <= 64.
-__device__ __forceinline__ void attn_merge_head(const double* __restrict__ P, int nch, double* __restrict__ out) {
+// The first batch of loads is clamped by maxc (the chunk slots the partials buffer holds), not by nch, so it
+// does not wait for the position; chunks past nch are masked to 0 (stale slots may hold anything).
+__device__ __forceinline__ void attn_merge_head(const double* __restrict__ P, int maxc, int nch, double* __restrict__ out) {
   const int lane = threadIdx.x & 63;
-  const double* pc = P + (size_t)min(lane, nch - 1) * (HD + 2);
+  const double* pc = P + (size_t)min(lane, maxc - 1) * (HD + 2);
   const double mc = pc[HD], lc = pc[HD + 1];
   double2 v[8];
 #pragma unroll
-  for (int u = 0; u < 8; ++u) v[u] = ((const double2*)(P + (size_t)min(u, nch - 1) * (HD + 2)))[lane];
+  for (int u = 0; u < 8; ++u) v[u] = ((const double2*)(P + (size_t)min(u, maxc - 1) * (HD + 2)))[lane];
   const double M = wave_max_d(lane < nch ? mc : -INFINITY);
   const double w = lane < nch ? exp(mc - M) : 0.0;
   const double L = wave_sum_d(w * (lane < nch ? lc : 0.0));
@@ -452,8 +455,9 @@ __device__ __forceinline__ void attn_merge_head(const double* __restrict__ P, in
       bi.x = __builtin_amdgcn_readlane(wi.x, c0 + u);   // 0 for chunks >= nch (w = 0 there)
       bi.y = __builtin_amdgcn_readlane(wi.y, c0 + u);
       const double wc = *reinterpret_cast<const double*>(&bi);
-      o0 = fma(wc, v[u].x, o0);
-      o1 = fma(wc, v[u].y, o1);
+      const bool live = c0 + u < nch;
+      o0 = fma(wc, live ? v[u].x : 0.0, o0);
+      o1 = fma(wc, live ? v[u].y : 0.0, o1);
     }
     if (c0 + 8 < nch) {
 #pragma unroll
@@ -470,7 +474,7 @@ __global__ void __launch_bounds__(64) k_attn_merge(const AttnArgs a) {
   __shared__ double sm[HD];
   const int j = blockIdx.x, h = blockIdx.y;
   const int nch = a.pos[j] / PAGE + 1;
-  attn_merge_head(a.part + ((size_t)j * a.nh + h) * a.max_chunks * (HD + 2), nch, sm);
+  attn_merge_head(a.part + ((size_t)j * a.nh + h) * a.max_chunks * (HD + 2), a.max_chunks, nch, sm);
   __syncthreads();
   const int n = a.nh * HD;
   if (a.oh) {                                           // fp16 output (the fp16 batched path)

@@ -191,7 +191,7 @@ struct XLoad {
       for (int j = 0; j < a.T; ++j) {
         const int nch = a.pos[j] / PAGE + 1;
         for (int h = threadIdx.x >> 6; h < nhs; h += NTH / 64)
-          attn_merge_head(a.attn_part + ((size_t)j * a.nh + h0 + h) * a.attn_max_chunks * (HD + 2), nch,
+          attn_merge_head(a.attn_part + ((size_t)j * a.nh + h0 + h) * a.attn_max_chunks * (HD + 2), a.attn_max_chunks, nch,
                           ob + h * HD);
         __syncthreads();
         for (int g = threadIdx.x; g < nhs * HD / 8; g += NTH) {   // quads stay whole (HD / 8 % 4 == 0)
