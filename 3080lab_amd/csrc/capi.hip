@@ -1089,3 +1089,12 @@ extern "C" int q355_mega_decode(const void* layers, int L, const uint8_t* emb_qs
   hipLaunchKernelGGL(k_mega_decode, dim3(MG_NWG), dim3(MG_NTH), MEGA_LDS, (hipStream_t)stream, a);
   return launched("mega_decode");
 }
+
+// Measurement only (bench.py): read `bytes` (a multiple of 16) from p once, streaming; no output.
+extern "C" int q355_stream_read(const void* p, int64_t bytes, void* stream) {
+  REQUIRE(p && bytes > 0 && bytes % 16 == 0, "stream_read: p=%p bytes=%lld", p, (long long)bytes);
+  const long n16 = (long)(bytes / 16);
+  hipLaunchKernelGGL(k_stream_read, dim3((unsigned)((n16 + 4095) / 4096)), dim3(256), 0, (hipStream_t)stream,
+                     (const uint4*)p, n16, (unsigned*)nullptr);
+  return launched("stream_read");
+}

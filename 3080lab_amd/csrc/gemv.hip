@@ -804,4 +804,22 @@ __global__ void __launch_bounds__(256) k_blockdots(const uint8_t* __restrict__ q
   }
 }
 
+// ---------------------------------------------------------------------------------------------
+// Measurement: a pure streaming read (16-byte non-temporal loads, 16 per lane, all in flight), the ceiling a
+// weight stream of the same size reaches when launched the way the decode step launches its GEMVs.
+__global__ void __launch_bounds__(256) k_stream_read(const uint4* __restrict__ p, long n16, unsigned* __restrict__ out) {
+  constexpr int PER = 16;
+  const long base = (long)blockIdx.x * 256 * PER + threadIdx.x;
+  uint4 v[PER];
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const long e = base + (long)i * 256;
+    v[i] = e < n16 ? ld_stream16(p + e) : make_uint4(0, 0, 0, 0);
+  }
+  unsigned acc = 0;
+#pragma unroll
+  for (int i = 0; i < PER; ++i) acc ^= v[i].x ^ v[i].w;
+  if (acc == 0x9e3779b9u && n16 < 0) out[blockIdx.x] = acc;   // never: keeps the loads
+}
+
 }  // namespace q355

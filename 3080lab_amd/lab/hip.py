@@ -67,6 +67,7 @@ _SIGS = {
     "q355_attn_decode_f64_wl": [_P, _P, _P, _P, _P, c_int, c_int, c_int, c_int, c_double, _P, _P, _P, _P, c_int, _P,
                                 _P],
     "q355_attn_f64_worklist_bytes": [c_int, c_int, c_int],
+    "q355_stream_read": [_P, ctypes.c_int64, _P],
     "q355_attn_f64_worklist": [_P, _P, c_int, c_int, c_int, c_int, _P, _P],
     "q355_gemm_f16_qkv_rope": [_P, _P, c_int, c_int, _P, c_int, _P, _P, _P, _P, _P, c_int, c_int, _P, _P, _P,
                                c_int, c_int, _P],

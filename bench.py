@@ -132,12 +132,22 @@ def gate_up_roofline(dm, dec) -> dict:
     # the same kernel's average in the committed rocprofv3 summary of this command (traced: each dispatch
     # carries the profiler's per-dispatch work, so it reads longer than the live HIP-event figure)
     pus = profile_avg_us()
+    # the practical ceiling for a stream of this size launched this way: a pure streaming read of the same
+    # bytes from 28 distinct buffers (435 MB: more than the 256 MB Infinity Cache), one graph of 28 launches
+    import torch
+    bufs = [torch.ones(algo // 16 * 4, dtype=torch.int32, device="cuda") for _ in range(c.L)]
+    sms = time_launches(lambda i: call("q355_stream_read", ptr(bufs[i]), bufs[i].numel() * 4), c.L)
+    ceil = bufs[0].numel() * 4 / (sms * 1e-3) / 1e9
+    del bufs
+    torch.cuda.empty_cache()
     return {"kernel": "q355_ffn_gate_up (k_gemv<1,5,4,3,PRO_RMS,EPI_SWIGLU>)", "bound": "hbm",
             "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4),
             "traffic": traffic_from_profile(), "traffic_source": str(TRAFFIC_PROFILE.relative_to(ROOT)),
             "algorithmic_bytes": int(algo), "avg_us": round(ms * 1e3, 3),
             "profile_avg_us": pus, "profile_source": str(KSTATS_PROFILE.relative_to(ROOT)),
-            "frac_profile": round(algo / (pus * 1e-6) / 1e9 / HBM_PEAK_GBS, 4) if pus else None}
+            "frac_profile": round(algo / (pus * 1e-6) / 1e9 / HBM_PEAK_GBS, 4) if pus else None,
+            "same_size_stream": {"us": round(sms * 1e3, 3), "GBps": round(ceil, 1),
+                                 "frac_of_peak": round(ceil / HBM_PEAK_GBS, 4), "achieved_over_it": round(ach / ceil, 4)}}
 
 
 def gemv_config0(copies: int = 64) -> dict:

@@ -343,6 +343,11 @@ int q355_mega_decode(const void* layers, int L, const uint8_t* emb_qs, const voi
                      double eps, int32_t* tok, int32_t* pos, int64_t* h, float* logits, void* ws,
                      int64_t spin_limit_us, void* stream);
 
+/* Measurement only: one streaming read of `bytes` (a multiple of 16) from p, 16-byte non-temporal loads all in
+ * flight, nothing written. bench.py times it over distinct buffers in a graph to give the practical ceiling
+ * for a weight stream of one GEMV's size. No counterpart in the reference. */
+int q355_stream_read(const void* p, int64_t bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
