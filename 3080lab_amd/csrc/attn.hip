@@ -622,8 +622,12 @@ __device__ __forceinline__ void pv_keys(double (&o)[G][2], const double (&pr)[G]
   (pv_key<T, G>(o, pr, vr, kg, nvalid), ...);
 }
 
-template <int G, int SPG>
-__global__ void __launch_bounds__(SPG * 256) __attribute__((amdgpu_waves_per_eu(6))) k_attn_batch_f64(const AttnArgs a) {
+// EARLY (launches with few workgroups, where occupancy does not matter): a register budget of two waves per
+// SIMD instead of six, spent on issuing the V loads together with the K loads (one memory latency instead of
+// two on the workgroup's path) and on the in-kernel merge's load batches of 20 splits instead of 4.
+template <int G, int SPG, bool EARLY = false>
+__global__ void __launch_bounds__(SPG * 256) __attribute__((amdgpu_waves_per_eu(EARLY ? 2 : 6)))
+k_attn_batch_f64(const AttnArgs a) {
   static_assert(G % 2 == 0 && G <= 8, "heads per KV group");
   constexpr int KEYS = SPG * PAGE;
   __shared__ __align__(16) double sq[4][G][KEYS];      // score partials per dim quarter
@@ -682,6 +686,11 @@ __global__ void __launch_bounds__(SPG * 256) __attribute__((amdgpu_waves_per_eu(
     uint4 kr[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) kr[i] = ld_stream16(a.kcache + base + (size_t)lane * HD + 32 * dq + 8 * i);
+    if (EARLY) {
+#pragma unroll
+      for (int t = 0; t < 16; ++t)
+        vr[t] = ld_stream4(a.vcache + base + (size_t)(4 * t + kg) * HD + 32 * dq + 2 * dp);
+    }
     double acc[G];
 #pragma unroll
     for (int h = 0; h < G; ++h) acc[h] = 0.0;
@@ -704,9 +713,11 @@ __global__ void __launch_bounds__(SPG * 256) __attribute__((amdgpu_waves_per_eu(
 #pragma unroll
     for (int h = 0; h < G; ++h) sq[dq][h][pg * PAGE + lane] = acc[h];
     // V operands of phase 3, in flight during the softmax: keys 4 t + l / 16, dims 32 dq + 2 (l % 16)
+    if (!EARLY) {
 #pragma unroll
-    for (int t = 0; t < 16; ++t)
-      vr[t] = ld_stream4(a.vcache + base + (size_t)(4 * t + kg) * HD + 32 * dq + 2 * dp);
+      for (int t = 0; t < 16; ++t)
+        vr[t] = ld_stream4(a.vcache + base + (size_t)(4 * t + kg) * HD + 32 * dq + 2 * dp);
+    }
   } else {
 #pragma unroll
     for (int h = 0; h < G; ++h) sq[dq][h][pg * PAGE + lane] = 0.0;
@@ -824,7 +835,7 @@ __global__ void __launch_bounds__(SPG * 256) __attribute__((amdgpu_waves_per_eu(
   }
   __syncthreads();
   if (!last) return;
-  if (t < G * 64) merge_f64<G, SPG, 4, true>(a, kvh, j, nsplit, t);   // 4 splits per load batch: VGPR budget
+  if (t < G * 64) merge_f64<G, SPG, EARLY ? 20 : 4, true>(a, kvh, j, nsplit, t);   // splits per load batch: VGPR budget
 }
 
 // The live work items of k_attn_batch_f64 for one step, built by one wave (T <= 64 tokens, lane t = token t):

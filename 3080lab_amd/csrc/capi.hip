@@ -659,7 +659,10 @@ constexpr int ATTN64_FUSED_MERGE_T = 16;              // work-list launches of u
 template <int G>
 static int launch_attn_f64(const AttnArgs& a, int T, hipStream_t s) {
   const int nsp = (a.max_chunks + ATTN64_SPG - 1) / ATTN64_SPG;
-  hipLaunchKernelGGL((k_attn_batch_f64<G, ATTN64_SPG>), dim3(a.nkv * nsp, T), dim3(ATTN64_SPG * 256), 0, s, a);
+  if (a.arrivals)                                       // up to 16 tokens: few workgroups, latency first
+    hipLaunchKernelGGL((k_attn_batch_f64<G, ATTN64_SPG, true>), dim3(a.nkv * nsp, T), dim3(ATTN64_SPG * 256), 0, s, a);
+  else
+    hipLaunchKernelGGL((k_attn_batch_f64<G, ATTN64_SPG>), dim3(a.nkv * nsp, T), dim3(ATTN64_SPG * 256), 0, s, a);
   if (int e = launched("attn_decode_f64")) return e;
   if (nsp == 1 || a.arrivals) return Q355_OK;          // every token fits one split, or merged by its last split
   hipLaunchKernelGGL((k_attn_merge_f64<G, ATTN64_SPG>), dim3(a.nkv, T), dim3(G * 64), 0, s, a);
