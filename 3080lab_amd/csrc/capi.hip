@@ -536,6 +536,18 @@ static int launch_mmq_logits_tile(const GemvArgs& a, hipStream_t s) {
 // (XF32): 64-row workgroups, K split 32 blocks per slice (16 waves x 2 up to 16 tokens, else 8 x 4) or <= 16
 // (4 waves x 4).
 // Returns -1 outside these classes.
+// Up to 8 tokens (TG = 1) the kernels run in their half-column form (k_mmq_r HALF).
+template <int TG, int NT, int NW, int KPW, int EPI, bool XF32>
+static void launch_mmq_r(const GemvArgs& a, dim3 grid, hipStream_t s) {
+  if constexpr (TG == 1) {
+    if (a.T <= 8) {
+      hipLaunchKernelGGL((k_mmq_r<TG, NT, NW, KPW, EPI, XF32, true>), grid, dim3(NW * 64), 0, s, a);
+      return;
+    }
+  }
+  hipLaunchKernelGGL((k_mmq_r<TG, NT, NW, KPW, EPI, XF32>), grid, dim3(NW * 64), 0, s, a);
+}
+
 template <int TG, int EPI, bool XF32>
 static int launch_mmq_r_tg(const GemvArgs& a, hipStream_t s) {
   const int nb = a.K / 32;
@@ -543,8 +555,8 @@ static int launch_mmq_r_tg(const GemvArgs& a, hipStream_t s) {
     if (a.N % 80 || a.N / 80 > 256 || nb > 8 * 6) return -1;
     // up to 16 tokens 16 waves x 3 blocks (8 x 6: 9.66 against 8.34 us at B = 8); 32 tokens keep 8 waves (the
     // 16-wave partials would need 160 KB of LDS)
-    if constexpr (TG == 1) hipLaunchKernelGGL((k_mmq_r<TG, 5, 16, 3, EPI, XF32>), dim3(a.N / 80), dim3(1024), 0, s, a);
-    else hipLaunchKernelGGL((k_mmq_r<TG, 5, 8, 6, EPI, XF32>), dim3(a.N / 80), dim3(512), 0, s, a);
+    if constexpr (TG == 1) launch_mmq_r<TG, 5, 16, 3, EPI, XF32>(a, dim3(a.N / 80), s);
+    else launch_mmq_r<TG, 5, 8, 6, EPI, XF32>(a, dim3(a.N / 80), s);
     return launched("mmq");
   }
   if constexpr (EPI == EPI_QKV && !XF32) {
@@ -552,21 +564,21 @@ static int launch_mmq_r_tg(const GemvArgs& a, hipStream_t s) {
     // at B = 8 / 32 against 5.20 / 8.94), bias + RoPE + K/V write in the epilogue (a RoPE pair sits in
     // adjacent rows of one tile)
     if (a.N % 16 || nb > 16 * 3) return -1;
-    hipLaunchKernelGGL((k_mmq_r<TG, 1, 16, 3, EPI, XF32>), dim3(a.N / 16), dim3(1024), 0, s, a);
+    launch_mmq_r<TG, 1, 16, 3, EPI, XF32>(a, dim3(a.N / 16), s);
     return launched("mmq");
   }
   if constexpr (EPI == EPI_RESID_FIX && XF32) {
     if (a.N % 64) return -1;
     if (nb >= 64) {
       const int KS = (nb + 31) / 32;
-      if constexpr (TG == 1) hipLaunchKernelGGL((k_mmq_r<TG, 4, 16, 2, EPI, XF32>), dim3(a.N / 64, KS), dim3(1024), 0, s, a);
-      else hipLaunchKernelGGL((k_mmq_r<TG, 4, 8, 4, EPI, XF32>), dim3(a.N / 64, KS), dim3(512), 0, s, a);
+      if constexpr (TG == 1) launch_mmq_r<TG, 4, 16, 2, EPI, XF32>(a, dim3(a.N / 64, KS), s);
+      else launch_mmq_r<TG, 4, 8, 4, EPI, XF32>(a, dim3(a.N / 64, KS), s);
       return launched("mmq");
     }
     int KS = 1;
     while ((a.N / 64) * KS < 256 && nb / (KS + 1) >= 4) ++KS;
     if ((nb + KS - 1) / KS > 16) return -1;
-    hipLaunchKernelGGL((k_mmq_r<TG, 4, 4, 4, EPI, XF32>), dim3(a.N / 64, KS), dim3(256), 0, s, a);
+    launch_mmq_r<TG, 4, 4, 4, EPI, XF32>(a, dim3(a.N / 64, KS), s);
     return launched("mmq");
   }
   return -1;

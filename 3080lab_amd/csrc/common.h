@@ -90,6 +90,7 @@ __device__ __forceinline__ int sum_i8x32(const int* x) {
 
 // DPP lane exchanges (no LDS traffic): quad_perm xor 1 / xor 2, half-row mirror, row mirror.
 constexpr int DPP_XOR1 = 0xB1, DPP_XOR2 = 0x4E, DPP_HALF_MIRROR = 0x141, DPP_MIRROR = 0x140;
+constexpr int DPP_ROR8 = 0x128;                     // row_ror:8: lane l of a 16-lane row takes lane l ^ 8's value
 template <int CTRL>
 __device__ __forceinline__ float dpp(float v) {
   return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, true));

@@ -196,8 +196,12 @@ __device__ __forceinline__ long q8_1_mfma8(const float (&x)[8], float& df) {
 // memory latency. Wave wv takes blocks b0 + wv + NW i of the K slice (i < KPW); activations come straight
 // from global memory (each element is used by one wave only): Q8_1 (xq / xds), or with XF32 fp32 values
 // (xf, the SwiGLU output) quantized to Q8_1 in registers. Partials reduce over waves through LDS.
-template <int TG, int NT, int NW, int KPW, int EPI, bool XF32>
+// HALF (T <= 8, TG == 1): the MFMA's token columns 8..15 are padding, so lane li + 8 takes over rows
+// 4 lg + 2, 4 lg + 3 of token li (their products and scales arrive by a DPP swap of the row's halves) and every
+// lane accumulates two rows instead of four: half the f64 work, the same arithmetic per output.
+template <int TG, int NT, int NW, int KPW, int EPI, bool XF32, bool HALF = false>
 __global__ void __launch_bounds__(NW * 64) k_mmq_r(const GemvArgs a) {
+  static_assert(!HALF || TG == 1, "the half-column form is for one token group");
   Q355_TRACE_POINT(0);
   __shared__ double part[NW][NT][16 * TG][16];
   constexpr int TT = 16 * TG;
@@ -306,20 +310,41 @@ __global__ void __launch_bounds__(NW * 64) k_mmq_r(const GemvArgs a) {
         v16f sc[NQ];
 #pragma unroll
         for (int q = 0; q < NQ; ++q) sc[q] = __builtin_amdgcn_mfma_f32_16x16x1f32(dwl[i][q], dx[i][g], zf, 0, 0, 0);
+        if constexpr (HALF) {
+          const bool hi = li >= 8;
 #pragma unroll
-        for (int t = 0; t < NT; ++t)
+          for (int t = 0; t < NT; ++t)
 #pragma unroll
-          for (int v = 0; v < 4; ++v)
-            acc[t][g][v] = mac(sc[t >> 2][4 * (t & 3) + v], c[t][g][v], acc[t][g][v]);
+            for (int v = 0; v < 2; ++v) {
+              const int cs = dpp<DPP_ROR8>(c[t][g][v + 2]);
+              const float ss = dpp<DPP_ROR8>(sc[t >> 2][4 * (t & 3) + v + 2]);
+              acc[t][g][v] = mac(hi ? ss : sc[t >> 2][4 * (t & 3) + v], hi ? cs : c[t][g][v], acc[t][g][v]);
+            }
+        } else {
+#pragma unroll
+          for (int t = 0; t < NT; ++t)
+#pragma unroll
+            for (int v = 0; v < 4; ++v)
+              acc[t][g][v] = mac(sc[t >> 2][4 * (t & 3) + v], c[t][g][v], acc[t][g][v]);
+        }
       }
     }
   }
+  if constexpr (HALF) {
+    const int tok = li & 7, r0 = 4 * lg + 2 * (li >> 3);
 #pragma unroll
-  for (int t = 0; t < NT; ++t)
+    for (int t = 0; t < NT; ++t) {
+      part[wv][t][tok][r0] = acc[t][0][0];
+      part[wv][t][tok][r0 + 1] = acc[t][0][1];
+    }
+  } else {
 #pragma unroll
-    for (int g = 0; g < TG; ++g)
+    for (int t = 0; t < NT; ++t)
 #pragma unroll
-      for (int v = 0; v < 4; ++v) part[wv][t][16 * g + li][4 * lg + v] = acc[t][g][v];
+      for (int g = 0; g < TG; ++g)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) part[wv][t][16 * g + li][4 * lg + v] = acc[t][g][v];
+  }
   Q355_TRACE_POINT(2);
   __syncthreads();
   Q355_TRACE_POINT(3);
