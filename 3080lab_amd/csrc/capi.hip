@@ -461,6 +461,12 @@ extern "C" int q355_rmsnorm_fix_q8_1(const int64_t* h, const float* w, int8_t* x
 
 template <int TG, int KPW, int EPI>
 static int launch_mmq_reg(const GemvArgs& a, dim3 grid, size_t lds, hipStream_t s) {
+  if constexpr (TG == 1) {
+    if (a.T <= 8) {                                     // half-column form (k_mmq_r HALF)
+      hipLaunchKernelGGL((k_mmq_reg<TG, 4, 4, KPW, EPI, false, true>), grid, dim3(256), lds, s, a);
+      return launched("mmq");
+    }
+  }
   hipLaunchKernelGGL((k_mmq_reg<TG, 4, 4, KPW, EPI>), grid, dim3(256), lds, s, a);
   return launched("mmq");
 }

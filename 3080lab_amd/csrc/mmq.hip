@@ -50,7 +50,7 @@ template <int TG> using MmqAcc = typename std::conditional<TG == 1, double, floa
 // dwl[q]: d_w of row li of tile 4 q + lg (0 past NT); the d_w d_x products of all outputs come from 4-block
 // outer products on the matrix cores (lane l receives d_w[tile][4 lg + v] d_x[token li] in register
 // 4 (tile % 4) + v).
-template <int NT, int TG, typename ACC>
+template <int NT, int TG, typename ACC, bool HALF = false>
 __device__ __forceinline__ void mmq_block(const uint2 (&w)[NT], const float (&dwl)[(NT + 3) / 4], const int8_t* __restrict__ xq,
                                           int xstride, const float* xd, int ld, int bb, int li, int lg, ACC (&acc)[NT][TG][4]) {
   v4i c[NT][TG];
@@ -71,10 +71,22 @@ __device__ __forceinline__ void mmq_block(const uint2 (&w)[NT], const float (&dw
     v16f sc[(NT + 3) / 4];
 #pragma unroll
     for (int q = 0; q < (NT + 3) / 4; ++q) sc[q] = __builtin_amdgcn_mfma_f32_16x16x1f32(dwl[q], dx[g], zf, 0, 0, 0);
+    if constexpr (HALF) {                              // see k_mmq_r: rows 4 lg + 2, + 3 of token li on lane li + 8
+      const bool hi = li >= 8;
 #pragma unroll
-    for (int t = 0; t < NT; ++t)
+      for (int t = 0; t < NT; ++t)
 #pragma unroll
-      for (int v = 0; v < 4; ++v) acc[t][g][v] = mac(sc[t >> 2][4 * (t & 3) + v], c[t][g][v], acc[t][g][v]);
+        for (int v = 0; v < 2; ++v) {
+          const int cs = dpp<DPP_ROR8>(c[t][g][v + 2]);
+          const float ss = dpp<DPP_ROR8>(sc[t >> 2][4 * (t & 3) + v + 2]);
+          acc[t][g][v] = mac(hi ? ss : sc[t >> 2][4 * (t & 3) + v], hi ? cs : c[t][g][v], acc[t][g][v]);
+        }
+    } else {
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) acc[t][g][v] = mac(sc[t >> 2][4 * (t & 3) + v], c[t][g][v], acc[t][g][v]);
+    }
   }
 }
 
@@ -451,8 +463,9 @@ __global__ void __launch_bounds__(NW * 64) k_mmq(const GemvArgs a) {
 // the activations are staged (wave wv takes blocks b0 + wv + NW i, i < KPW; the slice must have at most
 // NW * KPW blocks), so the HBM latency is paid once per workgroup instead of once per pipeline step. The
 // slice's scales go through LDS with the activations (registers hold only the nibbles).
-template <int TG, int NT, int NW, int KPW, int EPI, bool ATT = false>
+template <int TG, int NT, int NW, int KPW, int EPI, bool ATT = false, bool HALF = false>
 __global__ void __launch_bounds__(NW * 64) k_mmq_reg(const GemvArgs a) {
+  static_assert(!HALF || TG == 1, "the half-column form is for one token group");
   extern __shared__ __align__(16) char lds[];
   Q355_TRACE_POINT(0);
   constexpr int TT = 16 * TG;
@@ -504,19 +517,28 @@ __global__ void __launch_bounds__(NW * 64) k_mmq_reg(const GemvArgs a) {
 #pragma unroll
       for (int q = 0; q < (NT + 3) / 4; ++q)
         dv[q] = 4 * q + lg < NT ? __half2float(((const __half*)wsc)[((4 * q + lg) * nbs + bb) * 16 + li]) : 0.f;
-      mmq_block<NT, TG, ACC>(w[i], dv, xq, xstride, xd, nbs, bb, li, lg, acc);
+      mmq_block<NT, TG, ACC, HALF>(w[i], dv, xq, xstride, xd, nbs, bb, li, lg, acc);
     }
   }
   Q355_TRACE_POINT(2);
   __syncthreads();
   Q355_TRACE_POINT(3);
   ACC(&part)[NW][NT][TT][16] = *reinterpret_cast<ACC(*)[NW][NT][TT][16]>(lds);
+  if constexpr (HALF) {
+    const int tok = li & 7, r0 = 4 * lg + 2 * (li >> 3);
 #pragma unroll
-  for (int t = 0; t < NT; ++t)
+    for (int t = 0; t < NT; ++t) {
+      part[wv][t][tok][r0] = acc[t][0][0];
+      part[wv][t][tok][r0 + 1] = acc[t][0][1];
+    }
+  } else {
 #pragma unroll
-    for (int g = 0; g < TG; ++g)
+    for (int t = 0; t < NT; ++t)
 #pragma unroll
-      for (int v = 0; v < 4; ++v) part[wv][t][16 * g + li][4 * lg + v] = acc[t][g][v];
+      for (int g = 0; g < TG; ++g)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) part[wv][t][16 * g + li][4 * lg + v] = acc[t][g][v];
+  }
   __syncthreads();
   GemvArgs b = a;
   b.T = ntok;
