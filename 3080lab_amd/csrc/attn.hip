@@ -628,7 +628,9 @@ __device__ __forceinline__ void pv_keys(double (&o)[G][2], const double (&pr)[G]
 template <int G, int SPG, bool EARLY = false>
 __global__ void __launch_bounds__(SPG * 256) __attribute__((amdgpu_waves_per_eu(EARLY ? 2 : 6)))
 k_attn_batch_f64(const AttnArgs a) {
+  Q355_TRACE_POINT(0);
   static_assert(G % 2 == 0 && G <= 8, "heads per KV group");
+  static_assert(SPG * 4 >= G, "the in-kernel merge takes one wave per query head");
   constexpr int KEYS = SPG * PAGE;
   __shared__ __align__(16) double sq[4][G][KEYS];      // score partials per dim quarter
   __shared__ __align__(16) double ps[KEYS][G];         // p per key (16-byte reads give two heads)
@@ -681,6 +683,7 @@ k_attn_batch_f64(const AttnArgs a) {
       qd[h][1] = q[h * HD + 16];
     }
   }
+  Q355_TRACE_POINT(1);
   // 1. scores of this wave's dim quarter
   if (live) {
     uint4 kr[4];
@@ -723,6 +726,7 @@ k_attn_batch_f64(const AttnArgs a) {
     for (int h = 0; h < G; ++h) sq[dq][h][pg * PAGE + lane] = 0.0;
   }
   __syncthreads();
+  Q355_TRACE_POINT(2);
   // 2. softmax: wave w takes heads w, w + 4 SPG, ... over the split's keys (SPG per lane)
   for (int h = wv; h < G; h += 4 * SPG) {
     double sv[SPG], m = -INFINITY;
@@ -746,6 +750,7 @@ k_attn_batch_f64(const AttnArgs a) {
     if (lane == 0) { xm[h] = M; xl[h] = l; }
   }
   __syncthreads();
+  Q355_TRACE_POINT(3);
   // 3. P.V of this wave's dims and page: lane (row kg, position t) holds p of key 4 t + kg of the page, which
   // the FMAs of key 4 t + kg read as a row broadcast
   if (live) {
@@ -790,6 +795,7 @@ k_attn_batch_f64(const AttnArgs a) {
     }
   }
   __syncthreads();
+  Q355_TRACE_POINT(4);
   // 4. thread (head h, dims 8 dg .. 8 dg + 7): the split's live pages in page order
   const int t = threadIdx.x;
   if (t < G * 16) {                                     // whole quads (Q8_1 blocks) stay together
@@ -821,6 +827,7 @@ k_attn_batch_f64(const AttnArgs a) {
       if (dg == 0) *(double2*)(P + HD) = make_double2(xm[h], xl[h]);
     }
   }
+  Q355_TRACE_POINT(5);
   if (nsplit == 1 || !a.arrivals) return;             // uniform per workgroup
   // 5. the last split of this (token, KV head) to finish merges all of them (no separate merge launch): every
   // thread's partial stores are acknowledged before the workgroup counts itself, so the last to count finds
@@ -834,8 +841,10 @@ k_attn_batch_f64(const AttnArgs a) {
     if (last) stc(cnt, 0);
   }
   __syncthreads();
+  Q355_TRACE_POINT(6);
   if (!last) return;
   if (t < G * 64) merge_f64<G, SPG, EARLY ? 20 : 4, true>(a, kvh, j, nsplit, t);   // splits per load batch: VGPR budget
+  Q355_TRACE_POINT(7);
 }
 
 // The live work items of k_attn_batch_f64 for one step, built by one wave (T <= 64 tokens, lane t = token t):
