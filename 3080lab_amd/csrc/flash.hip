@@ -30,6 +30,28 @@ constexpr int FV_ROW = KP * PAGE + 4;   // Vt row (one dim, KP pages of keys) in
 
 __device__ __forceinline__ h8 as_h8(uint4 v) { return *reinterpret_cast<h8*>(&v); }
 
+// Scheduling of an unrolled run of N LDS operand reads feeding N MFMA groups (CBN MFMAs each): PF_DEPTH reads
+// first, then one MFMA group per further read, then the last groups (masks: 0x100 LDS read, 0x008 MFMA).
+// phase accounting hooks of the key loop: empty here; an instrumented build defines them
+#ifndef Q355_PF_PHASE
+#define Q355_PF_PHASE_INIT()
+#define Q355_PF_PHASE(k)
+#define Q355_PF_PHASE_END()
+#endif
+
+#ifndef PF_DEPTH
+#define PF_DEPTH 8
+#endif
+#define Q355_PIPELINE(N)                                                                       \
+  do {                                                                                         \
+    __builtin_amdgcn_sched_group_barrier(0x100, PF_DEPTH, 0);                                  \
+    _Pragma("unroll") for (int i_ = 0; i_ < (N) - PF_DEPTH; ++i_) {                            \
+      __builtin_amdgcn_sched_group_barrier(0x008, CBN, 0);                                     \
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);                                       \
+    }                                                                                          \
+    __builtin_amdgcn_sched_group_barrier(0x008, CBN * PF_DEPTH, 0);                            \
+  } while (0)
+
 constexpr int CBN = PF_QB / 16;      // 16-query MFMA column blocks per wave
 
 // Workgroup = one KV head x 16 queries x one key split of up to 32 pages, G = nh / nkv waves (wave w: query
@@ -107,8 +129,10 @@ __global__ void __launch_bounds__(512) k_attn_prefill(const PrefillAttnArgs a) {
   }
 
   Q355_LOAD_PAGE(kb0);
+  Q355_PF_PHASE_INIT();
   for (int kb = kb0; kb < nkb; kb += KP) {
     __syncthreads();                                       // previous step's LDS reads are done
+    Q355_PF_PHASE(0);
 #pragma unroll
     for (int p = 0; p < KP; ++p) {
 #pragma unroll
@@ -131,22 +155,33 @@ __global__ void __launch_bounds__(512) k_attn_prefill(const PrefillAttnArgs a) {
         }
       }
     }
+    Q355_PF_PHASE(1);
     __syncthreads();
+    Q355_PF_PHASE(2);
     Q355_LOAD_PAGE(min(kb + KP, nkb - 1));                 // next step (clamped: unconditional), in flight now
 
     // S^T tiles: keys 16t + (4g + v), query li of column block cb; each K operand feeds both blocks
+    // operand n = (c, t), t fastest: 4 KP independent accumulator chains; the schedule keeps PF_DEPTH LDS
+    // reads in flight ahead of the MFMAs (left to itself the compiler issues one or two)
     f4 s[CBN][4 * KP];
 #pragma unroll
-    for (int t = 0; t < 4 * KP; ++t) {
+    for (int t = 0; t < 4 * KP; ++t)
 #pragma unroll
       for (int cb = 0; cb < CBN; ++cb) s[cb][t] = f4{0.f, 0.f, 0.f, 0.f};
+    {
+      constexpr int NS = 16 * KP;
+      h8 kA[NS];
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const h8 kA = as_h8(*(const uint4*)&ks[16 * t + li][32 * c + 8 * lg]);
+      for (int n = 0; n < NS; ++n)
+        kA[n] = as_h8(*(const uint4*)&ks[16 * (n % (4 * KP)) + li][32 * (n / (4 * KP)) + 8 * lg]);
 #pragma unroll
-        for (int cb = 0; cb < CBN; ++cb) s[cb][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kA, qf[cb][c], s[cb][t], 0, 0, 0);
-      }
+      for (int n = 0; n < NS; ++n)
+#pragma unroll
+        for (int cb = 0; cb < CBN; ++cb)
+          s[cb][n % (4 * KP)] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kA[n], qf[cb][n / (4 * KP)], s[cb][n % (4 * KP)], 0, 0, 0);
+      Q355_PIPELINE(NS);
     }
+    Q355_PF_PHASE(3);
     h8 pB[CBN][2 * KP];
     // causal mask only where the step reaches past the block's first query (uniform; this includes the step
     // with a repeated page past the range); queries past P need none: each query column of S, P and O is
@@ -186,19 +221,27 @@ __global__ void __launch_bounds__(512) k_attn_prefill(const PrefillAttnArgs a) {
       }
     }
     // O^T += Vt P^T over 2 KP 32-key chunks; each Vt operand feeds every block
+    Q355_PF_PHASE(4);
+    {
+      constexpr int NV = 16 * KP;                          // operand n = (c, dt), dt fastest
+      h8 vA[NV];
 #pragma unroll
-    for (int c = 0; c < 2 * KP; ++c)
+      for (int n = 0; n < NV; ++n) {
+        const _Float16* row = &vt[16 * (n % 8) + li][32 * (n / 8)];
+        const uint2 lo = *(const uint2*)(row + 4 * lg);
+        const uint2 hi = *(const uint2*)(row + 16 + 4 * lg);
+        vA[n] = as_h8(make_uint4(lo.x, lo.y, hi.x, hi.y));
+      }
 #pragma unroll
-      for (int dt = 0; dt < 8; ++dt) {
-        const _Float16* row = &vt[16 * dt + li][0];
-        const uint2 lo = *(const uint2*)(row + 32 * c + 4 * lg);
-        const uint2 hi = *(const uint2*)(row + 32 * c + 16 + 4 * lg);
-        const h8 vA = as_h8(make_uint4(lo.x, lo.y, hi.x, hi.y));
+      for (int n = 0; n < NV; ++n)
 #pragma unroll
         for (int cb = 0; cb < CBN; ++cb)
-          acc[cb][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vA, pB[cb][c], acc[cb][dt], 0, 0, 0);
-      }
+          acc[cb][n % 8] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vA[n], pB[cb][n / 8], acc[cb][n % 8], 0, 0, 0);
+      Q355_PIPELINE(NV);
+    }
+    Q355_PF_PHASE(5);
   }
+  Q355_PF_PHASE_END();
 #undef Q355_LOAD_PAGE
   if (nsplit > 1) {
     // partial -> workspace (same lane order on both sides), then arrival count
