@@ -1050,7 +1050,9 @@ static int attn_prefill(const void* q, const void* kcache, const void* vcache, c
     a.ws = (float*)ws;
     a.max_splits = splits;
   }
-  hipLaunchKernelGGL(k_attn_prefill, dim3(nqb, splits, nkv), dim3(64 * (nh / nkv)), 0, stream, a);
+  const dim3 grid(nqb, splits, nkv), block(64 * (nh / nkv + PF_STAGERS));
+  if (block.x <= 512) hipLaunchKernelGGL(k_attn_prefill<512>, grid, block, 0, stream, a);
+  else hipLaunchKernelGGL(k_attn_prefill<640>, grid, block, 0, stream, a);
   return launched("attn_prefill");
 }
 

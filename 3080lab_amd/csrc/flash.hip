@@ -54,25 +54,29 @@ __device__ __forceinline__ h8 as_h8(uint4 v) { return *reinterpret_cast<h8*>(&v)
 
 constexpr int CBN = PF_QB / 16;      // 16-query MFMA column blocks per wave
 
-// Workgroup = one KV head x 16 queries x one key split of up to 32 pages, G = nh / nkv waves (wave w: query
-// head kvh * G + w), so each staged K/V page serves all G heads of the group. Wave tile: 16 queries (one
-// MFMA column block; 147 VGPRs, so two workgroups share a CU). grid (ceil(P / 16), max splits, nkv), the
-// longest query blocks first;
-// 64 G threads. With several splits, each writes its unnormalized O, m and l to the workspace; the last
-// to arrive (counter per query block and KV head, reset by it) merges them and writes the output. Partials
-// and counters use device-coherent accesses: the splits may run on different XCDs.
-__global__ void __launch_bounds__(512) k_attn_prefill(const PrefillAttnArgs a) {
-  __shared__ __align__(16) _Float16 ks[KP * PAGE][FK_ROW];
-  __shared__ __align__(16) _Float16 vt[HD][FV_ROW];
+// Workgroup = one KV head x 16 queries x one key split of up to 32 pages. Waves 0 .. G-1 are the head waves
+// (wave w: query head kvh * G + w), so each staged K/V page serves all G heads of the group; waves G and
+// G + 1 stage K and Vt into a double buffer: while the head waves compute step s from buffer s & 1, they write
+// step s + 1 into the other buffer and load step s + 2 into registers, so one barrier per step separates
+// the two roles and the head waves hold no staging registers. Wave tile: 16 queries (one MFMA column block).
+// grid (ceil(P / 16), max splits, nkv), the longest query blocks first; 64 (G + 2) threads. With several
+// splits, each writes its unnormalized O, m and l to the workspace; the last to arrive (counter per query
+// block and KV head, reset by it) merges them and writes the output. Partials and counters use
+// device-coherent accesses: the splits may run on different XCDs.
+// NT: the launch's thread bound (512 up to G = 6: two waves per SIMD, 256 VGPRs; 640 for G = 7, 8)
+template <int NT>
+__global__ void __launch_bounds__(NT) k_attn_prefill(const PrefillAttnArgs a) {
+  __shared__ __align__(16) _Float16 ks[2][KP * PAGE][FK_ROW];
+  __shared__ __align__(16) _Float16 vt[2][HD][FV_ROW];
   const int G = a.nh / a.nkv;
   const int qb = gridDim.x - 1 - blockIdx.x, split = blockIdx.y, kvh = blockIdx.z;
   const int nsplit = a.ws ? pf_splits(a.pos0, qb, a.P) : 1;
   if (split >= nsplit) return;                           // uniform per workgroup
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int li = lane & 15, lg = lane >> 4;
-  const int hq = kvh * G + wv;
+  const bool stager = wv >= G;
+  const int hq = kvh * G + min(wv, G - 1);
   const int nq = a.nh * HD;
-  const int nthr = 64 * G;
 
   int qi[CBN], qpos[CBN];
   h8 qf[CBN][4];
@@ -81,9 +85,10 @@ __global__ void __launch_bounds__(512) k_attn_prefill(const PrefillAttnArgs a) {
     qi[cb] = qb * PF_QB + 16 * cb + li;
     qpos[cb] = a.pos0 + qi[cb];
     const int qc = min(qi[cb], a.P - 1);
+    if (!stager)
 #pragma unroll
-    for (int c = 0; c < 4; ++c)
-      qf[cb][c] = as_h8(*(const uint4*)(a.q + (size_t)qc * nq + hq * HD + 32 * c + 8 * lg));
+      for (int c = 0; c < 4; ++c)
+        qf[cb][c] = as_h8(*(const uint4*)(a.q + (size_t)qc * nq + hq * HD + 32 * c + 8 * lg));
   }
 
   const int last_key = min(a.pos0 + qb * PF_QB + PF_QB - 1, a.pos0 + a.P - 1);
@@ -91,15 +96,16 @@ __global__ void __launch_bounds__(512) k_attn_prefill(const PrefillAttnArgs a) {
   const int nkb = a.ws ? min(last_key / PAGE + 1, kb0 + PF_SPLIT_PAGES) : last_key / PAGE + 1;
   const float sl2 = a.scale * 1.4426950408889634f;       // scores in log2 units
 
-  // staging: K as 1024 16 B pieces (key e / 16, dims 8 (e % 16) ..); V transposed: lane l of wave w takes
-  // dims 2l, 2l + 1 of the 8-key groups w, w + G, ...: 8 dword loads per group, packed into two 16 B rows
-  constexpr int VMAX = 2;                                // V key groups per thread (G >= 4)
-  u32x4 kr[KP][4];
-  unsigned vr[KP][VMAX][8];
-  const int kper = (1024 + nthr - 1) / nthr, vper = (8 + G - 1) / G;
+  // staging (the two staging waves, thread st = 0..127): K as 1024 16 B pieces per page (key e / 16, dims
+  // 8 (e % 16) ..); V transposed: lane l of staging wave sw takes dims 2l, 2l + 1 of the 8-key groups sw,
+  // sw + 2, ...: 8 dword loads per group, packed into two 16 B rows
+  constexpr int KPS = 1024 / (64 * PF_STAGERS), VPS = 8 / PF_STAGERS;
+  const int st = threadIdx.x - 64 * G, sw = wv - G;
+  u32x4 kr[KP][KPS];
+  unsigned vr[KP][VPS][8];
   // the page ids of this workgroup's key range, read once (each page's loads then wait on one latency)
   __shared__ int pages[64];
-  for (int i = threadIdx.x; i < nkb - kb0 && i < 64; i += nthr) pages[i] = a.block_table[kb0 + i];
+  for (int i = threadIdx.x; i < nkb - kb0 && i < 64; i += blockDim.x) pages[i] = a.block_table[kb0 + i];
   __syncthreads();
 #define Q355_LOAD_PAGE(kb)                                                                     \
   _Pragma("unroll") for (int p_ = 0; p_ < KP; ++p_) {                                          \
@@ -107,14 +113,27 @@ __global__ void __launch_bounds__(512) k_attn_prefill(const PrefillAttnArgs a) {
     const int pg_ = kbp_ - kb0 < 64 ? pages[kbp_ - kb0] : a.block_table[kbp_];                 \
     const u32x4* kp_ = (const u32x4*)(a.kcache + ((size_t)pg_ * a.nkv + kvh) * PAGE * HD);     \
     const unsigned* vp_ = (const unsigned*)(a.vcache + ((size_t)pg_ * a.nkv + kvh) * PAGE * HD); \
-    _Pragma("unroll") for (int i = 0; i < 4; ++i) {                                            \
-      const int e = threadIdx.x + nthr * i;                                                    \
-      if (i < kper && e < 1024) kr[p_][i] = kp_[e];                                            \
+    _Pragma("unroll") for (int i = 0; i < KPS; ++i) kr[p_][i] = kp_[st + 64 * PF_STAGERS * i]; \
+    _Pragma("unroll") for (int i = 0; i < VPS; ++i) {                                          \
+      const int kg = sw + PF_STAGERS * i;                                                      \
+      _Pragma("unroll") for (int u = 0; u < 8; ++u) vr[p_][i][u] = vp_[(kg * 8 + u) * (HD / 2) + lane]; \
     }                                                                                          \
-    _Pragma("unroll") for (int i = 0; i < VMAX; ++i) {                                         \
-      const int kg = wv + G * i;                                                               \
-      if (i < vper && kg < 8)                                                                  \
-        _Pragma("unroll") for (int u = 0; u < 8; ++u) vr[p_][i][u] = vp_[(kg * 8 + u) * (HD / 2) + lane]; \
+  }
+#define Q355_STORE_PAGE(bf)                                                                    \
+  _Pragma("unroll") for (int p_ = 0; p_ < KP; ++p_) {                                          \
+    _Pragma("unroll") for (int i = 0; i < KPS; ++i) {                                          \
+      const int e = st + 64 * PF_STAGERS * i;                                                  \
+      *(u32x4*)&ks[bf][p_ * PAGE + (e >> 4)][(e & 15) * 8] = kr[p_][i];                        \
+    }                                                                                          \
+    _Pragma("unroll") for (int i = 0; i < VPS; ++i) {                                          \
+      const int kg = sw + PF_STAGERS * i;                                                      \
+      u32x4 lo, hi;                                                                            \
+      _Pragma("unroll") for (int j = 0; j < 4; ++j) {                                          \
+        lo[j] = __builtin_amdgcn_perm(vr[p_][i][2 * j + 1], vr[p_][i][2 * j], 0x05040100u);    \
+        hi[j] = __builtin_amdgcn_perm(vr[p_][i][2 * j + 1], vr[p_][i][2 * j], 0x07060302u);    \
+      }                                                                                        \
+      *(u32x4*)&vt[bf][2 * lane][p_ * PAGE + kg * 8] = lo;                                     \
+      *(u32x4*)&vt[bf][2 * lane + 1][p_ * PAGE + kg * 8] = hi;                                 \
     }                                                                                          \
   }
 
@@ -128,38 +147,28 @@ __global__ void __launch_bounds__(512) k_attn_prefill(const PrefillAttnArgs a) {
     for (int t = 0; t < 8; ++t) acc[cb][t] = f4{0.f, 0.f, 0.f, 0.f};
   }
 
-  Q355_LOAD_PAGE(kb0);
-  Q355_PF_PHASE_INIT();
-  for (int kb = kb0; kb < nkb; kb += KP) {
-    __syncthreads();                                       // previous step's LDS reads are done
-    Q355_PF_PHASE(0);
-#pragma unroll
-    for (int p = 0; p < KP; ++p) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int e = threadIdx.x + nthr * i;
-        if (i < kper && e < 1024) *(u32x4*)&ks[p * PAGE + (e >> 4)][(e & 15) * 8] = kr[p][i];
-      }
-#pragma unroll
-      for (int i = 0; i < VMAX; ++i) {
-        const int kg = wv + G * i;
-        if (i < vper && kg < 8) {
-          u32x4 lo, hi;
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            lo[j] = __builtin_amdgcn_perm(vr[p][i][2 * j + 1], vr[p][i][2 * j], 0x05040100u);
-            hi[j] = __builtin_amdgcn_perm(vr[p][i][2 * j + 1], vr[p][i][2 * j], 0x07060302u);
-          }
-          *(u32x4*)&vt[2 * lane][p * PAGE + kg * 8] = lo;
-          *(u32x4*)&vt[2 * lane + 1][p * PAGE + kg * 8] = hi;
-        }
-      }
-    }
-    Q355_PF_PHASE(1);
+  if (stager) {                                            // the staging waves' own loop, same barriers
+    Q355_LOAD_PAGE(kb0);
+    Q355_STORE_PAGE(0);
+    if (kb0 + KP < nkb) Q355_LOAD_PAGE(kb0 + KP);
     __syncthreads();
-    Q355_PF_PHASE(2);
-    Q355_LOAD_PAGE(min(kb + KP, nkb - 1));                 // next step (clamped: unconditional), in flight now
-
+    for (int kb = kb0, bf = 0; kb < nkb; kb += KP, bf ^= 1) {
+      if (kb + KP < nkb) {                                 // uniform
+        Q355_STORE_PAGE(bf ^ 1);
+        if (kb + 2 * KP < nkb) Q355_LOAD_PAGE(kb + 2 * KP);
+      }
+      __syncthreads();
+    }
+    if (nsplit > 1) {                                      // the split merge's two barriers
+      __syncthreads();
+      __syncthreads();
+    }
+    return;
+  }
+  __syncthreads();
+  Q355_PF_PHASE_INIT();
+  for (int kb = kb0, bf = 0; kb < nkb; kb += KP, bf ^= 1) {
+    Q355_PF_PHASE(0);
     // S^T tiles: keys 16t + (4g + v), query li of column block cb; each K operand feeds both blocks
     // operand n = (c, t), t fastest: 4 KP independent accumulator chains; the schedule keeps PF_DEPTH LDS
     // reads in flight ahead of the MFMAs (left to itself the compiler issues one or two)
@@ -173,7 +182,7 @@ __global__ void __launch_bounds__(512) k_attn_prefill(const PrefillAttnArgs a) {
       h8 kA[NS];
 #pragma unroll
       for (int n = 0; n < NS; ++n)
-        kA[n] = as_h8(*(const uint4*)&ks[16 * (n % (4 * KP)) + li][32 * (n / (4 * KP)) + 8 * lg]);
+        kA[n] = as_h8(*(const uint4*)&ks[bf][16 * (n % (4 * KP)) + li][32 * (n / (4 * KP)) + 8 * lg]);
 #pragma unroll
       for (int n = 0; n < NS; ++n)
 #pragma unroll
@@ -227,7 +236,7 @@ __global__ void __launch_bounds__(512) k_attn_prefill(const PrefillAttnArgs a) {
       h8 vA[NV];
 #pragma unroll
       for (int n = 0; n < NV; ++n) {
-        const _Float16* row = &vt[16 * (n % 8) + li][32 * (n / 8)];
+        const _Float16* row = &vt[bf][16 * (n % 8) + li][32 * (n / 8)];
         const uint2 lo = *(const uint2*)(row + 4 * lg);
         const uint2 hi = *(const uint2*)(row + 16 + 4 * lg);
         vA[n] = as_h8(make_uint4(lo.x, lo.y, hi.x, hi.y));
@@ -240,9 +249,11 @@ __global__ void __launch_bounds__(512) k_attn_prefill(const PrefillAttnArgs a) {
       Q355_PIPELINE(NV);
     }
     Q355_PF_PHASE(5);
+    __syncthreads();                                       // this buffer is free; the next one is staged
   }
   Q355_PF_PHASE_END();
 #undef Q355_LOAD_PAGE
+#undef Q355_STORE_PAGE
   if (nsplit > 1) {
     // partial -> workspace (same lane order on both sides), then arrival count
     const size_t slot = (((size_t)qb * a.nkv + kvh) * a.max_splits + split) * G + wv;

@@ -110,6 +110,7 @@ struct PrefillAttnArgs {
 };
 
 constexpr int PF_QB = 16;              // queries per prefill-attention workgroup (16 per MFMA column block)
+constexpr int PF_STAGERS = 2;          // K/V staging waves per prefill-attention workgroup (beside the G head waves)
 constexpr int PF_SPLIT_PAGES = 32;     // KV pages per key split (2048 keys)
 
 __host__ __device__ inline int pf_splits(int pos0, int qb, int P) {   // key splits of query block qb
