@@ -1022,11 +1022,19 @@ extern "C" int q355_mmq_qkv_rope(const uint8_t* qs, const void* d, int N, int K,
   return launch_mmq_big<EPI_QKV>(a, (hipStream_t)stream);
 }
 
-static int pf_max_splits(int max_ctx) { return ((max_ctx - 1) / PAGE) / PF_SPLIT_PAGES + 1; }
-
 extern "C" int64_t q355_attn_prefill_ws_bytes(int P, int max_ctx, int nh, int nkv) {
   if (P < 1 || max_ctx < P || nh < 1 || nkv < 1 || nh % nkv) return -1;
-  return (int64_t)(pf_ws_floats((P + PF_QB - 1) / PF_QB, nkv, nh / nkv, pf_max_splits(max_ctx)) * sizeof(float));
+  return (int64_t)(pf_ws_floats((P + PF_QB - 1) / PF_QB, nkv, nh / nkv, pf_max_splits(0, max_ctx)) * sizeof(float));
+}
+
+// compute units of the current device (the persistent prefill attention's workgroups), cached per device
+static int device_cus() {
+  static int cus[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (!cus[dev] && hipDeviceGetAttribute(&cus[dev], hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+    cus[dev] = 256;
+  return cus[dev];
 }
 
 static int attn_prefill(const void* q, const void* kcache, const void* vcache, const int32_t* block_table, int pos0,
@@ -1040,17 +1048,28 @@ static int attn_prefill(const void* q, const void* kcache, const void* vcache, c
   a.q = (const __half*)q; a.kcache = (const __half*)kcache; a.vcache = (const __half*)vcache;
   a.block_table = block_table; a.pos0 = pos0; a.P = P; a.nh = nh; a.nkv = nkv; a.scale = scale; a.out = out;
   a.oq = oq; a.ods = (half2*)ods;
-  const int nqb = (P + PF_QB - 1) / PF_QB;
-  int splits = 1;
+  const int G = nh / nkv, nqb = (P + PF_QB - 1) / PF_QB;
+  const dim3 block(64 * (G + PF_STAGERS));
   if (ws) {
-    splits = pf_max_splits(pos0 + P);
-    const int64_t need = (int64_t)(pf_ws_floats(nqb, nkv, nh / nkv, splits) * sizeof(float));
-    REQUIRE(ws_bytes >= need, "attn_prefill: workspace of %lld bytes, %lld needed for pos0 + P = %d",
-            (long long)ws_bytes, (long long)need, pos0 + P);
-    a.ws = (float*)ws;
-    a.max_splits = splits;
+    // the persistent form: items balanced over one workgroup per CU, at most PF_MAX_ROUNDS each; where every
+    // row is one item and they fit one round, there is nothing to balance and the per-row kernel starts sooner
+    const int items = pf_items(pos0, P, nkv);
+    const int W = items < device_cus() ? items : device_cus();
+    const bool balance = pf_max_splits(pos0, P) > 1 || items > W;
+    if (balance && (items + W - 1) / W <= PF_MAX_ROUNDS) {
+      a.max_splits = pf_max_splits(pos0, P);
+      const int64_t need = (int64_t)(pf_ws_floats(nqb, nkv, G, a.max_splits) * sizeof(float));
+      REQUIRE(ws_bytes >= need, "attn_prefill: workspace of %lld bytes, %lld needed for pos0 + P = %d",
+              (long long)ws_bytes, (long long)need, pos0 + P);
+      a.ws = (float*)ws;
+      a.n_items = items;
+      if (block.x <= 512) hipLaunchKernelGGL(k_attn_prefill_pers<512>, dim3(W), block, 0, stream, a);
+      else hipLaunchKernelGGL(k_attn_prefill_pers<640>, dim3(W), block, 0, stream, a);
+      return launched("attn_prefill");
+    }
   }
-  const dim3 grid(nqb, splits, nkv), block(64 * (nh / nkv + PF_STAGERS));
+  // one workgroup per (query block, KV head) with all its keys
+  const dim3 grid(nqb, 1, nkv);
   if (block.x <= 512) hipLaunchKernelGGL(k_attn_prefill<512>, grid, block, 0, stream, a);
   else hipLaunchKernelGGL(k_attn_prefill<640>, grid, block, 0, stream, a);
   return launched("attn_prefill");

@@ -26,12 +26,14 @@ typedef float f4 __attribute__((ext_vector_type(4)));
 
 constexpr int KP = 2;              // KV pages per step of the key loop
 constexpr int FK_ROW = HD + 8;     // K row in LDS (halves), padded
-constexpr int FV_ROW = KP * PAGE + 4;   // Vt row (one dim, KP pages of keys) in LDS (halves), padded
+// V row (one key) in LDS (halves): rows 8 banks apart, so the four rows of a transposed read use disjoint banks
+constexpr int FV_ROW = HD + 16;
 
 __device__ __forceinline__ h8 as_h8(uint4 v) { return *reinterpret_cast<h8*>(&v); }
 
-// Scheduling of an unrolled run of N LDS operand reads feeding N MFMA groups (CBN MFMAs each): PF_DEPTH reads
-// first, then one MFMA group per further read, then the last groups (masks: 0x100 LDS read, 0x008 MFMA).
+// Scheduling of an unrolled run of N LDS operands (R reads each) feeding N MFMA groups (CBN MFMAs each):
+// PF_DEPTH operands first, then one MFMA group per further operand, then the last groups (masks: 0x100 LDS
+// read, 0x008 MFMA).
 // phase accounting hooks of the key loop: empty here; an instrumented build defines them
 #ifndef Q355_PF_PHASE
 #define Q355_PF_PHASE_INIT()
@@ -42,320 +44,424 @@ __device__ __forceinline__ h8 as_h8(uint4 v) { return *reinterpret_cast<h8*>(&v)
 #ifndef PF_DEPTH
 #define PF_DEPTH 8
 #endif
-#define Q355_PIPELINE(N)                                                                       \
+#define Q355_PIPELINE(N, R)  /* R LDS reads per operand */                                \
   do {                                                                                         \
-    __builtin_amdgcn_sched_group_barrier(0x100, PF_DEPTH, 0);                                  \
+    __builtin_amdgcn_sched_group_barrier(0x100, (R) * PF_DEPTH, 0);                            \
     _Pragma("unroll") for (int i_ = 0; i_ < (N) - PF_DEPTH; ++i_) {                            \
       __builtin_amdgcn_sched_group_barrier(0x008, CBN, 0);                                     \
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);                                       \
+      __builtin_amdgcn_sched_group_barrier(0x100, (R), 0);                                     \
     }                                                                                          \
     __builtin_amdgcn_sched_group_barrier(0x008, CBN * PF_DEPTH, 0);                            \
   } while (0)
 
 constexpr int CBN = PF_QB / 16;      // 16-query MFMA column blocks per wave
 
-// Workgroup = one KV head x 16 queries x one key split of up to 32 pages. Waves 0 .. G-1 are the head waves
-// (wave w: query head kvh * G + w), so each staged K/V page serves all G heads of the group; waves G and
-// G + 1 stage K and Vt into a double buffer: while the head waves compute step s from buffer s & 1, they write
-// step s + 1 into the other buffer and load step s + 2 into registers, so one barrier per step separates
-// the two roles and the head waves hold no staging registers. Wave tile: 16 queries (one MFMA column block).
-// grid (ceil(P / 16), max splits, nkv), the longest query blocks first; 64 (G + 2) threads. With several
-// splits, each writes its unnormalized O, m and l to the workspace; the last to arrive (counter per query
-// block and KV head, reset by it) merges them and writes the output. Partials and counters use
-// device-coherent accesses: the splits may run on different XCDs.
+static_assert(CBN == 1, "one 16-query MFMA column block per query block");
+
+// One key-loop step of a head wave over the staged pages kb, kb + 1: S^T = K Q^T, the online softmax (causal
+// mask on diagonal steps; queries past P need none: each query column of S, P and O is independent and is
+// never stored) and O^T += Vt P^T. Operand n of each product is read PF_DEPTH MFMAs ahead (Q355_PIPELINE).
+__device__ __forceinline__ void pf_consume(const _Float16 (&ks)[KP * PAGE][FK_ROW], const _Float16 (&vs)[KP * PAGE][FV_ROW],
+                                           const h8 (&qf)[4], int kb, int qpos, bool diag, float sl2, int li, int lg,
+                                           float& m, float& l, f4 (&acc)[8]) {
+  // S^T tiles: keys 16 t + (4 g + v), query li; operand n = (c, t), t fastest: 4 KP independent chains
+  f4 s[4 * KP];
+#pragma unroll
+  for (int t = 0; t < 4 * KP; ++t) s[t] = f4{0.f, 0.f, 0.f, 0.f};
+  {
+    constexpr int NS = 16 * KP;
+    h8 kA[NS];
+#pragma unroll
+    for (int n = 0; n < NS; ++n)
+      kA[n] = as_h8(*(const uint4*)&ks[16 * (n % (4 * KP)) + li][32 * (n / (4 * KP)) + 8 * lg]);
+#pragma unroll
+    for (int n = 0; n < NS; ++n)
+      s[n % (4 * KP)] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kA[n], qf[n / (4 * KP)], s[n % (4 * KP)], 0, 0, 0);
+    Q355_PIPELINE(NS, 1);
+  }
+  h8 pB[2 * KP];
+  if (diag) {
+#pragma unroll
+    for (int t = 0; t < 4 * KP; ++t)
+#pragma unroll
+      for (int v = 0; v < 4; ++v)
+        if (kb * PAGE + 16 * t + 4 * lg + v > qpos) s[t][v] = -INFINITY;
+  }
+  float bm = -INFINITY;                                  // raw-score max; scaled once below
+#pragma unroll
+  for (int t = 0; t < 4 * KP; ++t) bm = fmaxf(bm, fmaxf(fmaxf(s[t][0], s[t][1]), fmaxf(s[t][2], s[t][3])));
+  bm = col4_max(bm);
+  const float mn = fmaxf(m, bm * sl2);
+  const float ms = mn == -INFINITY ? 0.f : mn;           // fully masked so far: keep exp2 finite
+  const float alpha = __builtin_amdgcn_exp2f(m - ms);
+  float rs = 0.f;
+#pragma unroll
+  for (int t = 0; t < 4 * KP; ++t)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const float p = __builtin_amdgcn_exp2f(fmaf(s[t][v], sl2, -ms));
+      rs += p;
+      pB[t >> 1][4 * (t & 1) + v] = (_Float16)p;
+    }
+  rs = col4_sum(rs);
+  l = l * alpha + rs;
+  m = mn;
+  if (__any(alpha != 1.f)) {                             // the running max moved for some query of the wave
+#pragma unroll
+    for (int t = 0; t < 8; ++t) acc[t] *= alpha;
+  }
+  // O^T += Vt P^T over 2 KP 32-key chunks; operand n = (c, dt), dt fastest
+  {
+    constexpr int NV = 16 * KP;
+    // A operand of chunk c, dim tile dt: keys 32 c + 4 lg + (0..3) and 32 c + 16 + 4 lg + (0..3) of dim 16 dt + li,
+    // two transposed reads (ds_read_b64_tr_b16: lane j of a 16-lane group receives element j % 4 of the 4-value
+    // segments named by lanes j / 4 + 4 k, k = 0..3; here lane x names key 4 lg + x / 4, dims 4 (x % 4) ..)
+    h8 vA[NV];
+#pragma unroll
+    for (int n = 0; n < NV; ++n) {
+      const _Float16* seg = &vs[32 * (n / 8) + 4 * lg + (li >> 2)][16 * (n % 8) + 4 * (li & 3)];
+      typedef short s4 __attribute__((ext_vector_type(4)));
+      typedef __attribute__((address_space(3))) s4* lds_s4;
+      const s4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4)(seg));
+      const s4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4)(seg + 16 * FV_ROW));
+      const uint2 l2 = __builtin_bit_cast(uint2, lo), h2 = __builtin_bit_cast(uint2, hi);
+      vA[n] = as_h8(make_uint4(l2.x, l2.y, h2.x, h2.y));
+    }
+#pragma unroll
+    for (int n = 0; n < NV; ++n)
+      acc[n % 8] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vA[n], pB[n / 8], acc[n % 8], 0, 0, 0);
+    Q355_PIPELINE(NV, 2);
+  }
+}
+
+// The normalized output of query qi, head hq: fp32, or Q8_1 for the O projection (the values the fp32 path
+// stores, quantized as q355_quant_q8_1 does): block bk = dims 32 bk .. 32 bk + 31 lives in tiles dt = 2 bk,
+// 2 bk + 1 of the 4 lanes li + 16 g.
+__device__ __forceinline__ void pf_out(const PrefillAttnArgs& a, int qi, int hq, int lg, const f4 (&acc)[8], float l) {
+  const int nq = a.nh * HD;
+  const float inv = 1.f / l;
+  if (a.oq) {
+#pragma unroll
+    for (int bk = 0; bk < 4; ++bk) {
+      float x[2][4];
+      float amax = 0.f;
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          x[h][v] = acc[2 * bk + h][v] * inv;
+          amax = fmaxf(amax, fabsf(x[h][v]));
+        }
+      amax = col4_max(amax);
+      const float d32 = q8_scale(amax);
+      int sq = 0;
+      unsigned pk[2];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        pk[h] = 0;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const int q = q8_code(x[h][v], d32);
+          sq += q;
+          pk[h] |= (unsigned)(q & 255) << (8 * v);
+        }
+      }
+      sq = col4_isum(sq);
+      if (qi < a.P) {
+        int8_t* o = a.oq + (size_t)qi * nq + hq * HD;
+        *(unsigned*)(o + 32 * bk + 4 * lg) = pk[0];
+        *(unsigned*)(o + 32 * bk + 16 + 4 * lg) = pk[1];
+        if (lg == 0)
+          a.ods[((size_t)qi * nq + hq * HD) / 32 + bk] = __halves2half2(__float2half_rn(d32), q8_s16(d32, sq));
+      }
+    }
+  } else if (qi < a.P) {
+    float* o = a.out + (size_t)qi * nq + hq * HD;
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt)
+      *(float4*)(o + 16 * dt + 4 * lg) =
+          make_float4(acc[dt][0] * inv, acc[dt][1] * inv, acc[dt][2] * inv, acc[dt][3] * inv);
+  }
+}
+
+// Staging registers of one step (two pages) for the staging waves (thread st = 0 .. 64 PF_STAGERS - 1 of them):
+// K and V each as 1024 16 B pieces per page (key e / 16, dims 8 (e % 16) ..), stored key-major (16-byte
+// loads keep a wave's loads of a step within the 63 it can have in flight).
+constexpr int PF_KPS = 1024 / (64 * PF_STAGERS);
+struct PfStage {
+  u32x4 kr[KP][PF_KPS];
+  u32x4 vr[KP][PF_KPS];
+};
+__device__ __forceinline__ void pf_stage_load(PfStage& r, const PrefillAttnArgs& a, int kvh, int pg0, int pg1, int st) {
+#pragma unroll
+  for (int p = 0; p < KP; ++p) {
+    const size_t off = ((size_t)(p ? pg1 : pg0) * a.nkv + kvh) * PAGE * HD;
+    const u32x4* kp = (const u32x4*)(a.kcache + off);
+    const u32x4* vp = (const u32x4*)(a.vcache + off);
+#pragma unroll
+    for (int i = 0; i < PF_KPS; ++i) r.kr[p][i] = kp[st + 64 * PF_STAGERS * i];
+#pragma unroll
+    for (int i = 0; i < PF_KPS; ++i) r.vr[p][i] = vp[st + 64 * PF_STAGERS * i];
+  }
+}
+__device__ __forceinline__ void pf_stage_store(const PfStage& r, _Float16 (&ks)[KP * PAGE][FK_ROW],
+                                               _Float16 (&vs)[KP * PAGE][FV_ROW], int st) {
+#pragma unroll
+  for (int p = 0; p < KP; ++p)
+#pragma unroll
+    for (int i = 0; i < PF_KPS; ++i) {
+      const int e = st + 64 * PF_STAGERS * i;
+      *(u32x4*)&ks[p * PAGE + (e >> 4)][(e & 15) * 8] = r.kr[p][i];
+      *(u32x4*)&vs[p * PAGE + (e >> 4)][(e & 15) * 8] = r.vr[p][i];
+    }
+}
+// the 16 queries of block qb for head hq (rows past P repeat the last; they are never stored)
+__device__ __forceinline__ void pf_load_q(h8 (&qf)[4], const PrefillAttnArgs& a, int qb, int hq, int li, int lg) {
+  const int qc = min(qb * PF_QB + li, a.P - 1);
+#pragma unroll
+  for (int c = 0; c < 4; ++c)
+    qf[c] = as_h8(*(const uint4*)(a.q + (size_t)qc * a.nh * HD + hq * HD + 32 * c + 8 * lg));
+}
+
+// Workgroup = one KV head x 16 queries x all their keys (the form without a workspace). Waves 0 .. G-1 are
+// the head waves (wave w: query head kvh * G + w), so each staged K/V page serves all G heads of the group;
+// waves G and G + 1 stage K and Vt into a double buffer: while the head waves compute step s from buffer
+// s & 1, they write step s + 1 into the other buffer and load step s + 2 into registers, so one barrier per
+// step separates the two roles and the head waves hold no staging registers. grid (ceil(P / 16), 1, nkv),
+// the longest query blocks first; 64 (G + 2) threads.
 // NT: the launch's thread bound (512 up to G = 6: two waves per SIMD, 256 VGPRs; 640 for G = 7, 8)
 template <int NT>
 __global__ void __launch_bounds__(NT) k_attn_prefill(const PrefillAttnArgs a) {
   __shared__ __align__(16) _Float16 ks[2][KP * PAGE][FK_ROW];
-  __shared__ __align__(16) _Float16 vt[2][HD][FV_ROW];
+  __shared__ __align__(16) _Float16 vs[2][KP * PAGE][FV_ROW];
+  __shared__ int pages[64];
   const int G = a.nh / a.nkv;
-  const int qb = gridDim.x - 1 - blockIdx.x, split = blockIdx.y, kvh = blockIdx.z;
-  const int nsplit = a.ws ? pf_splits(a.pos0, qb, a.P) : 1;
-  if (split >= nsplit) return;                           // uniform per workgroup
+  const int qb = gridDim.x - 1 - blockIdx.x, kvh = blockIdx.z;
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int li = lane & 15, lg = lane >> 4;
-  const bool stager = wv >= G;
-  const int hq = kvh * G + min(wv, G - 1);
-  const int nq = a.nh * HD;
-
-  int qi[CBN], qpos[CBN];
-  h8 qf[CBN][4];
-#pragma unroll
-  for (int cb = 0; cb < CBN; ++cb) {
-    qi[cb] = qb * PF_QB + 16 * cb + li;
-    qpos[cb] = a.pos0 + qi[cb];
-    const int qc = min(qi[cb], a.P - 1);
-    if (!stager)
-#pragma unroll
-      for (int c = 0; c < 4; ++c)
-        qf[cb][c] = as_h8(*(const uint4*)(a.q + (size_t)qc * nq + hq * HD + 32 * c + 8 * lg));
-  }
-
-  const int last_key = min(a.pos0 + qb * PF_QB + PF_QB - 1, a.pos0 + a.P - 1);
-  const int kb0 = a.ws ? split * PF_SPLIT_PAGES : 0;
-  const int nkb = a.ws ? min(last_key / PAGE + 1, kb0 + PF_SPLIT_PAGES) : last_key / PAGE + 1;
+  const int nkb = pf_pages(a.pos0, qb, a.P);
   const float sl2 = a.scale * 1.4426950408889634f;       // scores in log2 units
-
-  // staging (the two staging waves, thread st = 0..127): K as 1024 16 B pieces per page (key e / 16, dims
-  // 8 (e % 16) ..); V transposed: lane l of staging wave sw takes dims 2l, 2l + 1 of the 8-key groups sw,
-  // sw + 2, ...: 8 dword loads per group, packed into two 16 B rows
-  constexpr int KPS = 1024 / (64 * PF_STAGERS), VPS = 8 / PF_STAGERS;
-  const int st = threadIdx.x - 64 * G, sw = wv - G;
-  u32x4 kr[KP][KPS];
-  unsigned vr[KP][VPS][8];
-  // the page ids of this workgroup's key range, read once (each page's loads then wait on one latency)
-  __shared__ int pages[64];
-  for (int i = threadIdx.x; i < nkb - kb0 && i < 64; i += blockDim.x) pages[i] = a.block_table[kb0 + i];
+  for (int i = threadIdx.x; i < nkb && i < 64; i += blockDim.x) pages[i] = a.block_table[i];
   __syncthreads();
-#define Q355_LOAD_PAGE(kb)                                                                     \
-  _Pragma("unroll") for (int p_ = 0; p_ < KP; ++p_) {                                          \
-    const int kbp_ = min((kb) + p_, nkb - 1);   /* past the range: a repeat, masked (diag step) */ \
-    const int pg_ = kbp_ - kb0 < 64 ? pages[kbp_ - kb0] : a.block_table[kbp_];                 \
-    const u32x4* kp_ = (const u32x4*)(a.kcache + ((size_t)pg_ * a.nkv + kvh) * PAGE * HD);     \
-    const unsigned* vp_ = (const unsigned*)(a.vcache + ((size_t)pg_ * a.nkv + kvh) * PAGE * HD); \
-    _Pragma("unroll") for (int i = 0; i < KPS; ++i) kr[p_][i] = kp_[st + 64 * PF_STAGERS * i]; \
-    _Pragma("unroll") for (int i = 0; i < VPS; ++i) {                                          \
-      const int kg = sw + PF_STAGERS * i;                                                      \
-      _Pragma("unroll") for (int u = 0; u < 8; ++u) vr[p_][i][u] = vp_[(kg * 8 + u) * (HD / 2) + lane]; \
-    }                                                                                          \
-  }
-#define Q355_STORE_PAGE(bf)                                                                    \
-  _Pragma("unroll") for (int p_ = 0; p_ < KP; ++p_) {                                          \
-    _Pragma("unroll") for (int i = 0; i < KPS; ++i) {                                          \
-      const int e = st + 64 * PF_STAGERS * i;                                                  \
-      *(u32x4*)&ks[bf][p_ * PAGE + (e >> 4)][(e & 15) * 8] = kr[p_][i];                        \
-    }                                                                                          \
-    _Pragma("unroll") for (int i = 0; i < VPS; ++i) {                                          \
-      const int kg = sw + PF_STAGERS * i;                                                      \
-      u32x4 lo, hi;                                                                            \
-      _Pragma("unroll") for (int j = 0; j < 4; ++j) {                                          \
-        lo[j] = __builtin_amdgcn_perm(vr[p_][i][2 * j + 1], vr[p_][i][2 * j], 0x05040100u);    \
-        hi[j] = __builtin_amdgcn_perm(vr[p_][i][2 * j + 1], vr[p_][i][2 * j], 0x07060302u);    \
-      }                                                                                        \
-      *(u32x4*)&vt[bf][2 * lane][p_ * PAGE + kg * 8] = lo;                                     \
-      *(u32x4*)&vt[bf][2 * lane + 1][p_ * PAGE + kg * 8] = hi;                                 \
-    }                                                                                          \
-  }
-
-  float m[CBN], l[CBN];
-  f4 acc[CBN][8];
-#pragma unroll
-  for (int cb = 0; cb < CBN; ++cb) {
-    m[cb] = -INFINITY;
-    l[cb] = 0.f;
-#pragma unroll
-    for (int t = 0; t < 8; ++t) acc[cb][t] = f4{0.f, 0.f, 0.f, 0.f};
-  }
-
-  if (stager) {                                            // the staging waves' own loop, same barriers
-    Q355_LOAD_PAGE(kb0);
-    Q355_STORE_PAGE(0);
-    if (kb0 + KP < nkb) Q355_LOAD_PAGE(kb0 + KP);
+  // page ids (a step's second page past the range repeats the last: masked on the diagonal step)
+  auto pg = [&](int kb) { return kb < 64 ? pages[kb] : a.block_table[kb]; };
+  if (wv >= G) {                                         // the staging waves' own loop, same barriers
+    const int st = threadIdx.x - 64 * G;
+    PfStage r;
+    pf_stage_load(r, a, kvh, pg(0), pg(min(1, nkb - 1)), st);
+    pf_stage_store(r, ks[0], vs[0], st);
+    if (KP < nkb) pf_stage_load(r, a, kvh, pg(KP), pg(min(KP + 1, nkb - 1)), st);
     __syncthreads();
-    for (int kb = kb0, bf = 0; kb < nkb; kb += KP, bf ^= 1) {
-      if (kb + KP < nkb) {                                 // uniform
-        Q355_STORE_PAGE(bf ^ 1);
-        if (kb + 2 * KP < nkb) Q355_LOAD_PAGE(kb + 2 * KP);
+    for (int kb = 0, bf = 0; kb < nkb; kb += KP, bf ^= 1) {
+      if (kb + KP < nkb) {                               // uniform
+        pf_stage_store(r, ks[bf ^ 1], vs[bf ^ 1], st);
+        if (kb + 2 * KP < nkb) pf_stage_load(r, a, kvh, pg(kb + 2 * KP), pg(min(kb + 2 * KP + 1, nkb - 1)), st);
       }
-      __syncthreads();
-    }
-    if (nsplit > 1) {                                      // the split merge's two barriers
-      __syncthreads();
       __syncthreads();
     }
     return;
   }
+  const int hq = kvh * G + wv;
+  h8 qf[4];
+  pf_load_q(qf, a, qb, hq, li, lg);
+  float m = -INFINITY, l = 0.f;
+  f4 acc[8];
+#pragma unroll
+  for (int t = 0; t < 8; ++t) acc[t] = f4{0.f, 0.f, 0.f, 0.f};
+  const int qpos = a.pos0 + qb * PF_QB + li;
   __syncthreads();
   Q355_PF_PHASE_INIT();
-  for (int kb = kb0, bf = 0; kb < nkb; kb += KP, bf ^= 1) {
+  for (int kb = 0, bf = 0; kb < nkb; kb += KP, bf ^= 1) {
     Q355_PF_PHASE(0);
-    // S^T tiles: keys 16t + (4g + v), query li of column block cb; each K operand feeds both blocks
-    // operand n = (c, t), t fastest: 4 KP independent accumulator chains; the schedule keeps PF_DEPTH LDS
-    // reads in flight ahead of the MFMAs (left to itself the compiler issues one or two)
-    f4 s[CBN][4 * KP];
-#pragma unroll
-    for (int t = 0; t < 4 * KP; ++t)
-#pragma unroll
-      for (int cb = 0; cb < CBN; ++cb) s[cb][t] = f4{0.f, 0.f, 0.f, 0.f};
-    {
-      constexpr int NS = 16 * KP;
-      h8 kA[NS];
-#pragma unroll
-      for (int n = 0; n < NS; ++n)
-        kA[n] = as_h8(*(const uint4*)&ks[bf][16 * (n % (4 * KP)) + li][32 * (n / (4 * KP)) + 8 * lg]);
-#pragma unroll
-      for (int n = 0; n < NS; ++n)
-#pragma unroll
-        for (int cb = 0; cb < CBN; ++cb)
-          s[cb][n % (4 * KP)] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kA[n], qf[cb][n / (4 * KP)], s[cb][n % (4 * KP)], 0, 0, 0);
-      Q355_PIPELINE(NS);
-    }
-    Q355_PF_PHASE(3);
-    h8 pB[CBN][2 * KP];
     // causal mask only where the step reaches past the block's first query (uniform; this includes the step
-    // with a repeated page past the range); queries past P need none: each query column of S, P and O is
-    // independent and is never stored
+    // with a repeated page past the range)
     const bool diag = (kb + KP) * PAGE - 1 > a.pos0 + qb * PF_QB;
-#pragma unroll
-    for (int cb = 0; cb < CBN; ++cb) {
-      if (diag) {
-#pragma unroll
-        for (int t = 0; t < 4 * KP; ++t)
-#pragma unroll
-          for (int v = 0; v < 4; ++v)
-            if (kb * PAGE + 16 * t + 4 * lg + v > qpos[cb]) s[cb][t][v] = -INFINITY;
-      }
-      float bm = -INFINITY;                                // raw-score max; scaled once below
-#pragma unroll
-      for (int t = 0; t < 4 * KP; ++t) bm = fmaxf(bm, fmaxf(fmaxf(s[cb][t][0], s[cb][t][1]), fmaxf(s[cb][t][2], s[cb][t][3])));
-      bm = col4_max(bm);
-      const float mn = fmaxf(m[cb], bm * sl2);
-      const float ms = mn == -INFINITY ? 0.f : mn;         // fully masked so far: keep exp2 finite
-      const float alpha = __builtin_amdgcn_exp2f(m[cb] - ms);
-      float rs = 0.f;
-#pragma unroll
-      for (int t = 0; t < 4 * KP; ++t)
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          const float p = __builtin_amdgcn_exp2f(fmaf(s[cb][t][v], sl2, -ms));
-          rs += p;
-          pB[cb][t >> 1][4 * (t & 1) + v] = (_Float16)p;
-        }
-      rs = col4_sum(rs);
-      l[cb] = l[cb] * alpha + rs;
-      m[cb] = mn;
-      if (__any(alpha != 1.f)) {                           // the running max moved for some query of the wave
-#pragma unroll
-        for (int t = 0; t < 8; ++t) acc[cb][t] *= alpha;
-      }
-    }
-    // O^T += Vt P^T over 2 KP 32-key chunks; each Vt operand feeds every block
-    Q355_PF_PHASE(4);
-    {
-      constexpr int NV = 16 * KP;                          // operand n = (c, dt), dt fastest
-      h8 vA[NV];
-#pragma unroll
-      for (int n = 0; n < NV; ++n) {
-        const _Float16* row = &vt[bf][16 * (n % 8) + li][32 * (n / 8)];
-        const uint2 lo = *(const uint2*)(row + 4 * lg);
-        const uint2 hi = *(const uint2*)(row + 16 + 4 * lg);
-        vA[n] = as_h8(make_uint4(lo.x, lo.y, hi.x, hi.y));
-      }
-#pragma unroll
-      for (int n = 0; n < NV; ++n)
-#pragma unroll
-        for (int cb = 0; cb < CBN; ++cb)
-          acc[cb][n % 8] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vA[n], pB[cb][n / 8], acc[cb][n % 8], 0, 0, 0);
-      Q355_PIPELINE(NV);
-    }
+    pf_consume(ks[bf], vs[bf], qf, kb, qpos, diag, sl2, li, lg, m, l, acc);
     Q355_PF_PHASE(5);
-    __syncthreads();                                       // this buffer is free; the next one is staged
+    __syncthreads();                                     // this buffer is free; the next one is staged
   }
   Q355_PF_PHASE_END();
-#undef Q355_LOAD_PAGE
-#undef Q355_STORE_PAGE
-  if (nsplit > 1) {
-    // partial -> workspace (same lane order on both sides), then arrival count
-    const size_t slot = (((size_t)qb * a.nkv + kvh) * a.max_splits + split) * G + wv;
-    float4* po = (float4*)a.ws + slot * (CBN * 8 * 64);
-    float* pml = a.ws + (size_t)gridDim.x * a.nkv * a.max_splits * G * (CBN * 8 * 64 * 4) + slot * (CBN * 16 * 2);
-#pragma unroll
-    for (int cb = 0; cb < CBN; ++cb) {
-#pragma unroll
-      for (int dt = 0; dt < 8; ++dt)
-#pragma unroll
-        for (int v = 0; v < 4; ++v) stc((float*)&po[(cb * 8 + dt) * 64 + lane] + v, acc[cb][dt][v]);
-      if (lg == 0) {
-        stc(pml + (cb * 16 + li) * 2, m[cb]);
-        stc(pml + (cb * 16 + li) * 2 + 1, l[cb]);
+  pf_out(a, qb * PF_QB + li, hq, lg, acc, l);
+}
+
+// The persistent form (with a workspace): gridDim.x workgroups of G head waves and PF_STAGERS staging waves,
+// each walking its items -- (query block, KV head, key split of PF_SPLIT_PAGES pages) -- as one sequence of
+// two-page steps, so the staging waves load across item boundaries and the causal rows are balanced over the
+// CUs. Items are numbered split-major, query blocks longest first, then KV head; workgroup w takes item
+// r W + w in even rounds r and r W + W - 1 - w in odd ones (W = gridDim.x), at most PF_MAX_ROUNDS.
+// A split item writes its unnormalized O, m and l to the workspace with device-coherent stores (the splits
+// may run on other XCDs) and goes on to the next item without waiting for them. After its last step each
+// head wave waits once for its stores and counts all its split items at once, per (query block, KV head,
+// head); the last to arrive merges every split of its head in split order (so the result does not depend on
+// arrival order), writes the output and resets its counter.
+template <int NT>
+__global__ void __launch_bounds__(NT) k_attn_prefill_pers(const PrefillAttnArgs a) {
+  __shared__ __align__(16) _Float16 ks[2][KP * PAGE][FK_ROW];
+  __shared__ __align__(16) _Float16 vs[2][KP * PAGE][FV_ROW];
+  __shared__ int4 items[PF_MAX_ROUNDS];                  // (qb, kvh, kb0 | nkb << 16, nsplit | split << 16)
+  __shared__ int4 steps[PF_MAX_ROUNDS * PF_SPLIT_PAGES / KP];   // (item, kb, page kb, page kb + 1 in range)
+  __shared__ int nstep_s, nitem_s;
+  const int G = a.nh / a.nkv;
+  const int nqb = (a.P + PF_QB - 1) / PF_QB;
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int li = lane & 15, lg = lane >> 4;
+  const float sl2 = a.scale * 1.4426950408889634f;
+
+  // this workgroup's items (wave 0, lane r = round r) and their steps
+  if (wv == 0) {
+    const int W = gridDim.x, w = blockIdx.x, r = lane;
+    int c = r * W + ((r & 1) ? W - 1 - w : w);
+    int ns = 0;
+    int4 it = make_int4(0, 0, 0, 0);
+    if (c < a.n_items) {
+      int sp = 0, q0 = pf_qmin(a.pos0, a.P, 0);
+      while (c >= (nqb - q0) * a.nkv) {                  // the split this item belongs to
+        c -= (nqb - q0) * a.nkv;
+        q0 = pf_qmin(a.pos0, a.P, ++sp);
       }
+      const int qb = nqb - 1 - c / a.nkv, kvh = c % a.nkv;
+      const int L = pf_pages(a.pos0, qb, a.P);
+      const int kb0 = sp * PF_SPLIT_PAGES, nkb = min(L, kb0 + PF_SPLIT_PAGES);
+      it = make_int4(qb, kvh, kb0 | (nkb << 16), ((L - 1) / PF_SPLIT_PAGES + 1) | (sp << 16));
+      ns = (nkb - kb0 + KP - 1) / KP;
     }
-    __builtin_amdgcn_s_waitcnt(0);                         // this wave's coherent stores have completed
-    __syncthreads();
-    __shared__ int last;
-    int* cnt = (int*)(a.ws + pf_ws_floats(gridDim.x, a.nkv, G, a.max_splits) - (size_t)gridDim.x * a.nkv) +
-               qb * a.nkv + kvh;
-    if (threadIdx.x == 0) {
-      last = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == nsplit - 1;
-      if (last) stc(cnt, 0);                             // every split has arrived: ready for the next call
+    int incl = ns;                                       // inclusive prefix of the step counts
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int t = __shfl_up(incl, o);
+      if (lane >= o) incl += t;
     }
-    __syncthreads();
-    if (!last) return;
-    // merge: rescale every split to the common max
-    const size_t slot0 = (((size_t)qb * a.nkv + kvh) * a.max_splits) * G + wv;
-    const float4* pa = (const float4*)a.ws + slot0 * (CBN * 8 * 64);   // read with coherent loads
-    const float* pmla = a.ws + (size_t)gridDim.x * a.nkv * a.max_splits * G * (CBN * 8 * 64 * 4) + slot0 * (CBN * 16 * 2);
-#pragma unroll
-    for (int cb = 0; cb < CBN; ++cb) {
-      float mt = m[cb];
-      for (int s2 = 0; s2 < nsplit; ++s2)
-        if (s2 != split) mt = fmaxf(mt, ldc(pmla + (size_t)s2 * G * (CBN * 32) + (cb * 16 + li) * 2));
-      const float f0 = __builtin_amdgcn_exp2f(m[cb] - mt);
-      l[cb] *= f0;
-#pragma unroll
-      for (int dt = 0; dt < 8; ++dt) acc[cb][dt] *= f0;
-      for (int s2 = 0; s2 < nsplit; ++s2) {
-        if (s2 == split) continue;
-        const float* ml = pmla + (size_t)s2 * G * (CBN * 32) + (cb * 16 + li) * 2;
-        const float f = __builtin_amdgcn_exp2f(ldc(ml) - mt);
-        l[cb] += f * ldc(ml + 1);
-        const float4* src = pa + (size_t)s2 * G * (CBN * 8 * 64) + cb * 8 * 64 + lane;
-#pragma unroll
-        for (int dt = 0; dt < 8; ++dt) {
-#pragma unroll
-          for (int v = 0; v < 4; ++v) acc[cb][dt][v] += f * ldc((const float*)&src[dt * 64] + v);
-        }
-      }
+    items[r] = it;
+    for (int k = 0; k < ns; ++k) steps[incl - ns + k] = make_int4(r, (it.z & 0xffff) + KP * k, 0, 0);
+    const unsigned long long live = __ballot(ns > 0);
+    if (lane == 63) {
+      nstep_s = incl;
+      nitem_s = __popcll(live);
     }
   }
-#pragma unroll
-  for (int cb = 0; cb < CBN; ++cb) {
-    const float inv = 1.f / l[cb];
-    if (a.oq) {
-      // Q8_1 of the output row (the values the fp32 path stores, quantized as q355_quant_q8_1 does): block
-      // bk = dims 32 bk .. 32 bk + 31 lives in tiles dt = 2 bk, 2 bk + 1 of the 4 lanes li + 16 g
-#pragma unroll
-      for (int bk = 0; bk < 4; ++bk) {
-        float x[2][4];
-        float amax = 0.f;
-#pragma unroll
-        for (int h = 0; h < 2; ++h)
-#pragma unroll
-          for (int v = 0; v < 4; ++v) {
-            x[h][v] = acc[cb][2 * bk + h][v] * inv;
-            amax = fmaxf(amax, fabsf(x[h][v]));
-          }
-        amax = col4_max(amax);
-        const float d32 = q8_scale(amax);
-        int sq = 0;
-        unsigned pk[2];
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          pk[h] = 0;
-#pragma unroll
-          for (int v = 0; v < 4; ++v) {
-            const int q = q8_code(x[h][v], d32);
-            sq += q;
-            pk[h] |= (unsigned)(q & 255) << (8 * v);
-          }
-        }
-        sq = col4_isum(sq);
-        if (qi[cb] < a.P) {
-          int8_t* o = a.oq + (size_t)qi[cb] * nq + hq * HD;
-          *(unsigned*)(o + 32 * bk + 4 * lg) = pk[0];
-          *(unsigned*)(o + 32 * bk + 16 + 4 * lg) = pk[1];
-          if (lg == 0)
-            a.ods[((size_t)qi[cb] * nq + hq * HD) / 32 + bk] = __halves2half2(__float2half_rn(d32), q8_s16(d32, sq));
-        }
+  __syncthreads();
+  const int nst = nstep_s, nit = nitem_s;
+  for (int e = threadIdx.x; e < nst; e += blockDim.x) {  // the page ids of every step (one latency for all)
+    int4 st = steps[e];
+    const int nkb = items[st.x].z >> 16;
+    st.z = a.block_table[st.y];
+    st.w = a.block_table[min(st.y + 1, nkb - 1)];       // past the range: a repeat, masked (diagonal step)
+    steps[e] = st;
+  }
+  __syncthreads();
+
+  if (wv >= G) {                                         // staging waves: same barriers as the head waves
+    const int st = threadIdx.x - 64 * G;
+    PfStage r;
+    if (nst > 0) {
+      pf_stage_load(r, a, items[steps[0].x].y, steps[0].z, steps[0].w, st);
+      pf_stage_store(r, ks[0], vs[0], st);
+      if (nst > 1) pf_stage_load(r, a, items[steps[1].x].y, steps[1].z, steps[1].w, st);
+    }
+    __syncthreads();
+    Q355_PF_PHASE_INIT();
+    for (int g = 0; g < nst; ++g) {
+      Q355_PF_PHASE(0);
+      if (g + 1 < nst) {
+        pf_stage_store(r, ks[(g + 1) & 1], vs[(g + 1) & 1], st);
+        Q355_PF_PHASE(2);
+        if (g + 2 < nst) pf_stage_load(r, a, items[steps[g + 2].x].y, steps[g + 2].z, steps[g + 2].w, st);
       }
-    } else if (qi[cb] < a.P) {
-      float* o = a.out + (size_t)qi[cb] * nq + hq * HD;
+      Q355_PF_PHASE(3);
+      __syncthreads();
+    }
+    Q355_PF_PHASE_END();
+    return;
+  }
+
+  h8 qf[4], qn[4];                                       // this item's queries and the next item's
+  if (nit > 0) pf_load_q(qf, a, items[0].x, items[0].y * G + wv, li, lg);
+  if (nit > 1) pf_load_q(qn, a, items[1].x, items[1].y * G + wv, li, lg);
+  float m = -INFINITY, l = 0.f;
+  f4 acc[8];
+  __syncthreads();
+  Q355_PF_PHASE_INIT();
+  for (int g = 0; g < nst; ++g) {
+    Q355_PF_PHASE(0);
+    const int4 st = steps[g];
+    const int4 it = items[st.x];
+    const int qb = it.x, kvh = it.y, kb0 = it.z & 0xffff, nkb = it.z >> 16;
+    if (st.y == kb0) {                                   // the item's first step
+      if (st.x > 0) {
 #pragma unroll
-      for (int dt = 0; dt < 8; ++dt)
-        *(float4*)(o + 16 * dt + 4 * lg) = make_float4(acc[cb][dt][0] * inv, acc[cb][dt][1] * inv,
-                                                       acc[cb][dt][2] * inv, acc[cb][dt][3] * inv);
+        for (int c = 0; c < 4; ++c) qf[c] = qn[c];
+        if (st.x + 1 < nit) pf_load_q(qn, a, items[st.x + 1].x, items[st.x + 1].y * G + wv, li, lg);
+      }
+      m = -INFINITY;
+      l = 0.f;
+#pragma unroll
+      for (int t = 0; t < 8; ++t) acc[t] = f4{0.f, 0.f, 0.f, 0.f};
+    }
+    const bool diag = (st.y + KP) * PAGE - 1 > a.pos0 + qb * PF_QB;
+    pf_consume(ks[g & 1], vs[g & 1], qf, st.y, a.pos0 + qb * PF_QB + li, diag, sl2, li, lg, m, l, acc);
+    Q355_PF_PHASE(5);
+    if (st.y + KP >= nkb) {                              // the item's last step
+      const int nsplit = it.w & 0xffff, sp = it.w >> 16;
+      const int hq = kvh * G + wv;
+      if (nsplit == 1) {
+        pf_out(a, qb * PF_QB + li, hq, lg, acc, l);
+      } else {
+        // this (query block, KV head)'s partials: [max_splits][G][8][64] float4 and (m, l, -, -) [max_splits][G][16]
+        const size_t row = (size_t)qb * a.nkv + kvh;
+        const int per = a.max_splits * G;
+        const Coh16 PO((const float4*)a.ws + row * per * 512, (unsigned)per * 512 * 16);
+        const Coh16 PM((const float4*)a.ws + (size_t)nqb * a.nkv * per * 512 + row * per * 16, (unsigned)per * 16 * 16);
+        const unsigned own = (unsigned)(sp * G + wv);
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt) PO.st16(((own * 512) + dt * 64 + lane) * 16, __builtin_bit_cast(int4, acc[dt]));
+        if (lg == 0) PM.st16((own * 16 + li) * 16, __builtin_bit_cast(int4, make_float4(m, l, 0.f, 0.f)));
+      }
+    }
+    Q355_PF_PHASE(1);
+    __syncthreads();                                     // this buffer is free; the next one is staged
+  }
+  // arrivals of this wave's split items, all at once (lane r: item r) after one wait for its partial stores;
+  // the last split of a head to arrive merges every split of it in split order and writes the output
+  __builtin_amdgcn_s_waitcnt(0);                         // this wave's coherent stores have completed
+  int* cnt0 = (int*)(a.ws + pf_ws_floats(nqb, a.nkv, G, a.max_splits) - (size_t)nqb * a.nkv * G);
+  bool merge = false;
+  if (lane < nit) {
+    const int4 it = items[lane];
+    const int nsplit = it.w & 0xffff;
+    if (nsplit > 1) {
+      int* cnt = cnt0 + ((size_t)it.x * a.nkv + it.y) * G + wv;
+      merge = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == nsplit - 1;
+      if (merge) stc(cnt, 0);                            // every split has arrived: ready for the next call
     }
   }
+  for (unsigned long long mb = __ballot(merge); mb; mb &= mb - 1) {
+    const int4 it = items[__builtin_ctzll(mb)];
+    const int qb = it.x, kvh = it.y, nsplit = it.w & 0xffff;
+    const size_t row = (size_t)qb * a.nkv + kvh;
+    const int per = a.max_splits * G;
+    const Coh16 PO((const float4*)a.ws + row * per * 512, (unsigned)per * 512 * 16);
+    const Coh16 PM((const float4*)a.ws + (size_t)nqb * a.nkv * per * 512 + row * per * 16, (unsigned)per * 16 * 16);
+    float mt = -INFINITY;
+    for (int s2 = 0; s2 < nsplit; ++s2)
+      mt = fmaxf(mt, __builtin_bit_cast(float4, PM.ld((((unsigned)(s2 * G + wv)) * 16 + li) * 16)).x);
+    float lt = 0.f;
+    f4 o[8];
+#pragma unroll
+    for (int t = 0; t < 8; ++t) o[t] = f4{0.f, 0.f, 0.f, 0.f};
+    for (int s2 = 0; s2 < nsplit; ++s2) {
+      const unsigned sl = (unsigned)(s2 * G + wv);
+      int4 v[8];
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) v[dt] = PO.ld((sl * 512 + dt * 64 + lane) * 16);
+      const float4 ml = __builtin_bit_cast(float4, PM.ld((sl * 16 + li) * 16));
+      const float f = __builtin_amdgcn_exp2f(ml.x - mt);
+      lt += f * ml.y;
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) o[dt] += f * __builtin_bit_cast(f4, v[dt]);
+    }
+    pf_out(a, qb * PF_QB + li, kvh * G + wv, lg, o, lt);
+  }
+  Q355_PF_PHASE_END();
 }
 
 }  // namespace q355

@@ -102,23 +102,42 @@ struct PrefillAttnArgs {
   float* out;                  // [P][nh*HD] fp32, or (oq set) instead:
   int8_t* oq;                  // Q8_1 of the output [P][nh*HD] int8 and
   half2* ods;                  //   [P][nh*HD/32] (d, d * sum q)
-  // split over keys (null: one workgroup per query block takes all its keys): partials
-  // [n_qblocks][nkv][max_splits][G][CBN][8][64] float4 (O^T in MFMA accumulator order), m / l
-  // [n_qblocks][nkv][max_splits][G][CBN][16][2], arrival counters [n_qblocks][nkv]
+  // null: one workgroup per (query block, KV head) takes all its keys (k_attn_prefill). Otherwise the
+  // persistent form (k_attn_prefill_pers) over n_items items (query block, KV head, key split of
+  // PF_SPLIT_PAGES pages), with partials [n_qblocks][nkv][max_splits][G][8][64] float4 (O^T in MFMA
+  // accumulator order), (m, l, -, -) [n_qblocks][nkv][max_splits][G][16] float4 and arrival counters
+  // [n_qblocks][nkv][G] (zero before the first launch; each launch leaves them zero)
   float* ws;
-  int max_splits;
+  int max_splits, n_items;
 };
 
 constexpr int PF_QB = 16;              // queries per prefill-attention workgroup (16 per MFMA column block)
 constexpr int PF_STAGERS = 2;          // K/V staging waves per prefill-attention workgroup (beside the G head waves)
-constexpr int PF_SPLIT_PAGES = 32;     // KV pages per key split (2048 keys)
+constexpr int PF_SPLIT_PAGES = 16;     // KV pages per key split of the persistent form (1024 keys)
+constexpr int PF_MAX_ROUNDS = 64;      // items per workgroup of the persistent form (one lane each)
 
-__host__ __device__ inline int pf_splits(int pos0, int qb, int P) {   // key splits of query block qb
-  const int last = (pos0 + (qb + 1) * PF_QB - 1 < pos0 + P - 1) ? pos0 + (qb + 1) * PF_QB - 1 : pos0 + P - 1;
-  return (last / PAGE) / PF_SPLIT_PAGES + 1;
+// KV pages of query block qb (keys 0 .. its last query)
+__host__ __device__ inline int pf_pages(int pos0, int qb, int P) {
+  const int last = (pos0 + qb * PF_QB + PF_QB - 1 < pos0 + P - 1) ? pos0 + qb * PF_QB + PF_QB - 1 : pos0 + P - 1;
+  return last / PAGE + 1;
+}
+// first query block that has a key split s (its pages reach page PF_SPLIT_PAGES s); nqb: none has
+__host__ __device__ inline int pf_qmin(int pos0, int P, int s) {
+  const int x = PAGE * PF_SPLIT_PAGES * s;               // the split's first key
+  if (pos0 + P - 1 < x) return (P + PF_QB - 1) / PF_QB;
+  const int q = (x - pos0 - (PF_QB - 1) + PF_QB - 1) / PF_QB;   // ceil((x - pos0 - 15) / 16) where positive
+  return x - pos0 - (PF_QB - 1) <= 0 ? 0 : q;
+}
+__host__ __device__ inline int pf_max_splits(int pos0, int P) { return (pf_pages(pos0, (P + PF_QB - 1) / PF_QB - 1, P) - 1) / PF_SPLIT_PAGES + 1; }
+// items of the persistent form: split-major, query blocks longest first, then KV head
+__host__ __device__ inline int pf_items(int pos0, int P, int nkv) {
+  const int nqb = (P + PF_QB - 1) / PF_QB;
+  int n = 0;
+  for (int s = 0; pf_qmin(pos0, P, s) < nqb; ++s) n += (nqb - pf_qmin(pos0, P, s)) * nkv;
+  return n;
 }
 __host__ __device__ inline size_t pf_ws_floats(int nqb, int nkv, int G, int max_splits) {
-  return (size_t)nqb * nkv * max_splits * G * ((PF_QB / 16) * (8 * 64 * 4 + 16 * 2)) + (size_t)nqb * nkv;
+  return (size_t)nqb * nkv * max_splits * G * (8 * 64 * 4 + 16 * 4) + (size_t)nqb * nkv * G;
 }
 
 struct AttnArgs {
