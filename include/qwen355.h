@@ -305,9 +305,10 @@ int q355_attn_decode_f64_wl(const double* q64, const void* kcache, const void* v
  * (block_table = the sequence's page ids, >= (pos0 + P - 1) / 64 + 1 of them; K/V of every attended
  * position already written); out fp32 [P][nh*128] = softmax(q k^T * scale) v. 4 to 8 query heads per KV
  * head. ws (optional, ws_bytes >= q355_attn_prefill_ws_bytes(P, pos0 + P, nh, nkv), zeroed once by the
- * caller and reused across calls) lets long query rows split their keys over several workgroups; with
- * ws = NULL each 32-query block takes all its keys in one workgroup. Calls sharing a workspace must not
- * overlap.
+ * caller and reused across calls) runs the persistent form: one workgroup per CU over (16-query block, KV
+ * head, 1024-key split) items balanced across the CUs, splits merged in split order (the result does not
+ * depend on scheduling). With ws = NULL, and where every query row fits one split and one round, each
+ * 16-query block takes all its keys in one workgroup. Calls sharing a workspace must not overlap.
  * Replaces flash_prefill_v3_source (lab/qwen_batched.py:1795-2037). */
 int q355_attn_prefill(const void* q, const void* kcache, const void* vcache, const int32_t* block_table, int pos0,
                       int P, int nh, int nkv, float scale, float* out, void* ws, int64_t ws_bytes, void* stream);

@@ -23,10 +23,13 @@ def relerr(a, b):
 @pytest.mark.parametrize("split", [False, True])
 @pytest.mark.parametrize("P,pos0,nh,nkv", [(1, 0, 12, 2), (64, 0, 12, 2), (100, 0, 12, 2), (200, 37, 12, 2),
                                            (130, 64, 8, 2), (17, 250, 12, 2), (700, 0, 12, 2), (300, 555, 16, 2),
-                                           (77, 1500, 12, 2), (64, 4100, 12, 2), (130, 2000, 8, 2)])
+                                           (77, 1500, 12, 2), (64, 4100, 12, 2), (130, 2000, 8, 2),
+                                           (2048, 0, 12, 2), (1024, 3000, 12, 2)])
 def test_attn_prefill_matches_oracle(cuda, P, pos0, nh, nkv, split):
-    """Without and with the key-split workspace (splits of 2048 keys: pos0 = 4100 merges 3 splits; pos0 = 2000
-    makes a query block straddle a split boundary, so some of its queries see no key of the last split)."""
+    """Without and with the workspace. With it, contexts past 1024 keys run the persistent form over key splits
+    of 1024 keys: pos0 = 4100 merges 5 splits; pos0 = 2000 makes a query block straddle a split boundary, so
+    some of its queries see no key of the last split; P = 2048 and (1024, 3000) give 384 and 512 items, two
+    rounds per workgroup. Two calls in a row reuse the self-resetting counters and give the same bits."""
     import torch
     rng = np.random.default_rng(P * 1000 + pos0)
     n = pos0 + P
@@ -51,15 +54,20 @@ def test_attn_prefill_matches_oracle(cuda, P, pos0, nh, nkv, split):
     if split:
         nb = call("q355_attn_prefill_ws_bytes", P, n, nh, nkv)
         ws = torch.zeros(nb // 4, dtype=torch.float32, device=cuda)
+    ref = OM.attn_prefill(q, K, V, pos0, nh, nkv)
+    first = None
     for rep in range(2 if split else 1):                  # the second call reuses the self-resetting counters
         out.zero_()
         call("q355_attn_prefill", ptr(q_t), ptr(kc_t), ptr(vc_t), ptr(table_t), pos0, P, nh, nkv,
              1.0 / math.sqrt(128), ptr(out), ptr(ws) if split else None, nb)
         torch.cuda.synchronize()
-        ref = OM.attn_prefill(q, K, V, pos0, nh, nkv)
         assert relerr(out.cpu().numpy(), ref) < ATT_TOL
+        if first is None:
+            first = out.clone()
+        else:                                             # merged in split order whatever the arrival order
+            assert torch.equal(out.view(torch.int32), first.view(torch.int32))
     if split:
-        cnt = ws[-((P + 15) // 16) * nkv:].view(torch.int32)
+        cnt = ws[-((P + 15) // 16) * nkv * (nh // nkv):].view(torch.int32)   # [query blocks][KV heads][heads]
         assert int(cnt.abs().sum()) == 0
     # the Q8_1-output form quantizes exactly the values the fp32 form stores
     oq = torch.zeros(P, nh * 128, dtype=torch.int8, device=cuda)
