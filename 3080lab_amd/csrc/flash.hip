@@ -300,19 +300,20 @@ __global__ void __launch_bounds__(NT) k_attn_prefill_pers(const PrefillAttnArgs 
   __shared__ __align__(16) _Float16 vs[2][KP * PAGE][FV_ROW];
   __shared__ int4 items[PF_MAX_ROUNDS];                  // (qb, kvh, kb0 | nkb << 16, nsplit | split << 16)
   __shared__ int4 steps[PF_MAX_ROUNDS * PF_SPLIT_PAGES / KP];   // (item, kb, page kb, page kb + 1 in range)
-  __shared__ int nstep_s, nitem_s;
   const int G = a.nh / a.nkv;
   const int nqb = (a.P + PF_QB - 1) / PF_QB;
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int li = lane & 15, lg = lane >> 4;
   const float sl2 = a.scale * 1.4426950408889634f;
+  Q355_PF_PHASE_INIT();
 
-  // this workgroup's items (wave 0, lane r = round r) and their steps
-  if (wv == 0) {
+  // this workgroup's items, computed by every wave (lane r = round r): the staging waves start on steps 0 and 1
+  // and the head waves on their queries before the one barrier of the prologue; wave 0 writes the tables
+  int4 it = make_int4(0, 0, 0, 0);
+  int ns = 0;
+  {
     const int W = gridDim.x, w = blockIdx.x, r = lane;
     int c = r * W + ((r & 1) ? W - 1 - w : w);
-    int ns = 0;
-    int4 it = make_int4(0, 0, 0, 0);
     if (c < a.n_items) {
       int sp = 0, q0 = pf_qmin(a.pos0, a.P, 0);
       while (c >= (nqb - q0) * a.nkv) {                  // the split this item belongs to
@@ -325,41 +326,42 @@ __global__ void __launch_bounds__(NT) k_attn_prefill_pers(const PrefillAttnArgs 
       it = make_int4(qb, kvh, kb0 | (nkb << 16), ((L - 1) / PF_SPLIT_PAGES + 1) | (sp << 16));
       ns = (nkb - kb0 + KP - 1) / KP;
     }
-    int incl = ns;                                       // inclusive prefix of the step counts
+  }
+  int incl = ns;                                         // inclusive prefix of the step counts
 #pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-      const int t = __shfl_up(incl, o);
-      if (lane >= o) incl += t;
-    }
-    items[r] = it;
-    for (int k = 0; k < ns; ++k) steps[incl - ns + k] = make_int4(r, (it.z & 0xffff) + KP * k, 0, 0);
-    const unsigned long long live = __ballot(ns > 0);
-    if (lane == 63) {
-      nstep_s = incl;
-      nitem_s = __popcll(live);
+  for (int o = 1; o < 64; o <<= 1) {
+    const int t = __shfl_up(incl, o);
+    if (lane >= o) incl += t;
+  }
+  const int nst = __shfl(incl, 63), nit = __popcll(__ballot(ns > 0));
+  auto item = [&](int r) {                               // item r's fields, from lane r
+    return make_int4(__shfl(it.x, r), __shfl(it.y, r), __shfl(it.z, r), __shfl(it.w, r));
+  };
+  if (wv == 0) {
+    // the steps (item, kb, page ids of kb and kb + 1, the second past the range a repeat: masked on the
+    // diagonal step), all page-id loads of a lane in flight together
+    items[lane] = it;
+    const int kb0 = it.z & 0xffff, nkb = it.z >> 16;
+    for (int k = 0; k < ns; ++k) {
+      const int kb = kb0 + KP * k;
+      steps[incl - ns + k] = make_int4(lane, kb, a.block_table[kb], a.block_table[min(kb + 1, nkb - 1)]);
     }
   }
-  __syncthreads();
-  const int nst = nstep_s, nit = nitem_s;
-  for (int e = threadIdx.x; e < nst; e += blockDim.x) {  // the page ids of every step (one latency for all)
-    int4 st = steps[e];
-    const int nkb = items[st.x].z >> 16;
-    st.z = a.block_table[st.y];
-    st.w = a.block_table[min(st.y + 1, nkb - 1)];       // past the range: a repeat, masked (diagonal step)
-    steps[e] = st;
-  }
-  __syncthreads();
-
   if (wv >= G) {                                         // staging waves: same barriers as the head waves
     const int st = threadIdx.x - 64 * G;
     PfStage r;
-    if (nst > 0) {
-      pf_stage_load(r, a, items[steps[0].x].y, steps[0].z, steps[0].w, st);
-      pf_stage_store(r, ks[0], vs[0], st);
-      if (nst > 1) pf_stage_load(r, a, items[steps[1].x].y, steps[1].z, steps[1].w, st);
+    // steps 0 and 1 from the items directly (step 1: item 0's second step, or item 1's first)
+    const int4 i0 = item(0);
+    const int kb00 = i0.z & 0xffff, nkb0 = i0.z >> 16;
+    pf_stage_load(r, a, i0.y, a.block_table[kb00], a.block_table[min(kb00 + 1, nkb0 - 1)], st);
+    pf_stage_store(r, ks[0], vs[0], st);
+    if (nst > 1) {
+      const bool same = kb00 + KP < nkb0;
+      const int4 i1 = same ? i0 : item(1);
+      const int kb = same ? kb00 + KP : (i1.z & 0xffff), nkb = i1.z >> 16;
+      pf_stage_load(r, a, i1.y, a.block_table[kb], a.block_table[min(kb + 1, nkb - 1)], st);
     }
     __syncthreads();
-    Q355_PF_PHASE_INIT();
     for (int g = 0; g < nst; ++g) {
       Q355_PF_PHASE(0);
       if (g + 1 < nst) {
@@ -375,12 +377,15 @@ __global__ void __launch_bounds__(NT) k_attn_prefill_pers(const PrefillAttnArgs 
   }
 
   h8 qf[4], qn[4];                                       // this item's queries and the next item's
-  if (nit > 0) pf_load_q(qf, a, items[0].x, items[0].y * G + wv, li, lg);
-  if (nit > 1) pf_load_q(qn, a, items[1].x, items[1].y * G + wv, li, lg);
+  {
+    const int4 i0 = item(0), i1 = item(1);
+    pf_load_q(qf, a, i0.x, i0.y * G + wv, li, lg);
+    if (nit > 1) pf_load_q(qn, a, i1.x, i1.y * G + wv, li, lg);
+  }
   float m = -INFINITY, l = 0.f;
   f4 acc[8];
-  __syncthreads();
-  Q355_PF_PHASE_INIT();
+  __syncthreads();                                       // the tables and step 0's stage are ready
+  Q355_PF_PHASE(3);
   for (int g = 0; g < nst; ++g) {
     Q355_PF_PHASE(0);
     const int4 st = steps[g];
@@ -441,26 +446,35 @@ __global__ void __launch_bounds__(NT) k_attn_prefill_pers(const PrefillAttnArgs 
     const int per = a.max_splits * G;
     const Coh16 PO((const float4*)a.ws + row * per * 512, (unsigned)per * 512 * 16);
     const Coh16 PM((const float4*)a.ws + (size_t)nqb * a.nkv * per * 512 + row * per * 16, (unsigned)per * 16 * 16);
-    float mt = -INFINITY;
-    for (int s2 = 0; s2 < nsplit; ++s2)
-      mt = fmaxf(mt, __builtin_bit_cast(float4, PM.ld((((unsigned)(s2 * G + wv)) * 16 + li) * 16)).x);
-    float lt = 0.f;
+    // running-max merge in split order, two splits' loads in flight at a time
+    float M = -INFINITY, lt = 0.f;
     f4 o[8];
 #pragma unroll
     for (int t = 0; t < 8; ++t) o[t] = f4{0.f, 0.f, 0.f, 0.f};
-    for (int s2 = 0; s2 < nsplit; ++s2) {
-      const unsigned sl = (unsigned)(s2 * G + wv);
-      int4 v[8];
+    for (int b0 = 0; b0 < nsplit; b0 += 2) {
+      int4 v[2][8];
+      float4 ml[2];
 #pragma unroll
-      for (int dt = 0; dt < 8; ++dt) v[dt] = PO.ld((sl * 512 + dt * 64 + lane) * 16);
-      const float4 ml = __builtin_bit_cast(float4, PM.ld((sl * 16 + li) * 16));
-      const float f = __builtin_amdgcn_exp2f(ml.x - mt);
-      lt += f * ml.y;
+      for (int u = 0; u < 2; ++u) {
+        const unsigned sl = (unsigned)(min(b0 + u, nsplit - 1) * G + wv);
 #pragma unroll
-      for (int dt = 0; dt < 8; ++dt) o[dt] += f * __builtin_bit_cast(f4, v[dt]);
+        for (int dt = 0; dt < 8; ++dt) v[u][dt] = PO.ld((sl * 512 + dt * 64 + lane) * 16);
+        ml[u] = __builtin_bit_cast(float4, PM.ld((sl * 16 + li) * 16));
+      }
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        if (b0 + u >= nsplit) break;                     // uniform
+        const float mn = fmaxf(M, ml[u].x);              // split 0 holds key 0: finite
+        const float fo = __builtin_amdgcn_exp2f(M - mn), f = __builtin_amdgcn_exp2f(ml[u].x - mn);
+        lt = lt * fo + f * ml[u].y;
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt) o[dt] = o[dt] * fo + f * __builtin_bit_cast(f4, v[u][dt]);
+        M = mn;
+      }
     }
     pf_out(a, qb * PF_QB + li, kvh * G + wv, lg, o, lt);
   }
+  Q355_PF_PHASE(4);
   Q355_PF_PHASE_END();
 }
 
