@@ -24,12 +24,13 @@ def relerr(a, b):
 @pytest.mark.parametrize("P,pos0,nh,nkv", [(1, 0, 12, 2), (64, 0, 12, 2), (100, 0, 12, 2), (200, 37, 12, 2),
                                            (130, 64, 8, 2), (17, 250, 12, 2), (700, 0, 12, 2), (300, 555, 16, 2),
                                            (77, 1500, 12, 2), (64, 4100, 12, 2), (130, 2000, 8, 2),
-                                           (2048, 0, 12, 2), (1024, 3000, 12, 2)])
+                                           (2048, 0, 12, 2), (1024, 3000, 12, 2), (100, 1500, 16, 2)])
 def test_attn_prefill_matches_oracle(cuda, P, pos0, nh, nkv, split):
     """Without and with the workspace. With it, contexts past 1024 keys run the persistent form over key splits
     of 1024 keys: pos0 = 4100 merges 5 splits; pos0 = 2000 makes a query block straddle a split boundary, so
     some of its queries see no key of the last split; P = 2048 and (1024, 3000) give 384 and 512 items, two
-    rounds per workgroup. Two calls in a row reuse the self-resetting counters and give the same bits."""
+    rounds per workgroup; (100, 1500, 16, 2) runs the 640-thread form (8 query heads per KV head). Two calls in
+    a row reuse the self-resetting counters and give the same bits."""
     import torch
     rng = np.random.default_rng(P * 1000 + pos0)
     n = pos0 + P
