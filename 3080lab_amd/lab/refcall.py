@@ -208,7 +208,10 @@ def launch_gemv(spec, args, grid=None):
     if epi == "resid" and not isinstance(X, NormedAct):         # down: Q8_1 of the fp32 SwiGLU output + residual
         if not isinstance(X, int) or not isinstance(Y, int):
             raise HipError("gemv(resid) down: X (fp32 SwiGLU output) and Y (int64 residual) must be plain buffers")
-        return call("q355_ffn_down", m.qs.data_ptr(), m.d.data_ptr(), N, K, X, Y, spec.params.get("T", 1))
+        # plain pointers carry no row count: the reference's fused step (scripts/qwen_fused.py) is batch 1
+        if spec.params.get("T", 1) != 1:
+            raise HipError("gemv(resid) down over plain buffers: batch 1 only (the buffers carry no row count)")
+        return call("q355_ffn_down", m.qs.data_ptr(), m.d.data_ptr(), N, K, X, Y, 1)
     # plain store / bias / accumulate over a materialised Q8_1 activation (fp32 Y)
     x = _need(X, NormedAct, "gemv X")
     if not isinstance(Y, (int, Logits)):

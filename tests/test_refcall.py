@@ -187,6 +187,23 @@ def test_reference_order_errors():
         KS.gemv_source(2, "bogus")
 
 
+def test_reference_order_down_is_batch_one(monkeypatch):
+    """The down product over plain pointers (no row count) runs one token; a spec asking for more is rejected."""
+    import dataclasses
+    from lab.hip import HipError
+    calls = []
+    monkeypatch.setattr(refcall, "call", lambda name, *a: calls.append((name, a)) or 0)
+    dm = _model("cpu")
+    W = dm.layers[0]["down"]
+    refcall.register(W.qs, W)
+    spec = KS.gemv_source(2, "resid")
+    refcall.launch_gemv(spec, [W.qs, W.d, 1000, 2000, 0, CFG.H, CFG.FFN])
+    assert calls and calls[-1][0] == "q355_ffn_down" and calls[-1][1][-1] == 1
+    wide = dataclasses.replace(spec, params={**spec.params, "T": 4})
+    with pytest.raises(HipError, match="batch 1"):
+        refcall.launch_gemv(wide, [W.qs, W.d, 1000, 2000, 0, CFG.H, CFG.FFN])
+
+
 @pytest.mark.gpu
 def test_reference_order_step_equals_decoder(cuda):
     """GPU: prompt + greedy steps through RefStep and through Decoder.step give bit-equal h and equal tokens."""
