@@ -5,15 +5,14 @@
 // its sequence; scores q.k * scale, softmax with running max (exp2 of scores pre-scaled by log2 e),
 // fp16 P, fp32 accumulation; output o = sum p v / sum p in fp32.
 //
-// Per 64-key block (one KV page): K (row-padded) and V transposed (Vt[dim][key]) are staged in LDS once for
-// all query heads of the KV head; the next page is loaded into registers while the current one is used.
-// The wave computes S^T = K Q^T (A = K rows from LDS, B = the wave's Q rows held in registers), so lane l
-// holds scores of ONE query (l % 16) for keys 16t + 4(l/16) + v: the softmax statistics of a query live
-// in the 4 lanes l % 16 + 16g and need only two cross-lane steps. The same registers, converted to fp16,
-// are directly the B operand of O^T = Vt P^T when a 32-key chunk c is ordered as k-slot 8g + j ->
-// key 32c + 4g + j (j < 4), 32c + 16 + 4g + j - 4 (j >= 4); Vt is read in that order (two 8-byte
-// LDS reads). O^T accumulators are again per query l % 16 (dims 16dt + 4g + v), so the running-max
-// rescale is per lane.
+// Per 64-key block (one KV page): K and V (key-major, rows padded) are staged in LDS once for all query heads
+// of the KV head by two staging waves, a step ahead (double buffer). The head wave computes S^T = K Q^T
+// (A = K rows from LDS, B = the wave's Q rows held in registers), so lane l holds scores of ONE query (l % 16)
+// for keys 16t + 4(l/16) + v: the softmax statistics of a query live in the 4 lanes l % 16 + 16g and need only
+// two cross-lane steps. The same registers, converted to fp16, are directly the B operand of O^T = Vt P^T when
+// a 32-key chunk c is ordered as k-slot 8g + j -> key 32c + 4g + j (j < 4), 32c + 16 + 4g + j - 4 (j >= 4);
+// the Vt operand is read in that order from the key-major V by two transposed LDS reads. O^T accumulators are
+// again per query l % 16 (dims 16dt + 4g + v), so the running-max rescale is per lane.
 // MFMA operand layouts (16x16x32): lane l holds A[row l%16][k 8(l/16)..+8], B[k 8(l/16)..+8][col l%16],
 // C[row 4(l/16)+v][col l%16].
 #include "common.h"
@@ -31,16 +30,16 @@ constexpr int FV_ROW = HD + 16;
 
 __device__ __forceinline__ h8 as_h8(uint4 v) { return *reinterpret_cast<h8*>(&v); }
 
-// Scheduling of an unrolled run of N LDS operands (R reads each) feeding N MFMA groups (CBN MFMAs each):
-// PF_DEPTH operands first, then one MFMA group per further operand, then the last groups (masks: 0x100 LDS
-// read, 0x008 MFMA).
-// phase accounting hooks of the key loop: empty here; an instrumented build defines them
+// phase accounting hooks: empty here; an instrumented build defines them
 #ifndef Q355_PF_PHASE
 #define Q355_PF_PHASE_INIT()
 #define Q355_PF_PHASE(k)
 #define Q355_PF_PHASE_END()
 #endif
 
+// Scheduling of an unrolled run of N LDS operands (R reads each) feeding N MFMA groups (CBN MFMAs each):
+// PF_DEPTH operands first, then one MFMA group per further operand, then the last groups (masks: 0x100 LDS
+// read, 0x008 MFMA).
 #ifndef PF_DEPTH
 #define PF_DEPTH 8
 #endif
