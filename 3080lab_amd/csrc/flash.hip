@@ -224,7 +224,7 @@ __device__ __forceinline__ void pf_load_q(h8 (&qf)[4], const PrefillAttnArgs& a,
 
 // Workgroup = one KV head x 16 queries x all their keys (the form without a workspace). Waves 0 .. G-1 are
 // the head waves (wave w: query head kvh * G + w), so each staged K/V page serves all G heads of the group;
-// waves G and G + 1 stage K and Vt into a double buffer: while the head waves compute step s from buffer
+// waves G and G + 1 stage K and V into a double buffer: while the head waves compute step s from buffer
 // s & 1, they write step s + 1 into the other buffer and load step s + 2 into registers, so one barrier per
 // step separates the two roles and the head waves hold no staging registers. grid (ceil(P / 16), 1, nkv),
 // the longest query blocks first; 64 (G + 2) threads.
